@@ -1,0 +1,213 @@
+"""Benchmark of the MI355X fused residual-add + RMSNorm + group-quant operator.
+
+Default workload: the headline configuration (BASELINE.json metric),
+16384 x 7168 bf16 -> fp8 e4m3fn, group 128, fp32 column-major scales, 1 %
+outlier channels.  A "step" is one call of the operator over the whole
+[16384, 7168] batch.  Inputs are resident in HBM before the timed region; K
+steps are timed between device synchronisations, rotating over enough
+input/output sets that no step reads data left in L2/MALL by the previous
+one.
+
+Prints one JSON line:
+  value       whole-job achieved bandwidth, algorithmic bytes / wall time per step
+  roofline    the kernel's algorithmic bytes / its average duration (HIP events
+              recorded on the launch stream around every timed launch), vs 8 TB/s;
+              traffic = measured HBM bytes per launch from the committed rocprofv3
+              counter summary for this workload (null if none)
+  cpu_baseline  the eager-PyTorch CPU restatement timed on a bounded row sample
+              of the same workload on the host cores (and checked against the
+              GPU's rows)
+
+Usage: python bench.py [--steps K] [--warmup W] [--config NAME] [--gpus 1]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO_DIR = Path(__file__).resolve().parent
+PEAK_HBM_GBS = 8000.0
+METRIC = "achieved HBM GB/s (% of 8 TB/s peak) + µs/call, 16384×7168 bf16→fp8 g128"
+ROTATE_BYTES = 1 << 30     # rotate buffer sets until > 1 GiB (4x the 256 MB MALL)
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--config", default=None, help="workload name (default: the headline one)")
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
+                   help="target CPU time of the cpu_baseline leg (0 disables it)")
+    p.add_argument("--cpu-rows", type=int, default=512, help="rows in the cpu_baseline sample")
+    return p.parse_args()
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(rows shard with no exchange; see DESIGN.md for the multi-GPU design)",
+              file=sys.stderr)
+        return 2
+    sys.path.insert(0, str(REPO_DIR))
+    import torch
+    import __graft_entry__ as ge
+
+    pkg = ge.load_package()
+    from fagq_mi355x.workloads import CONFIGS, HEADLINE, make_inputs
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 2
+    name = args.config or HEADLINE
+    w = CONFIGS[name]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = pkg.load_library()
+
+    x, res, gamma = make_inputs(w)
+    set_bytes = w.algorithmic_bytes()
+    nsets = max(2, math.ceil(ROTATE_BYTES / set_bytes) + 1)
+    nsets = min(nsets, 64)
+    xd, rd, gd = x.to(dev), res.to(dev), gamma.to(dev)
+    sets = []
+    for i in range(nsets):
+        xs, rs = (xd, rd) if i == 0 else (xd.clone(), rd.clone())
+        ro = torch.empty_like(rs)
+        q = torch.empty((w.M, w.D), dtype=w.out_dtype, device=dev)
+        sc = pkg.empty_scales(w.M, w.groups, ue8m0=w.scale_ue8m0, col_major=w.scale_col_major,
+                              device=dev)
+        sets.append((xs, rs, ro, q, sc))
+
+    def step(i: int):
+        xs, rs, ro, q, sc = sets[i % nsets]
+        pkg.fused_add_rmsnorm_group_quant(
+            xs, rs, gd, ro, None, q, sc, w.eps, w.group_size,
+            rounding=w.rounding if w.out_dtype == torch.int8 else None)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize(dev)
+
+    stream = torch.cuda.current_stream(dev)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record(stream)
+        step(i)
+        ends[i].record(stream)
+    torch.cuda.synchronize(dev)
+    t1 = time.perf_counter()
+    wall_ms = (t1 - t0) * 1e3 / args.steps
+    durs = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+    kern_ms = sum(durs) / len(durs)
+    med_ms = durs[len(durs) // 2]
+
+    value = set_bytes / (wall_ms * 1e-3) / 1e9
+    achieved = set_bytes / (kern_ms * 1e-3) / 1e9
+
+    traffic = None
+    tfile = REPO_DIR / "profiles" / f"traffic_{name}.json"
+    if tfile.exists():
+        try:
+            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+        except (ValueError, OSError):
+            traffic = None
+
+    route = pkg.route_for(w.M, w.D, w.group_size)
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": name, "M": w.M, "D": w.D, "group_size": w.group_size,
+                   "q": str(w.out_dtype).replace("torch.", ""),
+                   "scale": ("ue8m0" if w.scale_ue8m0 else "f32") +
+                            (" col-major" if w.scale_col_major else " row-major"),
+                   "inputs": w.dist, "algorithmic_bytes": set_bytes, "buffer_sets": nsets,
+                   "route": route},
+        "us_per_call": round(kern_ms * 1e3, 2),
+        "us_per_call_median": round(med_ms * 1e3, 2),
+        "pct_of_peak": round(100.0 * achieved / PEAK_HBM_GBS, 2),
+        "rows_per_s": round(w.M / (kern_ms * 1e-3), 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": traffic},
+        "cpu_baseline": None,
+    }
+
+    if args.cpu_seconds > 0:
+        out["cpu_baseline"] = cpu_baseline(w, x, res, gamma, sets[0], args, torch)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def cpu_baseline(w, x, res, gamma, gpu_set, args, torch) -> dict:
+    """Times the eager-PyTorch CPU restatement (oracle/torch_eager.py) on the
+    first rows of the same workload, and checks those rows of the GPU's
+    output against it."""
+    import numpy as np
+    from oracle.compare import compare
+    from oracle.torch_eager import fagq_torch
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    rows = max(1, min(args.cpu_rows, w.M))
+    xs, rs = x[:rows].contiguous(), res[:rows].contiguous()
+
+    def run():
+        return fagq_torch(xs, rs, gamma, w.eps, w.group_size, w.out_dtype, w.scale_ue8m0,
+                          w.scale_col_major, w.rounding)
+
+    ref = run()    # warm-up
+    run()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < args.cpu_seconds and len(times) < 1000):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    t = times[len(times) // 2]
+    nbytes = w.algorithmic_bytes() * rows // w.M
+
+    # Parity of the GPU rows against the CPU path (step 0 wrote set 0).
+    _, _, ro, q, sc = gpu_set
+    torch.cuda.synchronize()
+    scale_rows = sc[:rows]
+    scale_phys = scale_rows.t() if w.scale_col_major else scale_rows
+    gpu = {"residual_out": ro[:rows].cpu().view(torch.uint16).numpy(),
+           "q": q[:rows].cpu().view(torch.uint8).numpy(),
+           "scale": np.ascontiguousarray(scale_phys.cpu().numpy())}
+    refd = {"residual_out": ref[0].view(torch.uint16).numpy(),
+            "q": ref[1].view(torch.uint8).numpy(), "scale": ref[2].numpy()}
+    try:
+        st = compare(gpu, refd, fp8=w.out_dtype == torch.float8_e4m3fn, ue8m0=w.scale_ue8m0)
+        parity = {"ok": True, "exact": st["exact"], "q_mismatch": st["q_mismatch"]}
+    except AssertionError as e:
+        parity = {"ok": False, "error": str(e)[:200]}
+    return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port", "us_per_call": round(t * 1e6, 1),
+            "sample": f"first {rows} of {w.M} rows of {w.name}, eager PyTorch CPU "
+                      f"restatement (oracle/torch_eager.py), median of {len(times)} runs",
+            "parity_vs_gpu_rows": parity}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,21 @@
+"""MI355X (gfx950) fused residual-add + RMSNorm + per-token-group quantization.
+
+Drop-in for the Task 01 operator of sinpeyw/flagos-kernelgen-72h-shanghai-2026
+(src/task01_fused_add_rmsnorm_group_quant.py:1731), backed by hand-written HIP
+kernels in libfagq.so (C ABI: include/fagq.h).  The directory name is not a
+Python identifier; load it with ``__graft_entry__.load_package()``, which
+registers it as ``fagq_mi355x``.
+"""
+from . import _lib
+from ._lib import FagqError, load as load_library
+from .ops import (empty_scales, fused_add_rmsnorm_group_quant, fused_add_rmsnorm_group_quant_fn,
+                  route_for)
+
+__all__ = [
+    "FagqError",
+    "empty_scales",
+    "fused_add_rmsnorm_group_quant",
+    "fused_add_rmsnorm_group_quant_fn",
+    "load_library",
+    "route_for",
+]

@@ -1,0 +1,105 @@
+"""ctypes binding of libfagq.so (the C ABI declared in include/fagq.h and
+include/fagq_diag.h).
+
+The library is loaded after ``import torch`` so that its libamdhip64.so.7
+dependency resolves to the HIP runtime torch already loaded (same soname);
+kernels then run on torch's streams.  There is no fallback: if the library
+is missing or does not load, every operator call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (loads the HIP runtime the library binds to)
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "libfagq.so"
+
+# Enums of include/fagq.h.
+Q_INT8, Q_FP8_E4M3FN = 0, 1
+SCALE_F32, SCALE_UE8M0 = 0, 1
+LAYOUT_ROW_MAJOR, LAYOUT_COL_MAJOR = 0, 1
+ROUND_RNE, ROUND_TRUNC = 0, 1
+MAX_D = 32768
+
+STATUS_NAMES = {
+    0: "FAGQ_OK", 1: "FAGQ_E_NULL", 2: "FAGQ_E_SHAPE", 3: "FAGQ_E_GROUP", 4: "FAGQ_E_ALIGN",
+    5: "FAGQ_E_FORMAT", 6: "FAGQ_E_EPS", 7: "FAGQ_E_TOO_LARGE", 8: "FAGQ_E_DEVICE",
+    9: "FAGQ_E_ALIAS",
+}
+
+# Every exported function and its ctypes signature.
+_P, _I64, _I, _F = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
+
+
+class Route(ctypes.Structure):
+    _fields_ = [("waves_per_row", ctypes.c_int32), ("steps_per_wave", ctypes.c_int32),
+                ("rows_per_block", ctypes.c_int32), ("block_threads", ctypes.c_int32),
+                ("grid_blocks", ctypes.c_int64)]
+
+
+SIGNATURES = {
+    "fagq_launch": ([_P] * 7 + [_I64, _I64, _I64, _F, _I, _I, _I, _I, _P], _I),
+    "fagq_launch_mapped": ([_P] * 7 + [_I64, _I64, _I64, _F, _I, _I, _I, _I, _I, _I, _I, _P], _I),
+    "fagq_query_route": ([_I64, _I64, _I64, ctypes.POINTER(Route)], _I),
+    "fagq_status_string": ([_I], ctypes.c_char_p),
+    "fagq_version": ([], _I),
+    "fagq_diag_encode": ([_P, _P, _I64, _I, _I, _P], _I),
+    "fagq_diag_copy": ([_P, _P, _I64, _P], _I),
+}
+
+
+class FagqError(RuntimeError):
+    """A non-zero status from the library."""
+
+    def __init__(self, status: int, what: str = "fagq_launch"):
+        self.status = status
+        name = STATUS_NAMES.get(status, "HIP error" if status < 0 else "unknown")
+        super().__init__(f"{what} failed: status {status} ({name}): {describe(status)}")
+
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load(path: str | Path | None = None) -> ctypes.CDLL:
+    """Loads libfagq.so once; raises if it is absent or incomplete."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        p = Path(path) if path is not None else LIB_PATH
+        if not p.exists():
+            raise ImportError(
+                f"{p} is missing: build the HIP library first "
+                "(python __graft_entry__.py build, or build.build())")
+        lib = ctypes.CDLL(str(p))
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(lib, name)   # AttributeError if an export is missing
+            fn.argtypes = args
+            fn.restype = res
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def describe(status: int) -> str:
+    try:
+        return load().fagq_status_string(status).decode()
+    except Exception:  # pragma: no cover - only when the library cannot load
+        return STATUS_NAMES.get(status, "unknown")
+
+
+def check(status: int, what: str = "fagq_launch") -> None:
+    if status != 0:
+        raise FagqError(status, what)
+
+
+def query_route(M: int, D: int, group_size: int) -> dict:
+    r = Route()
+    check(load().fagq_query_route(M, D, group_size, ctypes.byref(r)), "fagq_query_route")
+    return {f: getattr(r, f) for f, _ in Route._fields_}

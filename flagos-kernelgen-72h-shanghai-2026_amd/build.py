@@ -1,0 +1,94 @@
+"""Builds libfagq.so, the gfx950 HIP library behind the operator.
+
+Every HIP translation unit is compiled by hipcc for gfx950 only, in
+parallel, into ``_build/``; the objects are linked into ``libfagq.so`` next
+to this file, which is what the Python layer loads.  Runs on a machine
+without a GPU (hipcc cross-compiles).
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+REPO_DIR = PKG_DIR.parent
+CSRC = PKG_DIR / "csrc"
+INCLUDE = REPO_DIR / "include"
+OBJ_DIR = PKG_DIR / "_build"
+LIB_PATH = PKG_DIR / "libfagq.so"
+
+ARCH = "gfx950"
+# (code format, scale format) pairs compiled from fagq_inst.hip:
+# code 0 = fp8 e4m3fn, 1 = int8 round-half-even, 2 = int8 truncate;
+# scale 0 = fp32, 1 = ue8m0.
+INST_COMBOS = [(q, s) for q in (0, 1, 2) for s in (0, 1)]
+
+
+def hipcc() -> str:
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    cand = Path(rocm) / "bin" / "hipcc"
+    if cand.exists():
+        return str(cand)
+    found = shutil.which("hipcc")
+    if not found:
+        raise RuntimeError("hipcc not found (set ROCM_PATH)")
+    return found
+
+
+def device_flags() -> list[str]:
+    # Packed-fp32 instructions are disabled on purpose: the kernels are written
+    # with scalar fp32 arithmetic and must not be auto-vectorised into them.
+    return [
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-ffp-contract=off",
+        "-fvisibility=hidden",
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        f"-I{INCLUDE}",
+        f"-I{CSRC}",
+    ]
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{res.stdout}")
+    # hipcc's host pass warns that it does not know the packed-fp32 feature.
+    noise = "-packed-fp32-ops' is not a recognized feature"
+    lines = [l for l in res.stdout.splitlines() if noise not in l and l.strip()]
+    if verbose and lines:
+        print("\n".join(lines), flush=True)
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compiles every HIP unit for gfx950 and links libfagq.so; returns its path."""
+    OBJ_DIR.mkdir(exist_ok=True)
+    cc = hipcc()
+    flags = device_flags()
+    units: list[tuple[Path, Path, list[str]]] = []
+    for q, s in INST_COMBOS:
+        units.append((CSRC / "fagq_inst.hip", OBJ_DIR / f"fagq_inst_q{q}_s{s}.o",
+                      [f"-DFAGQ_QF={q}", f"-DFAGQ_SF={s}"]))
+    units.append((CSRC / "fagq_api.hip", OBJ_DIR / "fagq_api.o", []))
+    jobs = jobs or min(len(units), max(1, min(16, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        futs = [ex.submit(_run, [cc, *flags, *defs, "-c", str(src), "-o", str(obj)], verbose)
+                for src, obj, defs in units]
+        for f in futs:
+            f.result()
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+          *[str(o) for _, o, _ in units]], verbose)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

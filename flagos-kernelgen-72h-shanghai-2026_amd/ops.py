@@ -1,0 +1,184 @@
+"""The operator's Python interface, mirroring the reference's.
+
+``fused_add_rmsnorm_group_quant`` keeps the reference's signature and
+semantics (src/task01_fused_add_rmsnorm_group_quant.py:1731-1741, returns at
+:1764/:1790/:1817/:1840/:1851): the caller allocates every output, the call
+is asynchronous on torch's current stream, and the same four objects are
+returned.  The output formats are read from the destination tensors:
+
+* ``x_q`` int8 -> int8 codes, rounded toward zero like the reference's
+  float->int cast (:112-116, :1100-1104) unless ``rounding="rne"``;
+  ``x_q`` float8_e4m3fn -> OCP fp8 codes, round to nearest even.
+* ``x_scale`` float32 -> fp32 scales; uint8 -> UE8M0 biased exponents.
+* ``x_scale`` contiguous [M, D/G] -> row-major (the reference's layout,
+  :121); a [M, D/G] view with strides (1, M), e.g.
+  ``torch.empty(D // G, M).t()``, -> column-major.
+* ``norm_out`` may be None: the 3-output form, which skips 2 bytes/element.
+
+The reference validates nothing; here shapes, dtypes, devices and layouts
+are checked in Python (TypeError / ValueError) and everything else by the
+library (FagqError with its status code).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_BF16 = torch.bfloat16
+_FP8 = torch.float8_e4m3fn
+
+
+def _q_format(x_q: torch.Tensor) -> int:
+    if x_q.dtype == torch.int8:
+        return _lib.Q_INT8
+    if x_q.dtype == _FP8:
+        return _lib.Q_FP8_E4M3FN
+    raise TypeError(f"x_q must be int8 or float8_e4m3fn, got {x_q.dtype}")
+
+
+def _scale_format(x_scale: torch.Tensor) -> int:
+    if x_scale.dtype == torch.float32:
+        return _lib.SCALE_F32
+    if x_scale.dtype == torch.uint8:
+        return _lib.SCALE_UE8M0
+    raise TypeError(f"x_scale must be float32 or uint8 (ue8m0), got {x_scale.dtype}")
+
+
+def _scale_layout(x_scale: torch.Tensor, M: int, groups: int) -> int:
+    if tuple(x_scale.shape) != (M, groups):
+        raise ValueError(f"x_scale must have shape ({M}, {groups}), got {tuple(x_scale.shape)}")
+    if x_scale.is_contiguous():
+        return _lib.LAYOUT_ROW_MAJOR
+    if x_scale.stride() == (1, M):
+        return _lib.LAYOUT_COL_MAJOR
+    raise ValueError(f"x_scale must be row-major [M, D/G] or column-major (strides (1, M)); "
+                     f"got strides {x_scale.stride()}")
+
+
+def _rounding(rounding: str | None, q_format: int) -> int:
+    if q_format == _lib.Q_FP8_E4M3FN:
+        if rounding not in (None, "rne"):
+            raise ValueError("fp8 codes are always rounded to nearest even")
+        return _lib.ROUND_RNE
+    if rounding in (None, "trunc"):
+        return _lib.ROUND_TRUNC
+    if rounding == "rne":
+        return _lib.ROUND_RNE
+    raise ValueError(f"rounding must be 'rne' or 'trunc', got {rounding!r}")
+
+
+def _check_rows(name: str, t: torch.Tensor, shape: tuple, device: torch.device) -> None:
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+    if t.dtype != _BF16:
+        raise TypeError(f"{name} must be bfloat16, got {t.dtype}")
+    if tuple(t.shape) != shape:
+        raise ValueError(f"{name} must have shape {shape}, got {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def fused_add_rmsnorm_group_quant(
+    x: torch.Tensor,
+    residual: torch.Tensor,
+    gamma: torch.Tensor,
+    residual_out: torch.Tensor,
+    norm_out: torch.Tensor | None,
+    x_q: torch.Tensor,
+    x_scale: torch.Tensor,
+    eps: float,
+    group_size: int,
+    *,
+    rounding: str | None = None,
+):
+    """residual_out = x + residual; x_q, x_scale = group-quant(RMSNorm(x + residual) * gamma).
+
+    Drop-in for the reference's operator of the same name and signature; see
+    the module docstring for how the formats are chosen.  Returns
+    ``(residual_out, norm_out, x_q, x_scale)``.
+    """
+    if x.dim() != 2:
+        raise ValueError(f"x must be 2-D [M, D], got shape {tuple(x.shape)}")
+    M, D = (int(s) for s in x.shape)
+    if not x.is_cuda:
+        raise ValueError("x must be a GPU (HIP) tensor; this operator has no CPU path")
+    device = x.device
+    _check_rows("x", x, (M, D), device)
+    _check_rows("residual", residual, (M, D), device)
+    _check_rows("gamma", gamma, (D,), device)
+    _check_rows("residual_out", residual_out, (M, D), device)
+    if norm_out is not None:
+        _check_rows("norm_out", norm_out, (M, D), device)
+    group_size = int(group_size)
+    if group_size <= 0 or D % group_size != 0:
+        raise ValueError(f"group_size {group_size} must divide D = {D}")
+    qf = _q_format(x_q)
+    if x_q.device != device or tuple(x_q.shape) != (M, D) or not x_q.is_contiguous():
+        raise ValueError(f"x_q must be a contiguous ({M}, {D}) tensor on {device}")
+    if x_scale.device != device:
+        raise ValueError(f"x_scale is on {x_scale.device}, expected {device}")
+    sf = _scale_format(x_scale)
+    layout = _scale_layout(x_scale, M, D // group_size)
+    rnd = _rounding(rounding, qf)
+    if M == 0:
+        return residual_out, norm_out, x_q, x_scale
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    with torch.cuda.device(device):
+        st = lib.fagq_launch(_ptr(x), _ptr(residual), _ptr(gamma), _ptr(residual_out),
+                             _ptr(norm_out), _ptr(x_q), _ptr(x_scale), M, D, group_size,
+                             float(eps), qf, sf, layout, rnd, ctypes.c_void_p(stream))
+    _lib.check(st)
+    return residual_out, norm_out, x_q, x_scale
+
+
+def empty_scales(M: int, groups: int, *, ue8m0: bool = False, col_major: bool = False,
+                 device=None) -> torch.Tensor:
+    """A [M, groups] scale tensor in the requested format and layout."""
+    dt = torch.uint8 if ue8m0 else torch.float32
+    if col_major:
+        return torch.empty(groups, M, dtype=dt, device=device).t()
+    return torch.empty(M, groups, dtype=dt, device=device)
+
+
+def fused_add_rmsnorm_group_quant_fn(
+    x: torch.Tensor,
+    residual: torch.Tensor,
+    weight: torch.Tensor,
+    eps: float = 1e-6,
+    group_size: int = 128,
+    out_dtype: torch.dtype = _FP8,
+    *,
+    scale_col_major: bool = False,
+    scale_ue8m0: bool = False,
+    rounding: str = "rne",
+    inplace_residual: bool = False,
+):
+    """Functional 3-output form: returns ``(residual_out, q, scale)``.
+
+    ``residual_out`` is ``residual`` itself when ``inplace_residual`` (the
+    "updated residual" of a transformer block), else a new tensor.  ``scale``
+    is a [M, D/G] tensor, column-major when ``scale_col_major``, holding
+    UE8M0 bytes when ``scale_ue8m0``.  int8 codes default to round-half-even
+    here (the reference-signature function defaults to truncation).
+    """
+    M, D = (int(s) for s in x.shape)
+    residual_out = residual if inplace_residual else torch.empty_like(residual)
+    q = torch.empty((M, D), dtype=out_dtype, device=x.device)
+    scale = empty_scales(M, D // group_size, ue8m0=scale_ue8m0, col_major=scale_col_major,
+                         device=x.device)
+    fused_add_rmsnorm_group_quant(x, residual, weight, residual_out, None, q, scale, eps,
+                                  group_size, rounding=None if out_dtype == _FP8 else rounding)
+    return residual_out, q, scale
+
+
+def route_for(M: int, D: int, group_size: int = 128) -> dict:
+    """The launch mapping the library chooses for a shape."""
+    return _lib.query_route(M, D, group_size)

@@ -1,0 +1,48 @@
+/*
+ * fagq_diag.h - test and measurement entry points of the fagq library.
+ *
+ * None of these has a counterpart in the reference
+ * (sinpeyw/flagos-kernelgen-72h-shanghai-2026); they exist so that tests can
+ * exercise every launch mapping and the device number-format encoders
+ * directly, and so that HBM byte counters can be calibrated against a copy
+ * of known size.  Same conventions as fagq.h: device pointers,
+ * stream-ordered, status codes, no allocation.
+ */
+#ifndef FAGQ_DIAG_H
+#define FAGQ_DIAG_H
+
+#include <stdint.h>
+
+#include "fagq.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* fagq_launch with an explicit mapping instead of the route table:
+ * waves_per_row in [1, 16], rows_per_block >= 1 with
+ * waves_per_row * rows_per_block <= 16, steps per wave
+ * ceil(ceil(D / 512) / waves_per_row) <= 16 and, when that exceeds 4,
+ * waves_per_row * rows_per_block <= 4.  xcd_remap selects the XCD-aware
+ * workgroup order (0 or 1).  Returns FAGQ_E_FORMAT for an invalid mapping. */
+FAGQ_API int fagq_launch_mapped(const void* x, const void* residual, const void* gamma,
+                                void* residual_out, void* norm_out, void* q, void* scale,
+                                int64_t M, int64_t D, int64_t group_size, float eps,
+                                int q_format, int scale_format, int scale_layout,
+                                int rounding, int waves_per_row, int rows_per_block,
+                                int xcd_remap, void* stream);
+
+/* Encodes n fp32 values (n % 8 == 0, 16-byte aligned) with the operator's
+ * device encoder after its clamp to [-QMAX, QMAX]: one byte per value. */
+FAGQ_API int fagq_diag_encode(const float* in, void* out, int64_t n, int q_format,
+                              int rounding, void* stream);
+
+/* Copies `bytes` (a multiple of 16, both pointers 16-byte aligned) with a
+ * plain 16-byte-vector streaming kernel. */
+FAGQ_API int fagq_diag_copy(const void* src, void* dst, int64_t bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FAGQ_DIAG_H */

@@ -1,0 +1,123 @@
+"""CPU oracle for the fused residual-add + RMSNorm + group-quant operator.
+
+TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg may import this package, and only as the checker
+(or, for the baseline, as the CPU path being timed); the product library
+never loads it.
+
+Two restatements of the reference algorithm
+(sinpeyw/flagos-kernelgen-72h-shanghai-2026,
+src/task01_fused_add_rmsnorm_group_quant.py:65-121 and :1066-1348):
+
+* ``fagq`` - the C restatement in fagq_oracle.c (scalar, OpenMP over rows),
+  called through ctypes on numpy arrays.  This is the parity reference.
+* ``torch_eager.fagq_torch`` - the same formulas as eager PyTorch CPU ops,
+  the "CPU PyTorch path" that the benchmark times as its CPU baseline.
+
+bf16 tensors are passed as their uint16 bit patterns.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+ORACLE_DIR = Path(__file__).resolve().parent
+LIB_PATH = ORACLE_DIR / "libfagq_oracle.so"
+
+Q_INT8, Q_FP8 = 0, 1
+S_F32, S_UE8M0 = 0, 1
+L_ROW, L_COL = 0, 1
+R_RNE, R_TRUNC = 0, 1
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            from . import build as _build
+            _build.build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        P, I64, I, F = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
+        L.orc_bf16_from_f32.argtypes = [P, P, I64]
+        L.orc_bf16_from_f32.restype = None
+        L.orc_encode.argtypes = [P, P, I64, I, I]
+        L.orc_encode.restype = None
+        L.orc_e4m3fn_raw.argtypes = [P, P, I64]
+        L.orc_e4m3fn_raw.restype = None
+        L.orc_ceil_log2.argtypes = [P, P, I64]
+        L.orc_ceil_log2.restype = None
+        L.orc_fagq.argtypes = [P, P, P, P, P, P, P, I64, I64, I64, F, I, I, I, I, I]
+        L.orc_fagq.restype = I
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def bf16_from_f32(v: np.ndarray) -> np.ndarray:
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    out = np.empty(v.shape, np.uint16)
+    lib().orc_bf16_from_f32(_ptr(v), _ptr(out), v.size)
+    return out
+
+
+def f32_from_bf16(b: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def encode(t: np.ndarray, q_format: int, rounding: int = R_RNE) -> np.ndarray:
+    """Codes for already-scaled values, after the operator's clamp to +-QMAX."""
+    t = np.ascontiguousarray(t, dtype=np.float32)
+    out = np.empty(t.shape, np.uint8)
+    lib().orc_encode(_ptr(t), _ptr(out), t.size, q_format, rounding)
+    return out
+
+
+def e4m3fn_raw(v: np.ndarray) -> np.ndarray:
+    """fp32 -> e4m3fn bits, round-to-nearest-even, no clamp (overflow -> NaN)."""
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    out = np.empty(v.shape, np.uint8)
+    lib().orc_e4m3fn_raw(_ptr(v), _ptr(out), v.size)
+    return out
+
+
+def ceil_log2(s: np.ndarray) -> np.ndarray:
+    s = np.ascontiguousarray(s, dtype=np.float32)
+    out = np.empty(s.shape, np.int32)
+    lib().orc_ceil_log2(_ptr(s), _ptr(out), s.size)
+    return out
+
+
+def fagq(x: np.ndarray, residual: np.ndarray, gamma: np.ndarray, eps: float, group_size: int,
+         q_format: int = Q_FP8, scale_format: int = S_F32, scale_layout: int = L_ROW,
+         rounding: int = R_RNE, with_norm: bool = False, nthreads: int = 0) -> dict:
+    """Runs the C restatement.  x, residual: uint16 [M, D] (bf16 bits);
+    gamma: uint16 [D].  Returns residual_out (uint16), q (uint8 codes),
+    scale (float32 or uint8, physical layout [M, groups] or [groups, M]) and
+    norm_out (uint16) when with_norm."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    residual = np.ascontiguousarray(residual, dtype=np.uint16)
+    gamma = np.ascontiguousarray(gamma, dtype=np.uint16)
+    M, D = x.shape
+    assert residual.shape == (M, D) and gamma.shape == (D,)
+    groups = D // group_size
+    res_out = np.empty((M, D), np.uint16)
+    norm_out = np.empty((M, D), np.uint16) if with_norm else None
+    q = np.empty((M, D), np.uint8)
+    sdt = np.float32 if scale_format == S_F32 else np.uint8
+    scale = np.empty((groups, M) if scale_layout == L_COL else (M, groups), sdt)
+    st = lib().orc_fagq(_ptr(x), _ptr(residual), _ptr(gamma), _ptr(res_out), _ptr(norm_out),
+                        _ptr(q), _ptr(scale), M, D, group_size, float(eps), q_format,
+                        scale_format, scale_layout, rounding, nthreads)
+    if st != 0:
+        raise ValueError(f"oracle rejected the arguments (status {st})")
+    out = {"residual_out": res_out, "q": q, "scale": scale}
+    if with_norm:
+        out["norm_out"] = norm_out
+    return out

@@ -1,0 +1,37 @@
+"""Builds the C oracle (test infrastructure) into oracle/libfagq_oracle.so.
+
+The oracle restates the reference's algorithm on the CPU and is used only as
+the checker by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+leg.  The reference repository itself is Python/Triton: there is no native
+reference source to compile, so there is no oracle/_ref build.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+from pathlib import Path
+
+ORACLE_DIR = Path(__file__).resolve().parent
+SRC = ORACLE_DIR / "fagq_oracle.c"
+LIB = ORACLE_DIR / "libfagq_oracle.so"
+
+CFLAGS = ["-O2", "-std=gnu11", "-fPIC", "-shared", "-fopenmp", "-ffp-contract=off",
+          "-fno-fast-math", "-fvisibility=hidden", "-Wall", "-Wextra"]
+
+
+def build(verbose: bool = False) -> Path:
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = ["gcc", *CFLAGS, "-o", str(tmp), str(SRC), "-lm"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"oracle build failed:\n{res.stdout}")
+    if verbose and res.stdout.strip():
+        print(res.stdout, flush=True)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,35 @@
+import sys
+from pathlib import Path
+
+import pytest
+
+REPO_DIR = Path(__file__).resolve().parents[1]
+if str(REPO_DIR) not in sys.path:
+    sys.path.insert(0, str(REPO_DIR))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+    config.addinivalue_line("markers", "slow: CPU test that takes more than a few seconds")
+
+
+@pytest.fixture(scope="session")
+def pkg():
+    import __graft_entry__ as ge
+    return ge.load_package()
+
+
+@pytest.fixture(scope="session")
+def lib(pkg):
+    return pkg.load_library()
+
+
+@pytest.fixture(scope="session")
+def gpu(pkg):
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    pkg.load_library()
+    return dev

@@ -1,0 +1,193 @@
+"""The C ABI boundary and the Python host layer, without a GPU: the library
+loads and exports everything include/*.h declares, the route table keeps its
+invariants, and every argument error is reported before any device work."""
+import ctypes
+import math
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+REPO = Path(__file__).resolve().parents[1]
+HEADERS = sorted((REPO / "include").glob("*.h"))
+
+
+def declared_functions():
+    names = []
+    for h in HEADERS:
+        text = h.read_text()
+        names += re.findall(r"FAGQ_API\s+[\w\s\*]+?\b(\w+)\s*\(", text)
+    return names
+
+
+def test_headers_declare_the_abi():
+    names = declared_functions()
+    assert "fagq_launch" in names and "fagq_query_route" in names
+    assert len(names) == len(set(names))
+
+
+def test_library_exports_every_declared_symbol(pkg, lib):
+    from fagq_mi355x import _lib
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, name
+    assert set(_lib.SIGNATURES) == set(declared_functions())
+
+
+def test_version_and_status_strings(lib):
+    assert lib.fagq_version() == 10000
+    for st in range(0, 10):
+        s = lib.fagq_status_string(st).decode()
+        assert s and s != "unknown status"
+    assert lib.fagq_status_string(-1).decode() == "HIP runtime error"
+
+
+SHAPES = [(M, D) for M in (1, 4, 16, 32, 100, 128, 512, 4096, 16384) for D in
+          (128, 640, 4096, 5120, 7168, 8192, 8448, 16384, 32768)]
+
+
+@pytest.mark.parametrize("M,D", SHAPES)
+def test_route_invariants(pkg, M, D):
+    r = pkg.route_for(M, D, 128)
+    wpr, ns, rpb = r["waves_per_row"], r["steps_per_wave"], r["rows_per_block"]
+    steps = math.ceil(D / 512)
+    assert 1 <= wpr <= 16 and 1 <= ns <= 16 and rpb >= 1
+    assert wpr * ns >= steps > (wpr - 1) * ns          # every wave owns >= 1 column
+    assert r["block_threads"] == 64 * wpr * rpb <= 1024
+    if ns > 4:
+        assert r["block_threads"] <= 256
+    assert r["grid_blocks"] * rpb >= M > (r["grid_blocks"] - 1) * rpb
+    if M >= 2048 and D <= 8192:
+        assert wpr == 1                                  # prefill: one wave per row
+    if M <= 32 and D == 8192:
+        assert (wpr, ns) == (16, 1)                      # decode: row split over 16 waves
+
+
+@pytest.mark.parametrize("args,status", [
+    ((4, 4096, 100), 3), ((4, 4000, 128), 2), ((-1, 4096, 128), 2), ((4, 0, 128), 2),
+    ((4, 65536, 128), 7),
+])
+def test_route_rejects_bad_shapes(lib, args, status):
+    from fagq_mi355x import _lib
+    r = _lib.Route()
+    assert lib.fagq_query_route(*args, ctypes.byref(r)) == status
+
+
+# Fake, aligned, non-overlapping device addresses: validation never dereferences them.
+BASE = 0x10_0000_0000
+
+
+def fake(i):
+    return ctypes.c_void_p(BASE + i * 0x1_0000_0000)
+
+
+def call(lib, **kw):
+    a = dict(x=fake(0), residual=fake(1), gamma=fake(2), residual_out=fake(3), norm_out=None,
+             q=fake(4), scale=fake(5), M=8, D=4096, G=128, eps=1e-6, qf=1, sf=0, layout=0,
+             rounding=0, stream=None)
+    a.update(kw)
+    return lib.fagq_launch(a["x"], a["residual"], a["gamma"], a["residual_out"], a["norm_out"],
+                           a["q"], a["scale"], a["M"], a["D"], a["G"], a["eps"], a["qf"],
+                           a["sf"], a["layout"], a["rounding"], a["stream"])
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(x=None), 1), (dict(residual=None), 1), (dict(gamma=None), 1),
+    (dict(residual_out=None), 1), (dict(q=None), 1), (dict(scale=None), 1),
+    (dict(qf=2), 5), (dict(sf=2), 5), (dict(layout=2), 5), (dict(rounding=2), 5),
+    (dict(qf=1, rounding=1), 5),                        # fp8 codes are RNE only
+    (dict(G=32), 3), (dict(G=512), 3), (dict(D=4000), 2), (dict(M=-1), 2),
+    (dict(D=65536), 7), (dict(eps=-1e-6), 6), (dict(eps=float("nan")), 6),
+    (dict(eps=float("inf")), 6),
+    (dict(x=ctypes.c_void_p(BASE + 8)), 4), (dict(gamma=ctypes.c_void_p(BASE + 0x2_0000_0004)), 4),
+    (dict(q=ctypes.c_void_p(BASE + 0x4_0000_0004)), 4),
+    (dict(scale=ctypes.c_void_p(BASE + 0x5_0000_0002)), 4),
+    (dict(norm_out=ctypes.c_void_p(BASE + 0x6_0000_0008)), 4),
+    (dict(q=ctypes.c_void_p(BASE + 0x1000)), 9),        # codes overlap x
+    (dict(residual_out=ctypes.c_void_p(BASE + 0x1_0000_0000 + 0x100)), 9),   # partial overlap
+    (dict(scale=fake(3)), 9),
+    (dict(norm_out=fake(4)), 9),
+    (dict(M=0), 0),                                     # no-op, device never touched
+])
+def test_launch_validation(lib, kw, status):
+    assert call(lib, **kw) == status
+
+
+def test_in_place_residual_is_accepted_by_validation(lib):
+    # residual_out == residual passes validation; with M = 0 nothing is launched.
+    assert call(lib, residual_out=fake(1), M=0) == 0
+
+
+def test_mapped_launch_rejects_bad_mappings(lib):
+    def mapped(wpr, rpb, remap=1, D=7168):
+        return lib.fagq_launch_mapped(fake(0), fake(1), fake(2), fake(3), None, fake(4), fake(5),
+                                      8, D, 128, 1e-6, 1, 0, 0, 0, wpr, rpb, remap, None)
+    assert mapped(0, 1) == 5
+    assert mapped(17, 1) == 5
+    assert mapped(4, 5) == 5          # 20 waves > 16
+    assert mapped(1, 8) == 5          # 14 steps per wave needs <= 4 waves per block
+    assert mapped(1, 1, remap=2) == 5
+    assert mapped(1, 1, D=16384) == 5  # 32 steps in one wave
+
+
+def test_diag_validation(lib):
+    assert lib.fagq_diag_encode(None, fake(1), 8, 1, 0, None) == 1
+    assert lib.fagq_diag_encode(fake(0), fake(1), 9, 1, 0, None) == 2
+    assert lib.fagq_diag_encode(fake(0), fake(1), 8, 1, 1, None) == 5
+    assert lib.fagq_diag_encode(fake(0), fake(1), 0, 1, 0, None) == 0
+    assert lib.fagq_diag_copy(fake(0), fake(1), 15, None) == 2
+    assert lib.fagq_diag_copy(None, fake(1), 16, None) == 1
+    assert lib.fagq_diag_copy(fake(0), fake(1), 0, None) == 0
+
+
+# ----------------------------------------------------------------- Python layer
+
+def cpu_args(M=4, D=512, qdt=torch.float8_e4m3fn):
+    x = torch.zeros(M, D, dtype=torch.bfloat16)
+    return dict(x=x, residual=x.clone(), gamma=torch.ones(D, dtype=torch.bfloat16),
+                residual_out=x.clone(), norm_out=None, x_q=torch.empty(M, D, dtype=qdt),
+                x_scale=torch.empty(M, D // 128), eps=1e-6, group_size=128)
+
+
+def test_cpu_tensors_are_rejected(pkg):
+    with pytest.raises(ValueError, match="GPU"):
+        pkg.fused_add_rmsnorm_group_quant(**cpu_args())
+
+
+def test_format_inference(pkg):
+    from fagq_mi355x import _lib, ops
+    assert ops._q_format(torch.empty(1, dtype=torch.int8)) == _lib.Q_INT8
+    assert ops._q_format(torch.empty(1, dtype=torch.float8_e4m3fn)) == _lib.Q_FP8_E4M3FN
+    with pytest.raises(TypeError):
+        ops._q_format(torch.empty(1, dtype=torch.uint8))
+    assert ops._scale_format(torch.empty(1)) == _lib.SCALE_F32
+    assert ops._scale_format(torch.empty(1, dtype=torch.uint8)) == _lib.SCALE_UE8M0
+    with pytest.raises(TypeError):
+        ops._scale_format(torch.empty(1, dtype=torch.float16))
+    row = pkg.empty_scales(6, 4)
+    col = pkg.empty_scales(6, 4, col_major=True)
+    assert ops._scale_layout(row, 6, 4) == _lib.LAYOUT_ROW_MAJOR
+    assert ops._scale_layout(col, 6, 4) == _lib.LAYOUT_COL_MAJOR
+    assert col.shape == (6, 4) and col.stride() == (1, 6)
+    with pytest.raises(ValueError):
+        ops._scale_layout(torch.empty(6, 8)[:, ::2], 6, 4)
+    with pytest.raises(ValueError):
+        ops._scale_layout(row, 6, 5)
+    # The reference's int8 cast truncates; fp8 rounds to nearest even only.
+    assert ops._rounding(None, _lib.Q_INT8) == _lib.ROUND_TRUNC
+    assert ops._rounding("rne", _lib.Q_INT8) == _lib.ROUND_RNE
+    assert ops._rounding(None, _lib.Q_FP8_E4M3FN) == _lib.ROUND_RNE
+    with pytest.raises(ValueError):
+        ops._rounding("trunc", _lib.Q_FP8_E4M3FN)
+    with pytest.raises(ValueError):
+        ops._rounding("floor", _lib.Q_INT8)
+
+
+def test_status_errors_name_the_code(pkg):
+    from fagq_mi355x import _lib
+    err = _lib.FagqError(9)
+    assert "FAGQ_E_ALIAS" in str(err) and err.status == 9
+    with pytest.raises(_lib.FagqError):
+        _lib.check(3)
+    _lib.check(0)
