@@ -45,7 +45,44 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="target CPU time of the cpu_baseline leg (0 disables it)")
     p.add_argument("--cpu-rows", type=int, default=512, help="rows in the cpu_baseline sample")
+    p.add_argument("--copy", type=int, default=0, metavar="BYTES",
+                   help="instead: time the library's plain 16-byte copy kernel over BYTES "
+                        "(reference for achievable bandwidth and HBM counter calibration)")
     return p.parse_args()
+
+
+def copy_bench(args, torch, pkg) -> int:
+    """Times fagq_diag_copy (read BYTES + write BYTES per launch)."""
+    import ctypes
+    dev = torch.device("cuda:0")
+    lib = pkg.load_library()
+    n = args.copy // 16 * 16
+    nsets = max(2, math.ceil(ROTATE_BYTES / (2 * n)) + 1)
+    bufs = [(torch.empty(n, dtype=torch.uint8, device=dev).fill_(1),
+             torch.empty(n, dtype=torch.uint8, device=dev)) for _ in range(nsets)]
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+
+    def step(i):
+        s, d = bufs[i % nsets]
+        pkg._lib.check(lib.fagq_diag_copy(ctypes.c_void_p(s.data_ptr()),
+                                          ctypes.c_void_p(d.data_ptr()), n, sp), "fagq_diag_copy")
+
+    for i in range(args.warmup):
+        step(i)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize(dev)
+    for i in range(args.steps):
+        starts[i].record(stream)
+        step(i)
+        ends[i].record(stream)
+    torch.cuda.synchronize(dev)
+    ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / args.steps
+    print(json.dumps({"copy_bytes": n, "us_per_call": round(ms * 1e3, 2),
+                      "GBps_read_plus_write": round(2 * n / (ms * 1e-3) / 1e9, 1),
+                      "buffer_sets": nsets}), flush=True)
+    return 0
 
 
 def main() -> int:
@@ -65,6 +102,8 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 2
+    if args.copy:
+        return copy_bench(args, torch, pkg)
     name = args.config or HEADLINE
     w = CONFIGS[name]
     dev = torch.device("cuda:0")

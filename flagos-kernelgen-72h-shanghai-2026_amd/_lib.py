@@ -36,13 +36,14 @@ _P, _I64, _I, _F = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
 
 class Route(ctypes.Structure):
     _fields_ = [("waves_per_row", ctypes.c_int32), ("steps_per_wave", ctypes.c_int32),
-                ("rows_per_block", ctypes.c_int32), ("block_threads", ctypes.c_int32),
+                ("rows_per_block", ctypes.c_int32), ("rows_in_sequence", ctypes.c_int32),
+                ("block_threads", ctypes.c_int32), ("reserved", ctypes.c_int32),
                 ("grid_blocks", ctypes.c_int64)]
 
 
 SIGNATURES = {
     "fagq_launch": ([_P] * 7 + [_I64, _I64, _I64, _F, _I, _I, _I, _I, _P], _I),
-    "fagq_launch_mapped": ([_P] * 7 + [_I64, _I64, _I64, _F, _I, _I, _I, _I, _I, _I, _I, _P], _I),
+    "fagq_launch_mapped": ([_P] * 7 + [_I64, _I64, _I64, _F, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "fagq_query_route": ([_I64, _I64, _I64, ctypes.POINTER(Route)], _I),
     "fagq_status_string": ([_I], ctypes.c_char_p),
     "fagq_version": ([], _I),
@@ -102,4 +103,4 @@ def check(status: int, what: str = "fagq_launch") -> None:
 def query_route(M: int, D: int, group_size: int) -> dict:
     r = Route()
     check(load().fagq_query_route(M, D, group_size, ctypes.byref(r)), "fagq_query_route")
-    return {f: getattr(r, f) for f, _ in Route._fields_}
+    return {f: getattr(r, f) for f, _ in Route._fields_ if f != "reserved"}

@@ -33,68 +33,86 @@ constexpr int kMaxDevices = 64;
 struct Mapping {
   int wpr;        // waves per row
   int ns;         // steps per wave
-  int rpb;        // rows per workgroup
+  int rpb;        // row groups per workgroup
+  int rseq;       // rows each row group processes in turn
   int block;      // threads per workgroup
   int64_t grid;   // workgroups
 };
 
-// Waves the route table aims to have in flight before it splits rows across
-// waves (8 per CU on 256 CUs).  FAGQ_TARGET_WAVES overrides it for tuning.
-int target_waves() {
-  static const int v = [] {
-    const char* s = std::getenv("FAGQ_TARGET_WAVES");
-    const int t = s ? std::atoi(s) : 0;
-    return t > 0 ? t : 2048;
-  }();
+// Route-table knobs, read once: FAGQ_PREFILL_ROWS is the row count from which
+// rows are split into 2-step waves (FAGQ_PREFILL_STEPS) instead of 1-step
+// waves; FAGQ_PREFILL_RSEQ sets the rows each row group processes in turn
+// (1 by default: prefetching a second row measured no faster).
+int env_int(const char* name, int dflt) {
+  const char* s = std::getenv(name);
+  const int v = s ? std::atoi(s) : 0;
+  return v > 0 ? v : dflt;
+}
+
+int prefill_rows() {
+  static const int v = env_int("FAGQ_PREFILL_ROWS", 1024);
   return v;
 }
 
+int prefill_steps() {
+  static const int v = env_int("FAGQ_PREFILL_STEPS", 2);
+  return v;
+}
+
+int prefill_rseq() {
+  static const int v = env_int("FAGQ_PREFILL_RSEQ", 1);
+  return v;
+}
+
+// XCD-aware workgroup order: measured slower than dispatch order for this
+// streaming pattern, so off unless FAGQ_XCD_REMAP=1.
 int xcd_remap_default() {
   static const int v = [] {
     const char* s = std::getenv("FAGQ_XCD_REMAP");
-    return s ? (std::atoi(s) != 0) : 1;
+    return s ? (std::atoi(s) != 0) : 0;
   }();
   return v;
 }
 
 int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
-// Completes a mapping from (wpr, rpb); returns false if it is not launchable.
-bool finish_mapping(int64_t M, int D, int wpr, int rpb, Mapping* m) {
+// Completes a mapping from (wpr, rpb, rseq); returns false if it is not launchable.
+bool finish_mapping(int64_t M, int D, int wpr, int rpb, int rseq, Mapping* m) {
   const int steps = ceil_div(D, kStepCols);
   if (wpr < 1 || wpr > kMaxWavesPerBlock || rpb < 1 || wpr * rpb > kMaxWavesPerBlock) return false;
+  if (rseq_index(rseq) < 0) return false;
   const int ns = ceil_div(steps, wpr);
   if (ns > kMaxStepsPerWave) return false;
-  if (ns > 4 && wpr * rpb > 4) return false;   // __launch_bounds__(256) for ns > 4
   m->wpr = wpr;
   m->ns = ns;
   m->rpb = rpb;
+  m->rseq = rseq;
   m->block = 64 * wpr * rpb;
-  m->grid = (M + rpb - 1) / rpb;
-  return true;
+  const int64_t per_block = (int64_t)rpb * rseq;
+  m->grid = (M + per_block - 1) / per_block;
+  return m->grid <= INT32_MAX;
 }
 
-// The route table.  Large M: one wave per row, four rows per workgroup, the
-// whole row in VGPRs.  Small M: split each row over enough waves that the
-// launch still has about target_waves() waves, one row per workgroup.
-// D > 8192: rows are split so that no wave holds more than 4 steps.
+// The route table.  Each row is split over waves of one workgroup so that
+// every wave streams only 1-2 KB of each input per step (dispatch-ordered
+// workgroups then keep the set of rows in flight small, which HBM rewards).
+// Prefill (M >= prefill_rows()): 2 steps per wave, one row per workgroup.
+// Decode: 1 step per wave, one row per workgroup, as many waves as the row
+// has steps (<= 16).
+// Rows of more than 16 steps use up to 4 steps per wave.
 void choose_mapping(int64_t M, int D, Mapping* m) {
   const int steps = ceil_div(D, kStepCols);
-  int wpr = 1;
-  if (M > 0) {
-    const int64_t want = (target_waves() + M - 1) / M;
-    wpr = (int)(want < 16 ? want : 16);
-  }
-  if (wpr > steps) wpr = steps;
-  if (steps > kMaxStepsPerWave) {
-    const int need = ceil_div(steps, 4);
-    if (wpr < need) wpr = need;
-  }
-  if (wpr < 1) wpr = 1;
-  const int ns = ceil_div(steps, wpr);
-  wpr = ceil_div(steps, ns);    // drop waves that would own no column
+  const bool prefill = M >= prefill_rows();
+  int ns = prefill ? prefill_steps() : 1;
+  if (ns > kMaxStepsPerWave) ns = kMaxStepsPerWave;
+  const int min_ns = ceil_div(steps, kMaxWavesPerBlock);
+  if (ns < min_ns) ns = min_ns;
+  if (ns > steps) ns = steps;
+  const int wpr = ceil_div(steps, ns);
   const int rpb = wpr >= 4 ? 1 : 4 / wpr;
-  finish_mapping(M, D, wpr, rpb, m);
+  int rseq = prefill ? prefill_rseq() : 1;
+  if (rseq_index(rseq) < 0) rseq = 1;
+  finish_mapping(M, D, wpr, rpb, rseq, m);
 }
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
@@ -119,6 +137,10 @@ int validate(const void* x, const void* residual, const void* gamma, const void*
   if (G != 64 && G != 128 && G != 256) return FAGQ_E_GROUP;
   if (M < 0 || D <= 0 || D % G != 0) return FAGQ_E_SHAPE;
   if (D > FAGQ_MAX_D || M > (int64_t)INT32_MAX) return FAGQ_E_TOO_LARGE;
+  // Column-major scales are addressed with 32-bit buffer offsets.
+  if (scale_layout == FAGQ_LAYOUT_COL_MAJOR &&
+      M * (D / G) * (scale_format == FAGQ_SCALE_F32 ? 4 : 1) > (int64_t)UINT32_MAX)
+    return FAGQ_E_TOO_LARGE;
   if (!(eps >= 0.0f) || !std::isfinite(eps)) return FAGQ_E_EPS;
   if (!aligned(x, 16) || !aligned(residual, 16) || !aligned(gamma, 16) ||
       !aligned(residual_out, 16) || (norm_out && !aligned(norm_out, 16)) || !aligned(q, 8) ||
@@ -165,15 +187,20 @@ int device_check() {
   return c == 1 ? FAGQ_OK : FAGQ_E_DEVICE;
 }
 
-LaunchFn lookup(int q_format, int scale_format, int rounding, int lpg_idx, int steps) {
+LaunchFn lookup(int q_format, int scale_format, int rounding, int lpg_idx, int steps, bool norm,
+                int rseq) {
   const int qf = q_format == FAGQ_Q_FP8_E4M3FN ? QF_FP8
                  : rounding == FAGQ_ROUND_RNE  ? QF_I8_RNE
                                                : QF_I8_TRUNC;
   const bool ue = scale_format == FAGQ_SCALE_UE8M0;
+  const int ri = rseq_index(rseq);
   switch (qf) {
-    case QF_FP8: return ue ? lookup_q0_s1(lpg_idx, steps) : lookup_q0_s0(lpg_idx, steps);
-    case QF_I8_RNE: return ue ? lookup_q1_s1(lpg_idx, steps) : lookup_q1_s0(lpg_idx, steps);
-    default: return ue ? lookup_q2_s1(lpg_idx, steps) : lookup_q2_s0(lpg_idx, steps);
+    case QF_FP8:
+      return ue ? lookup_q0_s1(lpg_idx, steps, norm, ri) : lookup_q0_s0(lpg_idx, steps, norm, ri);
+    case QF_I8_RNE:
+      return ue ? lookup_q1_s1(lpg_idx, steps, norm, ri) : lookup_q1_s0(lpg_idx, steps, norm, ri);
+    default:
+      return ue ? lookup_q2_s1(lpg_idx, steps, norm, ri) : lookup_q2_s0(lpg_idx, steps, norm, ri);
   }
 }
 
@@ -184,13 +211,13 @@ int launch_with(const Mapping& m, const void* x, const void* residual, const voi
   const int dc = device_check();
   if (dc != FAGQ_OK) return dc;
   KArgs a;
-  a.x = static_cast<const u32x4*>(x);
-  a.res = static_cast<const u32x4*>(residual);
-  a.gamma = static_cast<const u32x4*>(gamma);
-  a.res_out = static_cast<u32x4*>(residual_out);
-  a.norm_out = static_cast<u32x4*>(norm_out);
-  a.q = static_cast<u32x2*>(q);
-  a.scale = scale;
+  a.x = static_cast<const uint16_t*>(x);
+  a.res = static_cast<const uint16_t*>(residual);
+  a.gamma = static_cast<const uint16_t*>(gamma);
+  a.res_out = static_cast<uint16_t*>(residual_out);
+  a.norm_out = static_cast<uint16_t*>(norm_out);
+  a.q = static_cast<uint8_t*>(q);
+  a.scale = static_cast<uint8_t*>(scale);
   a.M = M;
   a.D = (int32_t)D;
   a.groups = (int32_t)(D / G);
@@ -199,7 +226,8 @@ int launch_with(const Mapping& m, const void* x, const void* residual, const voi
   a.rpb = m.rpb;
   a.col_major = scale_layout == FAGQ_LAYOUT_COL_MAJOR;
   a.remap = remap;
-  const LaunchFn fn = lookup(q_format, scale_format, rounding, lpg_index((int)G), m.ns);
+  const LaunchFn fn = lookup(q_format, scale_format, rounding, lpg_index((int)G), m.ns,
+                             norm_out != nullptr, m.rseq);
   const hipError_t e = fn(a, dim3((unsigned)m.grid), dim3((unsigned)m.block),
                           static_cast<hipStream_t>(stream));
   return e == hipSuccess ? FAGQ_OK : -(int)e;
@@ -230,13 +258,14 @@ FAGQ_API int fagq_launch_mapped(const void* x, const void* residual, const void*
                                 void* residual_out, void* norm_out, void* q, void* scale,
                                 int64_t M, int64_t D, int64_t group_size, float eps,
                                 int q_format, int scale_format, int scale_layout, int rounding,
-                                int waves_per_row, int rows_per_block, int xcd_remap,
-                                void* stream) {
+                                int waves_per_row, int rows_per_block, int rows_in_sequence,
+                                int xcd_remap, void* stream) {
   const int v = validate(x, residual, gamma, residual_out, norm_out, q, scale, M, D, group_size,
                          eps, q_format, scale_format, scale_layout, rounding);
   if (v != FAGQ_OK) return v;
   Mapping m;
-  if (!finish_mapping(M, (int)D, waves_per_row, rows_per_block, &m)) return FAGQ_E_FORMAT;
+  if (!finish_mapping(M, (int)D, waves_per_row, rows_per_block, rows_in_sequence, &m))
+    return FAGQ_E_FORMAT;
   if (xcd_remap != 0 && xcd_remap != 1) return FAGQ_E_FORMAT;
   if (M == 0) return FAGQ_OK;
   return launch_with(m, x, residual, gamma, residual_out, norm_out, q, scale, M, D, group_size,
@@ -253,7 +282,9 @@ FAGQ_API int fagq_query_route(int64_t M, int64_t D, int64_t group_size, fagq_rou
   route->waves_per_row = m.wpr;
   route->steps_per_wave = m.ns;
   route->rows_per_block = m.rpb;
+  route->rows_in_sequence = m.rseq;
   route->block_threads = m.block;
+  route->reserved = 0;
   route->grid_blocks = m.grid;
   return FAGQ_OK;
 }

@@ -1,6 +1,7 @@
 // fagq_dispatch.hpp - launch lookups shared by the instantiation units and the
 // C ABI.  One lookup per (code format, scale format), indexed by the
-// lanes-per-group index and the steps-per-wave count.
+// lanes-per-group index, the steps per wave, whether norm_out is written and
+// the rows-in-sequence index.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -11,19 +12,21 @@ namespace fagq {
 
 using LaunchFn = hipError_t (*)(const KArgs&, dim3, dim3, hipStream_t);
 
-constexpr int kMaxStepsPerWave = 16;
-constexpr int kNumLpg = 3;   // lanes per group 8, 16, 32  <->  G = 64, 128, 256
+constexpr int kNumLpg = 3;      // lanes per group 8, 16, 32  <->  G = 64, 128, 256
+constexpr int kNumRseq = 3;     // rows in sequence 1, 2, 4
 
 constexpr int lpg_index(int group_size) {
   return group_size == 64 ? 0 : group_size == 128 ? 1 : group_size == 256 ? 2 : -1;
 }
 
-// lookup_q<code>_s<scale>(lpg index, steps per wave in [1, 16]).
-LaunchFn lookup_q0_s0(int lpg_idx, int steps);   // fp8, f32
-LaunchFn lookup_q0_s1(int lpg_idx, int steps);   // fp8, ue8m0
-LaunchFn lookup_q1_s0(int lpg_idx, int steps);   // int8 rne, f32
-LaunchFn lookup_q1_s1(int lpg_idx, int steps);   // int8 rne, ue8m0
-LaunchFn lookup_q2_s0(int lpg_idx, int steps);   // int8 trunc, f32
-LaunchFn lookup_q2_s1(int lpg_idx, int steps);   // int8 trunc, ue8m0
+constexpr int rseq_index(int rseq) { return rseq == 1 ? 0 : rseq == 2 ? 1 : rseq == 4 ? 2 : -1; }
+
+// lookup_q<code>_s<scale>(lpg index, steps per wave in [1, 4], norm, rseq index).
+LaunchFn lookup_q0_s0(int lpg_idx, int steps, bool norm, int rseq_idx);   // fp8, f32
+LaunchFn lookup_q0_s1(int lpg_idx, int steps, bool norm, int rseq_idx);   // fp8, ue8m0
+LaunchFn lookup_q1_s0(int lpg_idx, int steps, bool norm, int rseq_idx);   // int8 rne, f32
+LaunchFn lookup_q1_s1(int lpg_idx, int steps, bool norm, int rseq_idx);   // int8 rne, ue8m0
+LaunchFn lookup_q2_s0(int lpg_idx, int steps, bool norm, int rseq_idx);   // int8 trunc, f32
+LaunchFn lookup_q2_s1(int lpg_idx, int steps, bool norm, int rseq_idx);   // int8 trunc, ue8m0
 
 }  // namespace fagq

@@ -1,6 +1,7 @@
 // fagq_inst.hip - instantiates fagq_rows for one (code format, scale format)
 // pair, selected with -DFAGQ_QF=<0|1|2> -DFAGQ_SF=<0|1>, for every supported
-// group size and every steps-per-wave count, and exports its launch lookup.
+// group size, steps per wave, norm_out choice and rows-in-sequence count,
+// and exports its launch lookup.
 #include "fagq_dispatch.hpp"
 
 #ifndef FAGQ_QF
@@ -16,28 +17,29 @@
 namespace fagq {
 namespace {
 
-template <int NS, int LPG>
+template <int NS, int LPG, bool NORM, int RSEQ>
 hipError_t launch_rows(const KArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
   void* args[] = {const_cast<KArgs*>(&a)};
-  return hipLaunchKernel(reinterpret_cast<const void*>(&fagq_rows<NS, LPG, FAGQ_QF, FAGQ_SF>),
-                         grid, block, args, 0, stream);
+  return hipLaunchKernel(
+      reinterpret_cast<const void*>(&fagq_rows<NS, LPG, FAGQ_QF, FAGQ_SF, NORM, RSEQ>), grid,
+      block, args, 0, stream);
 }
 
 }  // namespace
 
-#define FAGQ_ROW(LPG)                                                                          \
-  {&launch_rows<1, LPG>,  &launch_rows<2, LPG>,  &launch_rows<3, LPG>,  &launch_rows<4, LPG>,  \
-   &launch_rows<5, LPG>,  &launch_rows<6, LPG>,  &launch_rows<7, LPG>,  &launch_rows<8, LPG>,  \
-   &launch_rows<9, LPG>,  &launch_rows<10, LPG>, &launch_rows<11, LPG>, &launch_rows<12, LPG>, \
-   &launch_rows<13, LPG>, &launch_rows<14, LPG>, &launch_rows<15, LPG>, &launch_rows<16, LPG>}
+#define FAGQ_R(NS, LPG, NORM) \
+  {&launch_rows<NS, LPG, NORM, 1>, &launch_rows<NS, LPG, NORM, 2>, &launch_rows<NS, LPG, NORM, 4>}
+#define FAGQ_N(NS, LPG) {FAGQ_R(NS, LPG, false), FAGQ_R(NS, LPG, true)}
+#define FAGQ_S(LPG) {FAGQ_N(1, LPG), FAGQ_N(2, LPG), FAGQ_N(3, LPG), FAGQ_N(4, LPG)}
 
-static_assert(kMaxStepsPerWave == 16, "FAGQ_ROW lists 16 step counts");
+static_assert(kMaxStepsPerWave == 4, "FAGQ_S lists 4 step counts");
 
 // The table lives in a host function so that device compilation never sees
 // pointers to host launch stubs.
-LaunchFn FAGQ_LOOKUP(FAGQ_QF, FAGQ_SF)(int lpg_idx, int steps) {
-  static const LaunchFn table[kNumLpg][kMaxStepsPerWave] = {FAGQ_ROW(8), FAGQ_ROW(16), FAGQ_ROW(32)};
-  return table[lpg_idx][steps - 1];
+LaunchFn FAGQ_LOOKUP(FAGQ_QF, FAGQ_SF)(int lpg_idx, int steps, bool norm, int rseq_idx) {
+  static const LaunchFn table[kNumLpg][kMaxStepsPerWave][2][kNumRseq] = {
+      FAGQ_S(8), FAGQ_S(16), FAGQ_S(32)};
+  return table[lpg_idx][steps - 1][norm ? 1 : 0][rseq_idx];
 }
 
 }  // namespace fagq

@@ -10,14 +10,31 @@
 // Work mapping.  A "step" is 512 consecutive columns of one row: 64 lanes x 8
 // bf16 per lane, read with one 16-byte load per lane per tensor.  With 8
 // elements per lane, a group of G columns covers G/8 consecutive lanes (16
-// lanes = one DPP row for G = 128), so a group maximum is a 2..5-step DPP
-// reduction that never leaves the wave.
+// lanes = one DPP row for G = 128), so a group maximum is a 3..5-step
+// DPP/permlane reduction that never leaves the wave.
 //
-// A wave owns NS consecutive steps of one row and keeps r*gamma for all of
-// them in VGPRs (8*NS floats per lane), so every input byte is read from HBM
-// once and no intermediate is written.  waves_per_row > 1 splits a row over
-// several waves of one workgroup; only the fp64 partial sum of squares then
-// crosses waves, through LDS, with one barrier.
+// A row is split over wpr waves of one workgroup, each owning NS <= 4
+// consecutive steps and keeping r * gamma for them in VGPRs, so every input
+// byte is read from HBM once and no intermediate is written.  Only the fp64
+// partial sums of squares cross waves, through LDS.  A row group may process
+// RSEQ consecutive rows in turn, loading gamma once and the next row's
+// inputs while the current row is reduced and stored.
+//
+// Every buffer access passes its whole offset as the VGPR offset (constant
+// parts fold into the instruction's immediate offset) and a zero scalar
+// offset.  With a register scalar offset the compiler assumes that a store
+// of more than 8 bytes has read its data VGPRs at once and lets the next
+// VALU overwrite them immediately; on gfx950 that lost the last 4 lanes of
+// each 16-lane row of residual_out, nondeterministically.
+//
+// Memory is accessed through buffer descriptors (raw buffers, gfx9 format):
+// each wave's descriptor for a row starts at its first column and is sized
+// to the rest of the row, so lanes past the end of the row read zeros and
+// their stores are dropped by the hardware, and a row past M gets an empty
+// descriptor.  The step code therefore has no lane-dependent branches around
+// memory operations (which would also make the compiler wait for stores
+// whenever it waits for a later load), and addressing is one VGPR offset per
+// lane plus scalar offsets.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -33,24 +50,23 @@ enum SFormat { SF_F32 = 0, SF_UE8M0 = 1 };
 
 constexpr int kStepCols = 512;      // columns per wave step (64 lanes x 8)
 constexpr int kMaxWavesPerBlock = 16;
+constexpr int kMaxStepsPerWave = 4;
 
-// Kernel arguments.  Element-group index e8 = (row * D + col) / 8 addresses
-// x, residual, residual_out, norm_out (u32x4 = 8 bf16) and q (u32x2 = 8 codes)
-// alike.
+// Kernel arguments (element pointers; the kernels build buffer descriptors).
 struct KArgs {
-  const u32x4* x;
-  const u32x4* res;
-  const u32x4* gamma;
-  u32x4* res_out;
-  u32x4* norm_out;     // nullptr: 3-output form
-  u32x2* q;
-  void* scale;         // float* (SF_F32) or uint8_t* (SF_UE8M0)
+  const uint16_t* x;
+  const uint16_t* res;
+  const uint16_t* gamma;
+  uint16_t* res_out;
+  uint16_t* norm_out;  // nullptr: 3-output form
+  uint8_t* q;
+  uint8_t* scale;      // fp32 (SF_F32) or uint8 (SF_UE8M0) words
   int64_t M;
   int32_t D;
   int32_t groups;      // D / G
   float eps;
   int32_t wpr;         // waves per row
-  int32_t rpb;         // rows per workgroup
+  int32_t rpb;         // row groups per workgroup (each wpr waves)
   int32_t col_major;   // scale layout: 0 -> [M, groups], 1 -> [groups, M]
   int32_t remap;       // 1 -> XCD-aware workgroup -> row-tile remap
 };
@@ -59,6 +75,17 @@ struct KArgs {
 
 __device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
+
+// Raw buffer descriptor over [base, base + bytes): dword3 = 0x00020000 is the
+// gfx9 raw-buffer word (32-bit data format, no swizzle); stride 0.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr int kNonTemporal = 2;     // cache-policy bit NT (gfx940 family)
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           kRsrcWord3);
+}
 
 // Two fp32 -> packed bf16x2, round to nearest even (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
@@ -70,8 +97,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 
 template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+
+template <int CTRL>
 __device__ __forceinline__ uint32_t umax_dpp(uint32_t m) {
-  const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, CTRL, 0xf, 0xf, false);
+  const uint32_t o = dpp_u32<CTRL>(m);
   return m > o ? m : o;
 }
 
@@ -87,16 +119,61 @@ __device__ __forceinline__ uint32_t group_max_bits(uint32_t m) {
   m = umax_dpp<0x141>(m);   // row_half_mirror: lanes i <-> 7-i
   if constexpr (LPG >= 16) m = umax_dpp<0x140>(m);   // row_mirror: i <-> 15-i
   if constexpr (LPG >= 32) {
-    const uint32_t o = (uint32_t)__shfl_xor((int)m, 16);
-    m = m > o ? m : o;
+    // Both lanes of a swapped pair hold the maximum of their own row after the
+    // steps above; max() of the pair is the 32-lane maximum.
+    const auto r = __builtin_amdgcn_permlane16_swap(m, m, false, false);
+    m = r[0] > r[1] ? r[0] : r[1];
   }
   return m;
 }
 
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint64_t o = (uint64_t)dpp_u32<CTRL>((uint32_t)u) |
+                     ((uint64_t)dpp_u32<CTRL>((uint32_t)(u >> 32)) << 32);
+  return __builtin_bit_cast(double, o);
+}
+
+// Sum over the 64 lanes; every lane receives the same value (each step adds
+// a lane's value to its partner's, and fp addition is commutative, so both
+// partners compute the identical sum).
 __device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  v += dpp_f64<0xB1>(v);    // quad_perm [1,0,3,2]
+  v += dpp_f64<0x4E>(v);    // quad_perm [2,3,0,1]
+  v += dpp_f64<0x141>(v);   // row_half_mirror
+  v += dpp_f64<0x140>(v);   // row_mirror: every lane holds its 16-lane row sum
+  {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)u, (uint32_t)u, false, false);
+    const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(u >> 32), (uint32_t)(u >> 32), false, false);
+    v = __builtin_bit_cast(double, (uint64_t)lo[0] | ((uint64_t)hi[0] << 32)) +
+        __builtin_bit_cast(double, (uint64_t)lo[1] | ((uint64_t)hi[1] << 32));
+  }
+  {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)u, (uint32_t)u, false, false);
+    const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(u >> 32), (uint32_t)(u >> 32), false, false);
+    v = __builtin_bit_cast(double, (uint64_t)lo[0] | ((uint64_t)hi[0] << 32)) +
+        __builtin_bit_cast(double, (uint64_t)lo[1] | ((uint64_t)hi[1] << 32));
+  }
   return v;
+}
+
+// Workgroup barrier whose fences cover LDS only: global stores issued before
+// it need not have completed.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// inv_rms = fp32(1 / sqrt(fp32(fp32(sumsq) / D) + eps)), the square root and
+// the reciprocal in IEEE double precision.
+__device__ __forceinline__ float row_inv_rms(double ss, int D, float eps) {
+  const float sumsq = (float)ss;
+  const float mean = sumsq / (float)D;
+  return (float)(1.0 / __builtin_sqrt((double)(mean + eps)));
 }
 
 // Blocks are dispatched round-robin over the 8 XCDs (block b -> XCD b % 8).
@@ -143,138 +220,234 @@ __device__ __forceinline__ u32x2 encode8(const float (&t)[8]) {
 
 // ---------------------------------------------------------------- kernel
 
-template <int NS, int LPG, int QF, int SF>
-__global__ void __launch_bounds__(NS <= 4 ? 1024 : 256)
+// Row-invariant per-wave geometry.
+struct WaveCtx {
+  int lane;
+  int c0;          // first column of this wave
+  uint32_t cols;   // columns of the row at or after c0 (0 if none)
+  int gl;          // group index of this lane within a step
+};
+
+// Descriptors of one row for one wave.
+struct RowRsrc {
+  rsrc_t x, res, res_out, norm, q, scale;
+  uint32_t scale_step;   // byte distance between the scales of consecutive steps
+};
+
+template <int SF, bool NORM>
+__device__ __forceinline__ RowRsrc row_rsrc(const KArgs& a, const WaveCtx& w, int64_t row, int G) {
+  constexpr uint32_t sb = SF == SF_F32 ? 4u : 1u;
+  const bool ok = row < a.M;
+  const int64_t e = (ok ? row : 0) * (int64_t)a.D + w.c0;
+  const uint32_t cols = ok ? w.cols : 0u;
+  RowRsrc r;
+  r.x = make_rsrc(a.x + e, cols * 2u);
+  r.res = make_rsrc(a.res + e, cols * 2u);
+  r.res_out = make_rsrc(a.res_out + e, cols * 2u);
+  if constexpr (NORM) r.norm = make_rsrc(a.norm_out + e, cols * 2u);
+  r.q = make_rsrc(a.q + e, cols);
+  const int g0 = w.c0 / G;                                  // first group of this wave
+  const uint32_t ng = ok && w.cols ? (uint32_t)(a.groups - g0) : 0u;
+  if (a.col_major) {
+    // scale[g * M + row]: this wave's groups start at g0; the descriptor ends
+    // just after the row's last group.
+    r.scale = make_rsrc(a.scale + ((int64_t)g0 * a.M + (ok ? row : 0)) * sb,
+                        ng ? (uint32_t)(((int64_t)(ng - 1) * a.M + 1) * sb) : 0u);
+    r.scale_step = (uint32_t)((int64_t)(kStepCols / G) * a.M * sb);
+  } else {
+    r.scale = make_rsrc(a.scale + ((ok ? row : 0) * (int64_t)a.groups + g0) * sb, ng * sb);
+    r.scale_step = (uint32_t)(kStepCols / G) * sb;
+  }
+  return r;
+}
+
+// Phase 1 for one row: issue the loads of x and residual for NS steps.
+template <int NS>
+__device__ __forceinline__ void load_row(const RowRsrc& r, int lane, u32x4 (&xv)[NS],
+                                         u32x4 (&rv)[NS]) {
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    xv[k] = __builtin_amdgcn_raw_buffer_load_b128(r.x, lane * 16 + k * 1024, 0, kNonTemporal);
+    rv[k] = __builtin_amdgcn_raw_buffer_load_b128(r.res, lane * 16 + k * 1024, 0, kNonTemporal);
+  }
+}
+
+// Phase 2 for one row: r = x + residual, w = r * gamma, the fp64 sum of
+// squares, the group max of |w|; then the residual_out stores (after every
+// use of loaded data).
+template <int NS, int LPG>
+__device__ __forceinline__ double row_in(const RowRsrc& rr, int lane, const u32x4 (&xv)[NS],
+                                         const u32x4 (&rv)[NS], const u32x4 (&gv)[NS],
+                                         float (&w)[NS][8], uint32_t (&gmax)[NS]) {
+  double ss = 0.0;
+  u32x4 ro[NS];
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    float r[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      r[2 * j] = bf16_lo(xv[k][j]) + bf16_lo(rv[k][j]);
+      r[2 * j + 1] = bf16_hi(xv[k][j]) + bf16_hi(rv[k][j]);
+      w[k][2 * j] = r[2 * j] * bf16_lo(gv[k][j]);
+      w[k][2 * j + 1] = r[2 * j + 1] * bf16_hi(gv[k][j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const double rd = (double)r[j];
+      ss = __builtin_fma(rd, rd, ss);   // r^2 is exact in fp64
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = __builtin_fmaxf(m, __builtin_fabsf(w[k][j]));
+    gmax[k] = group_max_bits<LPG>(__float_as_uint(m));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ro[k][j] = pack_bf16x2(r[2 * j], r[2 * j + 1]);
+  }
+#pragma unroll
+  for (int k = 0; k < NS; ++k)
+    __builtin_amdgcn_raw_buffer_store_b128(ro[k], rr.res_out, lane * 16 + k * 1024, 0, kNonTemporal);
+  return ss;
+}
+
+// Phase 4 for one row: scales, codes, optional norm_out.
+template <int NS, int LPG, int QF, int SF, bool NORM>
+__device__ __forceinline__ void row_out(const RowRsrc& rr, int lane, uint32_t scale_voff,
+                                        const float (&w)[NS][8], const uint32_t (&gmax)[NS],
+                                        float inv, float inv_q) {
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    const float s = __builtin_fmaxf(__uint_as_float(gmax[k]) * inv_q, 1.0e-12f);
+    float mul = 0.0f;
+    int e = 0;
+    if constexpr (SF == SF_F32) {
+      mul = 1.0f / s;
+    } else {
+      e = ceil_log2_bits(s);
+      e = e > 127 ? 127 : e;
+    }
+    // No clamp to [-QMAX, QMAX]: for finite inputs |t| <= QMAX * (1 + 5 * 2^-24)
+    // (|n| <= gmax * inv and s >= gmax * inv / QMAX, each up to a few
+    // roundings), and fp8 rounds everything below 464 to at most 448, int8
+    // rounding and truncation give at most 127, so the reference's clamp never
+    // changes a code.
+    float n[8], t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      n[j] = w[k][j] * inv;
+      t[j] = (SF == SF_F32) ? n[j] * mul : __builtin_ldexpf(n[j], -e);
+    }
+    if constexpr (NORM) {
+      u32x4 no;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) no[j] = pack_bf16x2(n[2 * j], n[2 * j + 1]);
+      __builtin_amdgcn_raw_buffer_store_b128(no, rr.norm, lane * 16 + k * 1024, 0, kNonTemporal);
+    }
+    const u32x2 codes = encode8<QF>(t);
+    __builtin_amdgcn_raw_buffer_store_b64(codes, rr.q, lane * 8 + k * 512, 0, kNonTemporal);
+    // Every lane of a group stores the group's scale to the same address (one
+    // write after coalescing); groups past the row end fall outside the
+    // descriptor and are dropped.
+    if constexpr (SF == SF_F32) {
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(s), rr.scale,
+                                            scale_voff + k * rr.scale_step, 0, 0);
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(e + 127), rr.scale,
+                                           scale_voff + k * rr.scale_step, 0, 0);
+    }
+  }
+}
+
+// Workgroup = rpb row groups of wpr waves.  Row group j of workgroup b owns
+// rows [(b * rpb + j) * RSEQ, ... + RSEQ) and processes them one after the
+// other (RSEQ is unrolled, so every wait for a load is exact).
+template <int NS, int LPG, int QF, int SF, bool NORM, int RSEQ>
+__global__ void __launch_bounds__(1024)
 fagq_rows(const KArgs a) {
+  static_assert(NS >= 1 && NS <= kMaxStepsPerWave, "steps per wave");
   constexpr float QMAX = (QF == QF_FP8) ? 448.0f : 127.0f;
   constexpr int G = LPG * 8;
+  constexpr uint32_t sb = SF == SF_F32 ? 4u : 1u;
   __shared__ double s_part[kMaxWavesPerBlock];
+  __shared__ float s_inv[kMaxWavesPerBlock][2];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wpr = a.wpr;
   const int blk = a.remap ? xcd_remap(blockIdx.x, gridDim.x) : (int)blockIdx.x;
-  const int rib = wave / wpr;               // row within the workgroup
-  const int part = wave - rib * wpr;        // wave within the row
-  const int64_t row = (int64_t)blk * a.rpb + rib;
-  const int D = a.D;
-  const int c0 = part * (NS * kStepCols);   // first column of this wave
-  const int rem_cols = (row < a.M) ? D - c0 : 0;
-  // Steps entirely inside the row, and steps with at least one valid lane.
-  const int nfull = rem_cols <= 0 ? 0 : (rem_cols >> 9 < NS ? rem_cols >> 9 : NS);
-  const int nvalid = rem_cols <= 0 ? 0 : ((rem_cols + kStepCols - 1) >> 9 < NS ? (rem_cols + kStepCols - 1) >> 9 : NS);
-  const int64_t e8row = row * (int64_t)(D >> 3) + (c0 >> 3) + lane;   // e8 index of step 0
-  const int g8 = (c0 >> 3) + lane;                                    // gamma u32x4 index
+  int rib, part;                            // row group within the workgroup, wave within the row
+  if (a.rpb == 1) {
+    rib = 0;
+    part = wave;
+  } else if (wpr == 1) {
+    rib = wave;
+    part = 0;
+  } else {
+    rib = wave / wpr;
+    part = wave - rib * wpr;
+  }
+  const int64_t row0 = ((int64_t)blk * a.rpb + rib) * RSEQ;
+  WaveCtx wc;
+  wc.lane = lane;
+  wc.c0 = part * (NS * kStepCols);
+  wc.cols = a.D > wc.c0 ? (uint32_t)(a.D - wc.c0) : 0u;
+  wc.gl = lane / LPG;
+  const uint32_t scale_voff =
+      (uint32_t)wc.gl * (a.col_major ? (uint32_t)(a.M * (int64_t)sb) : sb);
 
-  // Phase 1: issue every load of this wave's slice of the row.
+  // gamma for this wave's columns, once for all RSEQ rows.
+  u32x4 gv[NS];
+  {
+    const rsrc_t rg = make_rsrc(a.gamma + wc.c0, wc.cols * 2u);
+#pragma unroll
+    for (int k = 0; k < NS; ++k)
+      gv[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, lane * 16 + k * 1024, 0, 0);
+  }
+
   u32x4 xv[NS], rv[NS];
+  RowRsrc rr = row_rsrc<SF, NORM>(a, wc, row0, G);
+  load_row<NS>(rr, lane, xv, rv);
+
 #pragma unroll
-  for (int k = 0; k < NS; ++k) {
-    if (k < nfull) {
-      xv[k] = __builtin_nontemporal_load(a.x + e8row + k * 64);
-      rv[k] = __builtin_nontemporal_load(a.res + e8row + k * 64);
-    } else if (k < nvalid) {
-      xv[k] = (u32x4){0u, 0u, 0u, 0u};
-      rv[k] = (u32x4){0u, 0u, 0u, 0u};
-      if (c0 + k * kStepCols + lane * 8 < D) {
-        xv[k] = __builtin_nontemporal_load(a.x + e8row + k * 64);
-        rv[k] = __builtin_nontemporal_load(a.res + e8row + k * 64);
-      }
+  for (int i = 0; i < RSEQ; ++i) {
+    float w[NS][8];
+    uint32_t gmax[NS];
+    double ss = row_in<NS, LPG>(rr, lane, xv, rv, gv, w, gmax);
+    RowRsrc rn;
+    if (i + 1 < RSEQ) {
+      // The next row's inputs go out now, behind this row's reduction and stores.
+      rn = row_rsrc<SF, NORM>(a, wc, row0 + i + 1, G);
+      load_row<NS>(rn, lane, xv, rv);
     }
-  }
 
-  // Phase 2: r = x + residual, residual_out, sum of squares (fp64), w = r * gamma,
-  // per-group max |w|.
-  double ss = 0.0;
-  float w[NS][8];
-  uint32_t gmax[NS];
-#pragma unroll
-  for (int k = 0; k < NS; ++k) {
-    if (k < nvalid) {
-      const bool lane_ok = (k < nfull) || (c0 + k * kStepCols + lane * 8 < D);
-      u32x4 gv = (u32x4){0u, 0u, 0u, 0u};
-      if (lane_ok) gv = a.gamma[g8 + k * 64];
-      float r[8];
-      u32x4 ro;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        r[2 * j] = bf16_lo(xv[k][j]) + bf16_lo(rv[k][j]);
-        r[2 * j + 1] = bf16_hi(xv[k][j]) + bf16_hi(rv[k][j]);
-        ro[j] = pack_bf16x2(r[2 * j], r[2 * j + 1]);
-      }
-      if (lane_ok) __builtin_nontemporal_store(ro, a.res_out + e8row + k * 64);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const double rd = (double)r[j];
-        ss = __builtin_fma(rd, rd, ss);   // r^2 is exact in fp64
-      }
-      float m = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        w[k][2 * j] = r[2 * j] * bf16_lo(gv[j]);
-        w[k][2 * j + 1] = r[2 * j + 1] * bf16_hi(gv[j]);
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) m = __builtin_fmaxf(m, __builtin_fabsf(w[k][j]));
-      gmax[k] = group_max_bits<LPG>(__float_as_uint(m));
-    }
-  }
-
-  // Phase 3: row sum of squares -> inv_rms.
-  ss = wave_sum(ss);
-  if (wpr > 1) {
-    if (lane == 0) s_part[wave] = ss;
-    __syncthreads();
-    ss = 0.0;
-    for (int p = 0; p < wpr; ++p) ss += s_part[rib * wpr + p];
-  }
-  const float sumsq = (float)ss;
-  const float mean = sumsq / (float)D;
-  const float inv = (float)(1.0 / __builtin_sqrt((double)(mean + a.eps)));
-  const float inv_q = inv / QMAX;
-
-  // Phase 4: scales, codes, optional norm_out.
-#pragma unroll
-  for (int k = 0; k < NS; ++k) {
-    if (k < nvalid) {
-      const int col = c0 + k * kStepCols + lane * 8;
-      const bool lane_ok = (k < nfull) || (col < D);
-      const float s = __builtin_fmaxf(__uint_as_float(gmax[k]) * inv_q, 1.0e-12f);
-      float mul = 0.0f;
-      int e = 0;
-      if constexpr (SF == SF_F32) {
-        mul = 1.0f / s;
-      } else {
-        e = ceil_log2_bits(s);
-        e = e > 127 ? 127 : e;
-      }
-      float n[8], t[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        n[j] = w[k][j] * inv;
-        const float u = (SF == SF_F32) ? n[j] * mul : __builtin_ldexpf(n[j], -e);
-        t[j] = __builtin_fminf(__builtin_fmaxf(u, -QMAX), QMAX);
-      }
-      if (a.norm_out != nullptr) {
-        u32x4 no;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) no[j] = pack_bf16x2(n[2 * j], n[2 * j + 1]);
-        if (lane_ok) __builtin_nontemporal_store(no, a.norm_out + e8row + k * 64);
-      }
-      const u32x2 codes = encode8<QF>(t);
-      if (lane_ok) {
-        __builtin_nontemporal_store(codes, a.q + e8row + k * 64);
-        if ((lane & (LPG - 1)) == 0) {
-          const int g = col / G;
-          const int64_t si = a.col_major ? (int64_t)g * a.M + row : row * (int64_t)a.groups + g;
-          if constexpr (SF == SF_F32) {
-            static_cast<float*>(a.scale)[si] = s;
-          } else {
-            static_cast<uint8_t*>(a.scale)[si] = (uint8_t)(e + 127);
-          }
+    // Phase 3: row sum of squares -> inv_rms.  With several waves per row, the
+    // row's first wave adds the partial sums (in wave order) and evaluates
+    // inv_rms once; a second barrier hands it to the others.  Both barriers
+    // are fenced for LDS only, so no global store has to complete before them.
+    ss = wave_sum(ss);
+    float inv, inv_q;
+    if (wpr > 1) {
+      if (lane == 0) s_part[wave] = ss;
+      lds_barrier();
+      if (part == 0) {
+        double t = 0.0;
+        for (int p = 0; p < wpr; ++p) t += s_part[rib * wpr + p];
+        inv = row_inv_rms(t, a.D, a.eps);
+        inv_q = inv / QMAX;
+        if (lane == 0) {
+          s_inv[rib][0] = inv;
+          s_inv[rib][1] = inv_q;
         }
       }
+      lds_barrier();
+      inv = s_inv[rib][0];
+      inv_q = s_inv[rib][1];
+    } else {
+      inv = row_inv_rms(ss, a.D, a.eps);
+      inv_q = inv / QMAX;
     }
+
+    row_out<NS, LPG, QF, SF, NORM>(rr, lane, scale_voff, w, gmax, inv, inv_q);
+    if (i + 1 < RSEQ) rr = rn;
   }
 }
 

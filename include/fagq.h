@@ -115,8 +115,10 @@ FAGQ_API int fagq_launch(const void* x, const void* residual, const void* gamma,
 typedef struct fagq_route {
   int32_t waves_per_row;    /* waves that split one row (1 = wave-per-row) */
   int32_t steps_per_wave;   /* 512-column steps each wave keeps in VGPRs */
-  int32_t rows_per_block;   /* rows per workgroup */
+  int32_t rows_per_block;   /* row groups (of waves_per_row waves) per workgroup */
+  int32_t rows_in_sequence; /* consecutive rows each row group processes in turn */
   int32_t block_threads;    /* workgroup size */
+  int32_t reserved;         /* zero */
   int64_t grid_blocks;      /* workgroups launched */
 } fagq_route;
 

@@ -23,17 +23,19 @@ extern "C" {
  * waves_per_row in [1, 16], rows_per_block >= 1 with
  * waves_per_row * rows_per_block <= 16, steps per wave
  * ceil(ceil(D / 512) / waves_per_row) <= 16 and, when that exceeds 4,
- * waves_per_row * rows_per_block <= 4.  xcd_remap selects the XCD-aware
+ * waves_per_row * rows_per_block <= 4; rows_in_sequence in [1, 64] rows
+ * per row group, processed in turn.  xcd_remap selects the XCD-aware
  * workgroup order (0 or 1).  Returns FAGQ_E_FORMAT for an invalid mapping. */
 FAGQ_API int fagq_launch_mapped(const void* x, const void* residual, const void* gamma,
                                 void* residual_out, void* norm_out, void* q, void* scale,
                                 int64_t M, int64_t D, int64_t group_size, float eps,
                                 int q_format, int scale_format, int scale_layout,
                                 int rounding, int waves_per_row, int rows_per_block,
-                                int xcd_remap, void* stream);
+                                int rows_in_sequence, int xcd_remap, void* stream);
 
 /* Encodes n fp32 values (n % 8 == 0, 16-byte aligned) with the operator's
- * device encoder after its clamp to [-QMAX, QMAX]: one byte per value. */
+ * device encoder, after a clamp to [-QMAX, QMAX] (which the operator itself
+ * never needs: its values are within that range): one byte per value. */
 FAGQ_API int fagq_diag_encode(const float* in, void* out, int64_t n, int q_format,
                               int rounding, void* stream);
 

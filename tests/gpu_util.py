@@ -47,7 +47,7 @@ def to_numpy(ro, q, sc, norm, col):
 def run_gpu(pkg, dev, x, r, g, G, fmt, ue8m0=False, col=False, eps=1e-6, with_norm=False,
             mapping=None, inplace=False, stream=None):
     """Runs the library on cuda tensors copied from the CPU inputs.
-    mapping = (waves_per_row, rows_per_block, xcd_remap) forces a launch
+    mapping = (waves_per_row, rows_per_block, rows_in_sequence, xcd_remap) forces a launch
     mapping through fagq_launch_mapped; otherwise the public Python operator
     (reference signature) is used."""
     qdt, rnd, _, _ = FMTS[fmt]
@@ -64,14 +64,14 @@ def run_gpu(pkg, dev, x, r, g, G, fmt, ue8m0=False, col=False, eps=1e-6, with_no
                                               rounding=rnd if qdt == torch.int8 else None)
     else:
         from fagq_mi355x import _lib
-        wpr, rpb, remap = mapping
+        wpr, rpb, rseq, remap = mapping
         p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())
         st = pkg.load_library().fagq_launch_mapped(
             p(xd), p(rd), p(gd), p(ro), p(norm), p(q), p(sc), M, D, G, eps,
             _lib.Q_FP8_E4M3FN if qdt == torch.float8_e4m3fn else _lib.Q_INT8,
             _lib.SCALE_UE8M0 if ue8m0 else _lib.SCALE_F32,
             _lib.LAYOUT_COL_MAJOR if col else _lib.LAYOUT_ROW_MAJOR,
-            _lib.ROUND_RNE if rnd == "rne" else _lib.ROUND_TRUNC, wpr, rpb, remap,
+            _lib.ROUND_RNE if rnd == "rne" else _lib.ROUND_TRUNC, wpr, rpb, rseq, remap,
             ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
         _lib.check(st, "fagq_launch_mapped")
     torch.cuda.synchronize(dev)

@@ -51,17 +51,17 @@ SHAPES = [(M, D) for M in (1, 4, 16, 32, 100, 128, 512, 4096, 16384) for D in
 def test_route_invariants(pkg, M, D):
     r = pkg.route_for(M, D, 128)
     wpr, ns, rpb = r["waves_per_row"], r["steps_per_wave"], r["rows_per_block"]
+    rseq = r["rows_in_sequence"]
     steps = math.ceil(D / 512)
-    assert 1 <= wpr <= 16 and 1 <= ns <= 16 and rpb >= 1
+    assert 1 <= wpr <= 16 and 1 <= ns <= 4 and rpb >= 1 and rseq in (1, 2, 4)
     assert wpr * ns >= steps > (wpr - 1) * ns          # every wave owns >= 1 column
     assert r["block_threads"] == 64 * wpr * rpb <= 1024
-    if ns > 4:
-        assert r["block_threads"] <= 256
-    assert r["grid_blocks"] * rpb >= M > (r["grid_blocks"] - 1) * rpb
-    if M >= 2048 and D <= 8192:
-        assert wpr == 1                                  # prefill: one wave per row
-    if M <= 32 and D == 8192:
-        assert (wpr, ns) == (16, 1)                      # decode: row split over 16 waves
+    per_block = rpb * rseq
+    assert r["grid_blocks"] * per_block >= M > (r["grid_blocks"] - 1) * per_block
+    if M >= 1024 and 2 <= steps <= 16:
+        assert (ns, rseq) == (2, 1)                      # prefill: 2-step waves
+    if M <= 32 and D <= 8192:
+        assert (wpr, ns, rseq) == (steps, 1, 1)          # decode: one step per wave
 
 
 @pytest.mark.parametrize("args,status", [
@@ -120,15 +120,18 @@ def test_in_place_residual_is_accepted_by_validation(lib):
 
 
 def test_mapped_launch_rejects_bad_mappings(lib):
-    def mapped(wpr, rpb, remap=1, D=7168):
+    def mapped(wpr, rpb, remap=1, D=7168, rseq=1):
         return lib.fagq_launch_mapped(fake(0), fake(1), fake(2), fake(3), None, fake(4), fake(5),
-                                      8, D, 128, 1e-6, 1, 0, 0, 0, wpr, rpb, remap, None)
+                                      8, D, 128, 1e-6, 1, 0, 0, 0, wpr, rpb, rseq, remap, None)
     assert mapped(0, 1) == 5
     assert mapped(17, 1) == 5
     assert mapped(4, 5) == 5          # 20 waves > 16
-    assert mapped(1, 8) == 5          # 14 steps per wave needs <= 4 waves per block
-    assert mapped(1, 1, remap=2) == 5
-    assert mapped(1, 1, D=16384) == 5  # 32 steps in one wave
+    assert mapped(1, 1) == 5          # 14 steps in one wave (at most 4)
+    assert mapped(7, 1, remap=2) == 5
+    assert mapped(7, 1, D=65536) == 7  # D above FAGQ_MAX_D
+    assert mapped(7, 1, rseq=0) == 5
+    assert mapped(7, 1, rseq=3) == 5
+    assert mapped(7, 1, rseq=8) == 5
 
 
 def test_diag_validation(lib):

@@ -67,31 +67,48 @@ def test_format_matrix(pkg, gpu, G, fmt, ue8m0, col):
     assert st["exact"], st
 
 
-@pytest.mark.parametrize("D,G", [(7168, 128), (5120, 256), (4160, 64), (8192, 128)])
+@pytest.mark.parametrize("D,G", [(7168, 128), (5120, 256), (4160, 64), (8192, 128), (1536, 64)])
 def test_every_launch_mapping(pkg, gpu, D, G):
-    """Every legal (waves_per_row, rows_per_block, xcd_remap) gives identical outputs."""
+    """Every legal (waves_per_row, rows_per_block, rows_in_sequence, xcd_remap)
+    gives identical outputs, including row counts that leave the last row
+    groups and sequences partly empty."""
     M = 19
     x, r, w = inputs(M, D, seed=D)
     ref = None
     steps = math.ceil(D / 512)
     n = 0
     for wpr in range(1, 17):
-        ns = math.ceil(steps / wpr)
-        if ns > 16:
+        if math.ceil(steps / wpr) > 4:
             continue
         for rpb in (1, 2, 3, 4, 8, 16):
-            if wpr * rpb > 16 or (ns > 4 and wpr * rpb > 4):
+            if wpr * rpb > 16:
                 continue
-            for remap in (0, 1):
-                st, gpu_out = check(pkg, gpu, x, r, w, G, "fp8", col=True,
-                                    mapping=(wpr, rpb, remap), label=f"map wpr={wpr} rpb={rpb}")
+            for rseq in (1, 2, 4):
+                for remap in ((0, 1) if rseq == 1 else (0,)):
+                    st, gpu_out = check(pkg, gpu, x, r, w, G, "fp8", col=True,
+                                        mapping=(wpr, rpb, rseq, remap),
+                                        label=f"map wpr={wpr} rpb={rpb} rseq={rseq}")
+                    assert st["exact"], st
+                    if ref is None:
+                        ref = gpu_out
+                    for k in ref:
+                        assert np.array_equal(ref[k], gpu_out[k]), (wpr, rpb, rseq, remap, k)
+                    n += 1
+    assert n >= 20
+
+
+@pytest.mark.parametrize("rseq", [2, 4])
+@pytest.mark.parametrize("M", [37, 8])
+def test_rows_in_sequence_all_formats(pkg, gpu, rseq, M):
+    """Rows processed in turn by one row group (gamma reused, next row prefetched),
+    with M not a multiple of the rows per workgroup."""
+    x, r, w = inputs(M, 5120, seed=rseq, scale=3.0)
+    for fmt in ("fp8", "int8_rne", "int8_trunc"):
+        for ue in (False, True):
+            for wpr in (5, 10):
+                st, _ = check(pkg, gpu, x, r, w, 128, fmt, ue8m0=ue, col=ue, with_norm=True,
+                              mapping=(wpr, 1, rseq, 0), label=f"rseq={rseq} wpr={wpr}")
                 assert st["exact"], st
-                if ref is None:
-                    ref = gpu_out
-                for k in ref:
-                    assert np.array_equal(ref[k], gpu_out[k]), (wpr, rpb, remap, k)
-                n += 1
-    assert n > 20
 
 
 @pytest.mark.parametrize("M,D,G", [(1, 192, 64), (5, 640, 128), (130, 4160, 64), (3, 8448, 128),
