@@ -9,11 +9,14 @@ input/output sets that no step reads data left in L2/MALL by the previous
 one.
 
 Prints one JSON line:
-  value       whole-job achieved bandwidth, algorithmic bytes / wall time per step
+  value       whole-job achieved bandwidth: algorithmic bytes / (wall time of K
+              steps between device synchronisations / K)
   roofline    the kernel's algorithmic bytes / its average duration (HIP events
-              recorded on the launch stream around every timed launch), vs 8 TB/s;
-              traffic = measured HBM bytes per launch from the committed rocprofv3
-              counter summary for this workload (null if none)
+              recorded on the launch stream around each of K more launches), vs
+              8 TB/s; traffic = measured HBM bytes per launch from the committed
+              rocprofv3 counter summary for this workload (null if none)
+  us_per_call_graph_replay  device time per call of consecutive launches
+              captured in a HIP graph (workloads under 64 MB only)
   cpu_baseline  the eager-PyTorch CPU restatement timed on a bounded row sample
               of the same workload on the host cores (and checked against the
               GPU's rows)
@@ -133,22 +136,57 @@ def main() -> int:
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize(dev)
-
     stream = torch.cuda.current_stream(dev)
+
+    # Timed region: K steps between device synchronisations (no events inside,
+    # so nothing but the launches themselves runs between the kernels).
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize(dev)
+    t1 = time.perf_counter()
+    wall_ms = (t1 - t0) * 1e3 / args.steps
+
+    # Kernel duration: the same K steps again, each bracketed by HIP events
+    # recorded on the stream the kernel is launched on.
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    torch.cuda.synchronize(dev)
-    t0 = time.perf_counter()
     for i in range(args.steps):
         starts[i].record(stream)
         step(i)
         ends[i].record(stream)
     torch.cuda.synchronize(dev)
-    t1 = time.perf_counter()
-    wall_ms = (t1 - t0) * 1e3 / args.steps
     durs = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
     kern_ms = sum(durs) / len(durs)
     med_ms = durs[len(durs) // 2]
+
+    # Device time per call without host launch gaps: a HIP graph of
+    # consecutive launches, replayed (matters when a call is shorter than its
+    # Python + launch overhead, i.e. decode-sized batches).
+    graph_us = None
+    if set_bytes < (64 << 20):
+        per_graph = min(64, args.steps)
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            step(0)                                  # warm the side stream
+            torch.cuda.synchronize(dev)
+            with torch.cuda.graph(g, stream=side):
+                for i in range(per_graph):
+                    step(i)
+        torch.cuda.synchronize(dev)
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize(dev)
+        ge0, ge1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 20
+        ge0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        ge1.record(stream)
+        torch.cuda.synchronize(dev)
+        graph_us = ge0.elapsed_time(ge1) * 1e3 / (reps * per_graph)
 
     value = set_bytes / (wall_ms * 1e-3) / 1e9
     achieved = set_bytes / (kern_ms * 1e-3) / 1e9
@@ -183,6 +221,8 @@ def main() -> int:
                    "route": route},
         "us_per_call": round(kern_ms * 1e3, 2),
         "us_per_call_median": round(med_ms * 1e3, 2),
+        "us_per_call_host_wall": round(wall_ms * 1e3, 2),
+        "us_per_call_graph_replay": None if graph_us is None else round(graph_us, 2),
         "pct_of_peak": round(100.0 * achieved / PEAK_HBM_GBS, 2),
         "rows_per_s": round(w.M / (kern_ms * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,

@@ -64,15 +64,22 @@ int prefill_rseq() {
   return v;
 }
 
-// XCD-aware workgroup order: measured slower than dispatch order for this
-// streaming pattern, so off unless FAGQ_XCD_REMAP=1.
-int xcd_remap_default() {
-  static const int v = [] {
+// Workgroup -> row-tile order (see tile_of_block): column-major scales put
+// neighbouring rows' scale words next to each other, so chunks of 8 (fp32)
+// or 32 (ue8m0) consecutive row tiles go to one XCD and leave its L2 as full
+// 32-byte writes; otherwise dispatch order.  FAGQ_XCD_REMAP overrides.
+int remap_for(int scale_layout, int scale_format, int rpb) {
+  static const int forced = [] {
     const char* s = std::getenv("FAGQ_XCD_REMAP");
-    return s ? (std::atoi(s) != 0) : 0;
+    return s ? std::atoi(s) : -1;
   }();
-  return v;
+  if (forced >= 0) return forced;
+  if (scale_layout != FAGQ_LAYOUT_COL_MAJOR) return 0;
+  const int rows = scale_format == FAGQ_SCALE_F32 ? 8 : 32;
+  return rows / rpb > 1 ? rows / rpb : 0;
 }
+
+bool valid_remap(int r) { return r == 0 || r == 1 || (r >= 2 && r <= 64 && (r & (r - 1)) == 0); }
 
 int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
@@ -250,8 +257,8 @@ FAGQ_API int fagq_launch(const void* x, const void* residual, const void* gamma,
   Mapping m;
   choose_mapping(M, (int)D, &m);
   return launch_with(m, x, residual, gamma, residual_out, norm_out, q, scale, M, D, group_size,
-                     eps, q_format, scale_format, scale_layout, rounding, xcd_remap_default(),
-                     stream);
+                     eps, q_format, scale_format, scale_layout, rounding,
+                     remap_for(scale_layout, scale_format, m.rpb * m.rseq), stream);
 }
 
 FAGQ_API int fagq_launch_mapped(const void* x, const void* residual, const void* gamma,
@@ -266,7 +273,7 @@ FAGQ_API int fagq_launch_mapped(const void* x, const void* residual, const void*
   Mapping m;
   if (!finish_mapping(M, (int)D, waves_per_row, rows_per_block, rows_in_sequence, &m))
     return FAGQ_E_FORMAT;
-  if (xcd_remap != 0 && xcd_remap != 1) return FAGQ_E_FORMAT;
+  if (!valid_remap(xcd_remap)) return FAGQ_E_FORMAT;
   if (M == 0) return FAGQ_OK;
   return launch_with(m, x, residual, gamma, residual_out, norm_out, q, scale, M, D, group_size,
                      eps, q_format, scale_format, scale_layout, rounding, xcd_remap, stream);

@@ -68,7 +68,7 @@ struct KArgs {
   int32_t wpr;         // waves per row
   int32_t rpb;         // row groups per workgroup (each wpr waves)
   int32_t col_major;   // scale layout: 0 -> [M, groups], 1 -> [groups, M]
-  int32_t remap;       // 1 -> XCD-aware workgroup -> row-tile remap
+  int32_t remap;       // workgroup -> row-tile order, see tile_of_block
 };
 
 // ---------------------------------------------------------------- helpers
@@ -176,12 +176,26 @@ __device__ __forceinline__ float row_inv_rms(double ss, int D, float eps) {
   return (float)(1.0 / __builtin_sqrt((double)(mean + eps)));
 }
 
-// Blocks are dispatched round-robin over the 8 XCDs (block b -> XCD b % 8).
-// Give the blocks of one XCD consecutive row tiles so that neighbouring
-// rows' column-major scale words meet in the same L2.
-__device__ __forceinline__ int xcd_remap(int b, int nb) {
-  const int x = b & 7, i = b >> 3, per = nb >> 3, rem = nb & 7;
-  return x * per + (x < rem ? x : rem) + i;
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup b runs on
+// XCD b % 8), and each XCD has its own L2.  Row-tile order:
+//   remap 0: tile = b (dispatch order);
+//   remap 1: each XCD gets one contiguous range of tiles;
+//   remap n >= 2: in every chunk of 8 * n consecutive workgroups, XCD x gets
+//     the n consecutive tiles starting at x * n (a partial last chunk keeps
+//     dispatch order).  The tiles in flight stay one contiguous window, and
+//     n neighbouring rows' column-major scale words meet in one L2, so they
+//     leave it as one full 32-byte write instead of n partial ones.
+__device__ __forceinline__ int tile_of_block(int b, int nb, int remap) {
+  if (remap == 0) return b;
+  if (remap == 1) {
+    const int x = b & 7, i = b >> 3, per = nb >> 3, rem = nb & 7;
+    return x * per + (x < rem ? x : rem) + i;
+  }
+  const int chunk = 8 * remap;
+  const int c = b / chunk;
+  if ((c + 1) * chunk > nb) return b;
+  const int w = b - c * chunk;
+  return c * chunk + (w & 7) * remap + (w >> 3);
 }
 
 // ceil(log2(s)) for a positive normal fp32 s, exactly, from its bits.
@@ -373,7 +387,7 @@ fagq_rows(const KArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wpr = a.wpr;
-  const int blk = a.remap ? xcd_remap(blockIdx.x, gridDim.x) : (int)blockIdx.x;
+  const int blk = tile_of_block((int)blockIdx.x, (int)gridDim.x, a.remap);
   int rib, part;                            // row group within the workgroup, wave within the row
   if (a.rpb == 1) {
     rib = 0;

@@ -24,8 +24,10 @@ extern "C" {
  * waves_per_row * rows_per_block <= 16, steps per wave
  * ceil(ceil(D / 512) / waves_per_row) <= 16 and, when that exceeds 4,
  * waves_per_row * rows_per_block <= 4; rows_in_sequence in [1, 64] rows
- * per row group, processed in turn.  xcd_remap selects the XCD-aware
- * workgroup order (0 or 1).  Returns FAGQ_E_FORMAT for an invalid mapping. */
+ * per row group, processed in turn.  xcd_remap selects the workgroup ->
+ * row-tile order: 0 dispatch order, 1 one contiguous range of tiles per XCD,
+ * n in {2, 4, .., 64} chunks of n consecutive tiles per XCD.  Returns
+ * FAGQ_E_FORMAT for an invalid mapping. */
 FAGQ_API int fagq_launch_mapped(const void* x, const void* residual, const void* gamma,
                                 void* residual_out, void* norm_out, void* q, void* scale,
                                 int64_t M, int64_t D, int64_t group_size, float eps,

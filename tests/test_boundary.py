@@ -127,7 +127,8 @@ def test_mapped_launch_rejects_bad_mappings(lib):
     assert mapped(17, 1) == 5
     assert mapped(4, 5) == 5          # 20 waves > 16
     assert mapped(1, 1) == 5          # 14 steps in one wave (at most 4)
-    assert mapped(7, 1, remap=2) == 5
+    assert mapped(7, 1, remap=3) == 5
+    assert mapped(7, 1, remap=128) == 5
     assert mapped(7, 1, D=65536) == 7  # D above FAGQ_MAX_D
     assert mapped(7, 1, rseq=0) == 5
     assert mapped(7, 1, rseq=3) == 5

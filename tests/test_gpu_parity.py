@@ -84,7 +84,7 @@ def test_every_launch_mapping(pkg, gpu, D, G):
             if wpr * rpb > 16:
                 continue
             for rseq in (1, 2, 4):
-                for remap in ((0, 1) if rseq == 1 else (0,)):
+                for remap in ((0, 1, 2, 8) if rseq == 1 else (0, 4)):
                     st, gpu_out = check(pkg, gpu, x, r, w, G, "fp8", col=True,
                                         mapping=(wpr, rpb, rseq, remap),
                                         label=f"map wpr={wpr} rpb={rpb} rseq={rseq}")
