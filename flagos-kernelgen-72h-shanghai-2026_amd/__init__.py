@@ -8,14 +8,17 @@ registers it as ``fagq_mi355x``.
 """
 from . import _lib
 from ._lib import FagqError, load as load_library
+from .gemm import fp8_block_scaled_gemm, gemm_route
 from .ops import (empty_scales, fused_add_rmsnorm_group_quant, fused_add_rmsnorm_group_quant_fn,
                   route_for)
 
 __all__ = [
     "FagqError",
     "empty_scales",
+    "fp8_block_scaled_gemm",
     "fused_add_rmsnorm_group_quant",
     "fused_add_rmsnorm_group_quant_fn",
+    "gemm_route",
     "load_library",
     "route_for",
 ]

@@ -1,5 +1,5 @@
-"""ctypes binding of libfagq.so (the C ABI declared in include/fagq.h and
-include/fagq_diag.h).
+"""ctypes binding of libfagq.so (the C ABI declared in include/fagq.h,
+include/fagq_gemm.h and include/fagq_diag.h).
 
 The library is loaded after ``import torch`` so that its libamdhip64.so.7
 dependency resolves to the HIP runtime torch already loaded (same soname);
@@ -41,6 +41,12 @@ class Route(ctypes.Structure):
                 ("grid_blocks", ctypes.c_int64)]
 
 
+class GemmRoute(ctypes.Structure):
+    _fields_ = [("block_m", ctypes.c_int32), ("block_n", ctypes.c_int32),
+                ("block_threads", ctypes.c_int32), ("group_m", ctypes.c_int32),
+                ("grid_blocks", ctypes.c_int64)]
+
+
 SIGNATURES = {
     "fagq_launch": ([_P] * 7 + [_I64, _I64, _I64, _F, _I, _I, _I, _I, _P], _I),
     "fagq_launch_mapped": ([_P] * 7 + [_I64, _I64, _I64, _F, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
@@ -49,6 +55,8 @@ SIGNATURES = {
     "fagq_version": ([], _I),
     "fagq_diag_encode": ([_P, _P, _I64, _I, _I, _P], _I),
     "fagq_diag_copy": ([_P, _P, _I64, _P], _I),
+    "fagq_gemm_launch": ([_P] * 5 + [_I64, _I64, _I64, _I, _I, _I, _P], _I),
+    "fagq_gemm_query_route": ([_I64, _I64, _I64, ctypes.POINTER(GemmRoute)], _I),
 }
 
 

@@ -176,6 +176,8 @@ int validate(const void* x, const void* residual, const void* gamma, const void*
   return FAGQ_OK;
 }
 
+}  // namespace
+
 // gfx950 check, done once per device.
 int device_check() {
   static std::atomic<int> cache[kMaxDevices];   // 0 unknown, 1 gfx950, 2 other
@@ -193,6 +195,8 @@ int device_check() {
   }
   return c == 1 ? FAGQ_OK : FAGQ_E_DEVICE;
 }
+
+namespace {
 
 LaunchFn lookup(int q_format, int scale_format, int rounding, int lpg_idx, int steps, bool norm,
                 int rseq) {

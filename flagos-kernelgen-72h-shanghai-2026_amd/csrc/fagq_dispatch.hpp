@@ -21,6 +21,10 @@ constexpr int lpg_index(int group_size) {
 
 constexpr int rseq_index(int rseq) { return rseq == 1 ? 0 : rseq == 2 ? 1 : rseq == 4 ? 2 : -1; }
 
+// FAGQ_OK if the current device is gfx950 (cached per device), else
+// FAGQ_E_DEVICE or -hipError_t.
+int device_check();
+
 // lookup_q<code>_s<scale>(lpg index, steps per wave in [1, 4], norm, rseq index).
 LaunchFn lookup_q0_s0(int lpg_idx, int steps, bool norm, int rseq_idx);   // fp8, f32
 LaunchFn lookup_q0_s1(int lpg_idx, int steps, bool norm, int rseq_idx);   // fp8, ue8m0

@@ -1,0 +1,350 @@
+// fagq_gemm.hip - gfx950 fp8 block-scaled GEMM that consumes the quantizer's
+// codes and per-token 1 x 128 scales (C ABI: include/fagq_gemm.h).
+//
+//   C[m, n] = bf16( sum_kb fp32(sa(m, kb) * sb(n / 128, kb)) * P_kb[m, n] )
+//
+// No counterpart in the reference repository (its operator,
+// src/task01_fused_add_rmsnorm_group_quant.py:1731-1851, stops at the
+// quantized tensor and scales); this is the layer those formats feed.
+//
+// Work mapping.  A workgroup of 8 waves computes a 256 x 256 tile of C; wave
+// (wm, wn) owns rows 64 wm .. +64 and columns 128 wn .. +128, i.e. 4 x 8
+// tiles of 16 x 16, each one v_mfma_scale_f32_16x16x128_f8f6f4 per 128-deep
+// k-block.  The weight tile is the MFMA's first operand and the activation
+// tile its second, so each lane's four results are four consecutive columns
+// of one row of C (lane l: row l % 16, columns 4 (l / 16) .. +4) and the
+// activation scale a lane needs is that of its own row.
+//
+// Operand staging.  Per k-block, the 256 x 128-byte tiles of A and B go from
+// global memory straight into LDS (buffer_load_dwordx4 ... lds: each
+// instruction writes 1 KB, 16 bytes per lane, in lane order).  A lane fetches
+// 16-byte chunk (lane % 8) ^ (row % 8) of its row, so LDS holds each row with
+// its chunks XOR-swizzled by the row index: the MFMA operand reads (two
+// ds_read_b128 per lane, 16 consecutive rows at one chunk) then hit distinct
+// banks.  Two LDS stages (2 x 64 KB): the next k-block's copies are issued
+// before the current one is consumed.
+//
+// Scales.  fp32 (or mixed) scales: each k-block's 16 x 16 x 128 product goes
+// to a temporary and is added to the accumulator as t * (sa * sb) with fmaf.
+// Both UE8M0: the matrix core applies 2^(ea - 127) and 2^(eb - 127) itself
+// (the MFMA's per-lane E8M0 operands), which is exact, so the product
+// accumulates directly.
+//
+// Every global access goes through a buffer descriptor sized to the
+// workgroup's rows: rows of A or B past M or N read zeros and stores of rows
+// past M are dropped in hardware; column tiles past N are skipped (N % 16 ==
+// 0, so a 16-column tile is wholly inside or outside).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fagq.h"
+#include "fagq_dispatch.hpp"
+#include "fagq_gemm.h"
+
+namespace fagq {
+namespace gemm {
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+constexpr int kBM = 256;                 // rows of C per workgroup
+constexpr int kBN = 256;                 // columns of C per workgroup
+constexpr int kBK = 128;                 // k per block (one MFMA deep, one scale block)
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kTileBytes = 256 * kBK;    // one operand tile in LDS
+constexpr int kStageBytes = 2 * kTileBytes;
+constexpr int kTM = 4;                   // 16-row tiles per wave
+constexpr int kTN = 8;                   // 16-column tiles per wave
+constexpr int kGroupM = 4;               // row tiles per group of the tile order
+constexpr int kVmcnt0 = 0x0F70;          // s_waitcnt vmcnt(0) (other counters not waited)
+
+struct GArgs {
+  const uint8_t* a;       // fp8 [M, K]
+  const uint8_t* as;      // activation scales
+  const uint8_t* b;       // fp8 [N, K]
+  const uint8_t* bs;      // weight scales [ceil(N / 128), K / 128]
+  uint16_t* c;            // bf16 [M, N]
+  int32_t M, N, K;
+  int32_t kblocks;        // K / 128
+  int32_t as_kstride;     // elements between the scales of consecutive k-blocks of one row
+  int32_t as_mstride;     // elements between the scales of consecutive rows
+  int32_t m_tiles, n_tiles;
+  uint32_t as_bytes, bs_bytes;
+};
+
+// Workgroup b runs on XCD b % 8.  XCD x takes one contiguous range of the
+// tile order, and the order walks kGroupM row tiles at a time column by
+// column, so the tiles an XCD has in flight share a few row and column
+// panels in its L2.
+__device__ __forceinline__ void tile_coords(int b, int m_tiles, int n_tiles, int& mt, int& nt) {
+  const int T = m_tiles * n_tiles;
+  const int x = b & 7, i = b >> 3, per = T >> 3, rem = T & 7;
+  const int t = x * per + (x < rem ? x : rem) + i;
+  const int group = t / (kGroupM * n_tiles);
+  const int first_m = group * kGroupM;
+  const int gm = m_tiles - first_m < kGroupM ? m_tiles - first_m : kGroupM;
+  const int w = t - group * kGroupM * n_tiles;
+  mt = first_m + w % gm;
+  nt = w / gm;
+}
+
+// One 16 x 128-byte MFMA operand: lane l gets row (r0 + l % 16), k bytes
+// 32 (l / 16) .. +32, from a swizzled LDS tile.
+__device__ __forceinline__ i32x8 lds_frag(const uint8_t* tile, int row, int lane) {
+  const int c0 = (lane >> 4) * 2;
+  const int sw = row & 7;
+  const uint8_t* r = tile + row * kBK;
+  const i32x4 lo = *reinterpret_cast<const i32x4*>(r + ((c0 ^ sw) << 4));
+  const i32x4 hi = *reinterpret_cast<const i32x4*>(r + (((c0 + 1) ^ sw) << 4));
+  return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+__device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
+  // 2^(e - 127); e = 0 is the subnormal 2^-127 (e = 255, NaN, never produced).
+  return e ? __uint_as_float(e << 23) : __uint_as_float(0x00400000u);
+}
+
+template <int ASF, int BSF>
+__global__ void __launch_bounds__(kThreads, 1) fagq_gemm_kernel(const GArgs g) {
+  constexpr bool kHwScale = ASF == SF_UE8M0 && BSF == SF_UE8M0;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStageBytes];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave & 3, wn = wave >> 2;
+  int mt, nt;
+  tile_coords((int)blockIdx.x, g.m_tiles, g.n_tiles, mt, nt);
+  const int m0 = mt * kBM, n0 = nt * kBN;
+  const int mrows = g.M - m0 < kBM ? g.M - m0 : kBM;
+  const int nrows = g.N - n0 < kBN ? g.N - n0 : kBN;
+  const rsrc_t ra = make_rsrc(g.a + (int64_t)m0 * g.K, (uint32_t)mrows * (uint32_t)g.K);
+  const rsrc_t rb = make_rsrc(g.b + (int64_t)n0 * g.K, (uint32_t)nrows * (uint32_t)g.K);
+  const rsrc_t ras = make_rsrc(g.as, g.as_bytes);
+  const rsrc_t rbs = make_rsrc(g.bs, g.bs_bytes);
+
+  // Copy geometry: instruction u of this wave fills LDS rows (4 wave + u) * 8
+  // .. +8; the lane's row within them is lane / 8 and its chunk is swizzled.
+  // The whole offset goes in the VGPR offset and the scalar offset is zero:
+  // the hardware range-checks only the VGPR offset (plus the immediate), so
+  // this is what turns rows past M or N into zero reads.  The lane part is
+  // kept in one VGPR and the uniform part added per instruction.
+  const int crow = lane >> 3;
+  const uint32_t cvoff = (uint32_t)crow * (uint32_t)g.K + (uint32_t)((lane & 7) ^ crow) * 16u;
+
+  auto issue = [&](int kb, int stage) {
+    uint8_t* sa_tile = lds + stage * kStageBytes;
+    uint8_t* sb_tile = sa_tile + kTileBytes;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int inst = wave * 4 + u;
+      const uint32_t off = cvoff + (uint32_t)__builtin_amdgcn_readfirstlane(inst * 8 * g.K + kb * kBK);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(sa_tile + inst * 1024), 16, off,
+                                               0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(sb_tile + inst * 1024), 16, off,
+                                               0, 0, 0);
+    }
+  };
+
+  // Scales of this lane's rows (m0 + 64 wm + 16 i + lane % 16) and of the
+  // wave's 128-column weight block (n0 / 128 + wn) for k-block kb, as loaded
+  // bits: they are converted only after the barrier that ends the k-block,
+  // so no wait for them (and, the counter being in order, for the LDS copies
+  // issued before them) lands inside the MFMA loop.
+  const int arow = m0 + wm * 64 + (lane & 15);
+  const int wblk = (n0 >> 7) + wn;
+  struct Scales {
+    uint32_t a[kTM], b;
+  };
+  // Offsets as for the copies: all in the range-checked VGPR offset, so scale
+  // reads for rows past M or weight blocks past N fall outside the arrays'
+  // descriptors and read zeros.
+  constexpr uint32_t asb = ASF == SF_F32 ? 4u : 1u, bsb = BSF == SF_F32 ? 4u : 1u;
+  const uint32_t a_voff = (uint32_t)arow * (uint32_t)g.as_mstride * asb;   // lane part
+  auto load_scales = [&](int kb) {
+    Scales sc;
+    const uint32_t boff = (uint32_t)__builtin_amdgcn_readfirstlane((wblk * g.kblocks + kb) * (int)bsb);
+    sc.b = BSF == SF_F32 ? __builtin_amdgcn_raw_buffer_load_b32(rbs, boff, 0, 0)
+                         : (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rbs, boff, 0, 0);
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+      const uint32_t off = a_voff + (uint32_t)__builtin_amdgcn_readfirstlane(
+                                        (kb * g.as_kstride + 16 * i * g.as_mstride) * (int)asb);
+      sc.a[i] = ASF == SF_F32 ? __builtin_amdgcn_raw_buffer_load_b32(ras, off, 0, 0)
+                              : (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(ras, off, 0, 0);
+    }
+    return sc;
+  };
+  auto to_f32 = [](uint32_t bits, bool e8m0) { return e8m0 ? e8m0_to_f32(bits) : __uint_as_float(bits); };
+
+  f32x4 acc[kTN][kTM];
+#pragma unroll
+  for (int j = 0; j < kTN; ++j)
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) acc[j][i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  issue(0, 0);
+  Scales cur = load_scales(0);
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);
+  __syncthreads();
+
+  for (int kb = 0; kb < g.kblocks; ++kb) {
+    const int stage = kb & 1;
+    Scales nxt = cur;
+    if (kb + 1 < g.kblocks) {
+      issue(kb + 1, stage ^ 1);
+      nxt = load_scales(kb + 1);
+    }
+    float smul[kTM];
+    if constexpr (!kHwScale) {
+      const float sb = to_f32(cur.b, BSF == SF_UE8M0);
+#pragma unroll
+      for (int i = 0; i < kTM; ++i) smul[i] = to_f32(cur.a[i], ASF == SF_UE8M0) * sb;
+    }
+    const uint8_t* ta = lds + stage * kStageBytes;
+    const uint8_t* tb = ta + kTileBytes;
+    i32x8 af[kTM];
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) af[i] = lds_frag(ta, wm * 64 + 16 * i + (lane & 15), lane);
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+      const i32x8 bf = lds_frag(tb, wn * 128 + 16 * j + (lane & 15), lane);
+#pragma unroll
+      for (int i = 0; i < kTM; ++i) {
+        if constexpr (kHwScale) {
+          acc[j][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              bf, af[i], acc[j][i], 0, 0, 0, (int)cur.b, 0, (int)cur.a[i]);
+        } else {
+          const f32x4 t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              bf, af[i], f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 127, 0, 127);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[j][i][r] = __builtin_fmaf(t[r], smul[i], acc[j][i][r]);
+        }
+      }
+    }
+    cur = nxt;
+    // The next stage's copies have landed (each wave waits for its own) and
+    // every wave is done reading this stage before it is refilled.
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    __syncthreads();
+  }
+
+  const rsrc_t rc = make_rsrc(g.c + (int64_t)m0 * g.N, (uint32_t)mrows * (uint32_t)g.N * 2u);
+#pragma unroll
+  for (int j = 0; j < kTN; ++j) {
+    const int ncol = n0 + wn * 128 + 16 * j;
+    if (ncol >= g.N) continue;   // uniform over the wave
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+      const uint32_t row = (uint32_t)(wm * 64 + 16 * i + (lane & 15));
+      u32x2 v;
+      v[0] = pack_bf16x2(acc[j][i][0], acc[j][i][1]);
+      v[1] = pack_bf16x2(acc[j][i][2], acc[j][i][3]);
+      const uint32_t off = (row * (uint32_t)g.N + (uint32_t)(ncol + 4 * (lane >> 4))) * 2u;
+      __builtin_amdgcn_raw_buffer_store_b64(v, rc, off, 0, 0);
+    }
+  }
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+bool overlap(const void* a, int64_t na, const void* b, int64_t nb) {
+  const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+  return a0 < b0 + (uintptr_t)nb && b0 < a0 + (uintptr_t)na;
+}
+
+int validate(const void* a_q, const void* a_scale, const void* b_q, const void* b_scale,
+             const void* c, int64_t M, int64_t N, int64_t K, int asf, int asl, int bsf) {
+  if (!a_q || !a_scale || !b_q || !b_scale || !c) return FAGQ_E_NULL;
+  if ((asf != FAGQ_SCALE_F32 && asf != FAGQ_SCALE_UE8M0) ||
+      (bsf != FAGQ_SCALE_F32 && bsf != FAGQ_SCALE_UE8M0) ||
+      (asl != FAGQ_LAYOUT_ROW_MAJOR && asl != FAGQ_LAYOUT_COL_MAJOR))
+    return FAGQ_E_FORMAT;
+  if (M < 0 || N <= 0 || K <= 0 || N % 16 != 0 || K % kBK != 0) return FAGQ_E_SHAPE;
+  const int64_t kb = K / kBK;
+  const int64_t asb = asf == FAGQ_SCALE_F32 ? 4 : 1, bsb = bsf == FAGQ_SCALE_F32 ? 4 : 1;
+  // 32-bit buffer offsets: one workgroup's rows of A, B and C, and each scale array.
+  if (M > INT32_MAX || (int64_t)kBM * K > (int64_t)UINT32_MAX ||
+      (int64_t)kBN * K > (int64_t)UINT32_MAX || (int64_t)kBM * N * 2 > (int64_t)UINT32_MAX ||
+      M * kb * asb > (int64_t)UINT32_MAX || ceil_div(N, 128) * kb * bsb > (int64_t)UINT32_MAX ||
+      ceil_div(M, kBM) * ceil_div(N, kBN) > INT32_MAX)
+    return FAGQ_E_TOO_LARGE;
+  if (!aligned(a_q, 16) || !aligned(b_q, 16) || !aligned(c, 16) ||
+      (asf == FAGQ_SCALE_F32 && !aligned(a_scale, 4)) ||
+      (bsf == FAGQ_SCALE_F32 && !aligned(b_scale, 4)))
+    return FAGQ_E_ALIGN;
+  if (M == 0) return FAGQ_OK;
+  const int64_t cb = M * N * 2;
+  if (overlap(c, cb, a_q, M * K) || overlap(c, cb, b_q, N * K) ||
+      overlap(c, cb, a_scale, M * kb * asb) || overlap(c, cb, b_scale, ceil_div(N, 128) * kb * bsb))
+    return FAGQ_E_ALIAS;
+  return FAGQ_OK;
+}
+
+const void* kernel_for(int asf, int bsf) {
+  const bool au = asf == FAGQ_SCALE_UE8M0, bu = bsf == FAGQ_SCALE_UE8M0;
+  if (au && bu) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_UE8M0, SF_UE8M0>);
+  if (au) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_UE8M0, SF_F32>);
+  if (bu) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_F32, SF_UE8M0>);
+  return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_F32, SF_F32>);
+}
+
+}  // namespace
+}  // namespace gemm
+}  // namespace fagq
+
+using namespace fagq;
+using namespace fagq::gemm;
+
+extern "C" {
+
+FAGQ_API int fagq_gemm_launch(const void* a_q, const void* a_scale, const void* b_q,
+                              const void* b_scale, void* c, int64_t M, int64_t N, int64_t K,
+                              int a_scale_format, int a_scale_layout, int b_scale_format,
+                              void* stream) {
+  const int v = validate(a_q, a_scale, b_q, b_scale, c, M, N, K, a_scale_format, a_scale_layout,
+                         b_scale_format);
+  if (v != FAGQ_OK || M == 0) return v;
+  const int dc = device_check();
+  if (dc != FAGQ_OK) return dc;
+  GArgs g;
+  g.a = static_cast<const uint8_t*>(a_q);
+  g.as = static_cast<const uint8_t*>(a_scale);
+  g.b = static_cast<const uint8_t*>(b_q);
+  g.bs = static_cast<const uint8_t*>(b_scale);
+  g.c = static_cast<uint16_t*>(c);
+  g.M = (int32_t)M;
+  g.N = (int32_t)N;
+  g.K = (int32_t)K;
+  g.kblocks = (int32_t)(K / kBK);
+  const bool col = a_scale_layout == FAGQ_LAYOUT_COL_MAJOR;
+  g.as_kstride = col ? (int32_t)M : 1;
+  g.as_mstride = col ? 1 : g.kblocks;
+  g.m_tiles = (int32_t)ceil_div(M, kBM);
+  g.n_tiles = (int32_t)ceil_div(N, kBN);
+  g.as_bytes = (uint32_t)(M * g.kblocks * (a_scale_format == FAGQ_SCALE_F32 ? 4 : 1));
+  g.bs_bytes = (uint32_t)(ceil_div(N, 128) * g.kblocks * (b_scale_format == FAGQ_SCALE_F32 ? 4 : 1));
+  void* args[] = {&g};
+  const hipError_t e = hipLaunchKernel(kernel_for(a_scale_format, b_scale_format),
+                                       dim3((unsigned)(g.m_tiles * g.n_tiles)), dim3(kThreads),
+                                       args, 0, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? FAGQ_OK : -(int)e;
+}
+
+FAGQ_API int fagq_gemm_query_route(int64_t M, int64_t N, int64_t K, fagq_gemm_route* route) {
+  if (!route) return FAGQ_E_NULL;
+  if (M < 0 || N <= 0 || K <= 0 || N % 16 != 0 || K % kBK != 0) return FAGQ_E_SHAPE;
+  route->block_m = kBM;
+  route->block_n = kBN;
+  route->block_threads = kThreads;
+  route->group_m = kGroupM;
+  route->grid_blocks = ceil_div(M, kBM) * ceil_div(N, kBN);
+  return FAGQ_OK;
+}
+
+}  // extern "C"

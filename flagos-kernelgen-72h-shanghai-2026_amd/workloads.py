@@ -87,3 +87,63 @@ def make_inputs(w: Workload, M: int | None = None):
         x[:, ch] *= 50.0
         res[:, ch] *= 50.0
     return x.to(torch.bfloat16), res.to(torch.bfloat16), weight.to(torch.bfloat16)
+
+
+# ------------------------------------------------------------- GEMM consumer
+
+@dataclass(frozen=True)
+class GemmWorkload:
+    """The fp8 block-scaled GEMM fed by the quantizer: A [M, K] fp8 codes with 1 x 128
+    scales (column-major [K/128, M] physical), B [N, K] fp8 with 128 x 128 block scales."""
+    name: str
+    M: int
+    N: int
+    K: int
+    a_scale: str = "f32"       # "f32" | "ue8m0"
+    b_scale: str = "f32"
+    seed: int = 0
+
+    def flops(self) -> int:
+        return 2 * self.M * self.N * self.K
+
+    def min_bytes(self) -> int:
+        """Bytes that must cross HBM at least once: A, B, their scales, C (bf16)."""
+        sa = 4 if self.a_scale == "f32" else 1
+        sb = 4 if self.b_scale == "f32" else 1
+        kb = self.K // 128
+        return (self.M * self.K + self.N * self.K + sa * self.M * kb
+                + sb * ((self.N + 127) // 128) * kb + 2 * self.M * self.N)
+
+
+# DeepSeek-V3 shapes whose input is the headline quantizer's output (16384 tokens, hidden
+# 7168): an expert / shared-expert gate+up projection (N = 2 x 2048) with fp32 or UE8M0
+# scales, and the fused q_a + kv_a projection (N = 1536 + 576).
+GEMM_CONFIGS = {
+    "gemm_dsv3_16384x4096x7168": GemmWorkload("gemm_dsv3_16384x4096x7168", 16384, 4096, 7168),
+    "gemm_dsv3_ue8m0_16384x4096x7168": GemmWorkload("gemm_dsv3_ue8m0_16384x4096x7168", 16384,
+                                                    4096, 7168, "ue8m0", "ue8m0"),
+    "gemm_qkva_16384x2112x7168": GemmWorkload("gemm_qkva_16384x2112x7168", 16384, 2112, 7168),
+}
+
+
+def make_gemm_inputs(w: GemmWorkload, M: int | None = None):
+    """(a_q, a_scale, b_q, b_scale) CPU tensors: fp8 codes spread over the e4m3fn range
+    (normal, sigma 56, clamped to +-448), scales exp(U(-12, 2)) (fp32) or biased
+    exponents in [100, 140) (UE8M0).  a_scale is the physical [K/128, M] array."""
+    M = w.M if M is None else M
+    g = torch.Generator(device="cpu").manual_seed(w.seed)
+    kb, nb = w.K // 128, (w.N + 127) // 128
+
+    def codes(shape):
+        return (torch.randn(shape, generator=g) * 56.0).clamp_(-448.0, 448.0).to(torch.float8_e4m3fn)
+
+    def scales(shape, fmt):
+        if fmt == "f32":
+            return torch.exp(torch.empty(shape).uniform_(-12.0, 2.0, generator=g))
+        return torch.randint(100, 140, shape, generator=g, dtype=torch.uint8)
+
+    a_q = codes((M, w.K))
+    b_q = codes((w.N, w.K))
+    a_s = scales((kb, M), w.a_scale)
+    b_s = scales((nb, kb), w.b_scale)
+    return a_q, a_s, b_q, b_s

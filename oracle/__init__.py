@@ -13,6 +13,9 @@ src/task01_fused_add_rmsnorm_group_quant.py:65-121 and :1066-1348):
   called through ctypes on numpy arrays.  This is the parity reference.
 * ``torch_eager.fagq_torch`` - the same formulas as eager PyTorch CPU ops,
   the "CPU PyTorch path" that the benchmark times as its CPU baseline.
+* ``gemm`` - gemm_oracle.c, the fp8 block-scaled GEMM that consumes the
+  operator's codes and scales (no reference counterpart; its definition is
+  in include/fagq_gemm.h).
 
 bf16 tensors are passed as their uint16 bit patterns.
 """
@@ -52,6 +55,10 @@ def lib() -> ctypes.CDLL:
         L.orc_ceil_log2.restype = None
         L.orc_fagq.argtypes = [P, P, P, P, P, P, P, I64, I64, I64, F, I, I, I, I, I]
         L.orc_fagq.restype = I
+        L.orc_e4m3fn_to_f64.argtypes = [P, P, I64]
+        L.orc_e4m3fn_to_f64.restype = None
+        L.orc_gemm.argtypes = [P, P, P, P, P, P, I64, I64, I64, I, I, I, I]
+        L.orc_gemm.restype = I
         _lib = L
     return _lib
 
@@ -121,3 +128,40 @@ def fagq(x: np.ndarray, residual: np.ndarray, gamma: np.ndarray, eps: float, gro
     if with_norm:
         out["norm_out"] = norm_out
     return out
+
+
+def e4m3fn_to_f64(b: np.ndarray) -> np.ndarray:
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    out = np.empty(b.shape, np.float64)
+    lib().orc_e4m3fn_to_f64(_ptr(b), _ptr(out), b.size)
+    return out
+
+
+def gemm(a_q: np.ndarray, a_scale: np.ndarray, b_q: np.ndarray, b_scale: np.ndarray,
+         a_layout: int = L_COL, nthreads: int = 0) -> tuple[np.ndarray, np.ndarray]:
+    """The block-scaled GEMM in double.  a_q [M, K], b_q [N, K]: uint8 fp8 bits;
+    a_scale: float32 or uint8 (UE8M0), physical [K/128, M] (a_layout L_COL) or
+    [M, K/128]; b_scale: float32 or uint8 [ceil(N/128), K/128].  Returns (C,
+    bound): C[m, n] and sum_kb |s| sum_k |A B|, both float64 [M, N]."""
+    a_q = np.ascontiguousarray(a_q, dtype=np.uint8)
+    b_q = np.ascontiguousarray(b_q, dtype=np.uint8)
+    a_scale = np.ascontiguousarray(a_scale)
+    b_scale = np.ascontiguousarray(b_scale)
+    M, K = a_q.shape
+    N = b_q.shape[0]
+    kb = K // 128
+    nb = (N + 127) // 128
+    assert b_q.shape[1] == K and K % 128 == 0
+    assert a_scale.shape == ((kb, M) if a_layout == L_COL else (M, kb))
+    assert b_scale.shape == (nb, kb)
+    fmt = lambda s: S_F32 if s.dtype == np.float32 else S_UE8M0
+    assert a_scale.dtype in (np.float32, np.uint8) and b_scale.dtype in (np.float32, np.uint8)
+    c = np.empty((M, N), np.float64)
+    bound = np.empty((M, N), np.float64)
+    import os
+    st = lib().orc_gemm(_ptr(a_q), _ptr(a_scale), _ptr(b_q), _ptr(b_scale), _ptr(c), _ptr(bound),
+                        M, N, K, fmt(a_scale), a_layout, fmt(b_scale),
+                        nthreads or min(8, os.cpu_count() or 1))
+    if st != 0:
+        raise ValueError(f"oracle rejected the arguments (status {st})")
+    return c, bound

@@ -1,4 +1,6 @@
-"""Builds the C oracle (test infrastructure) into oracle/libfagq_oracle.so.
+"""Builds the C oracle (test infrastructure) into oracle/libfagq_oracle.so:
+fagq_oracle.c (the operator) and gemm_oracle.c (the fp8 block-scaled GEMM
+that consumes the operator's output).
 
 The oracle restates the reference's algorithm on the CPU and is used only as
 the checker by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
@@ -12,7 +14,7 @@ import subprocess
 from pathlib import Path
 
 ORACLE_DIR = Path(__file__).resolve().parent
-SRC = ORACLE_DIR / "fagq_oracle.c"
+SRCS = [ORACLE_DIR / "fagq_oracle.c", ORACLE_DIR / "gemm_oracle.c"]
 LIB = ORACLE_DIR / "libfagq_oracle.so"
 
 CFLAGS = ["-O2", "-std=gnu11", "-fPIC", "-shared", "-fopenmp", "-ffp-contract=off",
@@ -21,7 +23,7 @@ CFLAGS = ["-O2", "-std=gnu11", "-fPIC", "-shared", "-fopenmp", "-ffp-contract=of
 
 def build(verbose: bool = False) -> Path:
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = ["gcc", *CFLAGS, "-o", str(tmp), str(SRC), "-lm"]
+    cmd = ["gcc", *CFLAGS, "-o", str(tmp), *[str(s) for s in SRCS], "-lm"]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)

@@ -195,3 +195,55 @@ def test_status_errors_name_the_code(pkg):
     with pytest.raises(_lib.FagqError):
         _lib.check(3)
     _lib.check(0)
+
+
+# ----------------------------------------------------------------- GEMM consumer
+
+def gemm_call(lib, **kw):
+    a = dict(a=fake(0), sa=fake(1), b=fake(2), sb=fake(3), c=fake(4), M=256, N=256, K=1024,
+             asf=0, asl=1, bsf=0)
+    a.update(kw)
+    return lib.fagq_gemm_launch(a["a"], a["sa"], a["b"], a["sb"], a["c"], a["M"], a["N"], a["K"],
+                                a["asf"], a["asl"], a["bsf"], None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(a=None), 1), (dict(sa=None), 1), (dict(b=None), 1), (dict(sb=None), 1), (dict(c=None), 1),
+    (dict(asf=2), 5), (dict(bsf=-1), 5), (dict(asl=2), 5),
+    (dict(K=1000), 2), (dict(K=0), 2), (dict(N=100), 2), (dict(N=0), 2), (dict(M=-1), 2),
+    (dict(K=1 << 24), 7), (dict(N=1 << 23), 7),
+    (dict(a=ctypes.c_void_p(BASE + 8)), 4), (dict(c=ctypes.c_void_p(BASE + 0x4_0000_0008)), 4),
+    (dict(sa=ctypes.c_void_p(BASE + 0x1_0000_0002)), 4),
+    (dict(c=fake(0)), 9), (dict(c=fake(3)), 9),
+    (dict(M=0), 0),
+])
+def test_gemm_validation(lib, kw, status):
+    assert gemm_call(lib, **kw) == status
+
+
+def test_gemm_ue8m0_scales_need_no_alignment(lib):
+    # M = 0 so that nothing is launched after validation.
+    odd = ctypes.c_void_p(BASE + 0x1_0000_0003)
+    assert gemm_call(lib, sa=odd, asf=1, M=0) == 0
+    assert gemm_call(lib, sa=odd, asf=0, M=0) == 4
+
+
+def test_gemm_route(pkg):
+    r = pkg.gemm_route(16384, 4096, 7168)
+    assert (r["block_m"], r["block_n"], r["block_threads"]) == (256, 256, 512)
+    assert r["grid_blocks"] == 64 * 16
+    assert pkg.gemm_route(1, 16, 128)["grid_blocks"] == 1
+    with pytest.raises(pkg.FagqError):
+        pkg.gemm_route(16, 16, 100)
+
+
+def test_gemm_workloads():
+    from fagq_mi355x.workloads import GEMM_CONFIGS, GemmWorkload, make_gemm_inputs
+    w = GemmWorkload("t", 300, 272, 512, "f32", "ue8m0", seed=3)
+    a_q, a_s, b_q, b_s = make_gemm_inputs(w)
+    assert a_q.shape == (300, 512) and a_q.dtype == torch.float8_e4m3fn
+    assert a_s.shape == (4, 300) and a_s.dtype == torch.float32
+    assert b_q.shape == (272, 512) and b_s.shape == (3, 4) and b_s.dtype == torch.uint8
+    again = make_gemm_inputs(w)
+    assert torch.equal(again[0].view(torch.uint8), a_q.view(torch.uint8))
+    assert GEMM_CONFIGS["gemm_dsv3_16384x4096x7168"].flops() == 2 * 16384 * 4096 * 7168
