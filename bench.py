@@ -21,6 +21,11 @@ Prints one JSON line:
               of the same workload on the host cores (and checked against the
               GPU's rows)
 
+--config gemm_*: the fp8 block-scaled GEMM that consumes the operator's
+output (fagq_gemm_launch); value and roofline in TFLOP/s against MI355X's
+5.0 PFLOP/s dense fp8 peak, cpu_baseline = the C oracle (oracle/gemm_oracle.c)
+on a row sample.
+
 Usage: python bench.py [--steps K] [--warmup W] [--config NAME] [--gpus 1]
 """
 from __future__ import annotations
@@ -35,6 +40,7 @@ from pathlib import Path
 
 REPO_DIR = Path(__file__).resolve().parent
 PEAK_HBM_GBS = 8000.0
+PEAK_FP8_TFLOPS = 5000.0   # MI355X dense fp8 MFMA
 METRIC = "achieved HBM GB/s (% of 8 TB/s peak) + µs/call, 16384×7168 bf16→fp8 g128"
 ROTATE_BYTES = 1 << 30     # rotate buffer sets until > 1 GiB (4x the 256 MB MALL)
 
@@ -108,6 +114,9 @@ def main() -> int:
     if args.copy:
         return copy_bench(args, torch, pkg)
     name = args.config or HEADLINE
+    from fagq_mi355x.workloads import GEMM_CONFIGS
+    if name in GEMM_CONFIGS:
+        return gemm_bench(args, torch, pkg, GEMM_CONFIGS[name])
     w = CONFIGS[name]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -286,6 +295,120 @@ def cpu_baseline(w, x, res, gamma, gpu_set, args, torch) -> dict:
             "sample": f"first {rows} of {w.M} rows of {w.name}, eager PyTorch CPU "
                       f"restatement (oracle/torch_eager.py), median of {len(times)} runs",
             "parity_vs_gpu_rows": parity}
+
+
+def gemm_bench(args, torch, pkg, w) -> int:
+    """Times fagq_gemm_launch on a GEMM workload (inputs resident in HBM, sets
+    rotated past the MALL), kernel time by HIP events on the launch stream."""
+    from fagq_mi355x.workloads import make_gemm_inputs
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    a_q, a_s, b_q, b_s = make_gemm_inputs(w)
+    set_bytes = w.min_bytes()
+    nsets = max(2, min(8, math.ceil(ROTATE_BYTES / set_bytes) + 1))
+    A, SA, B, SB = a_q.to(dev), a_s.to(dev), b_q.to(dev), b_s.to(dev)
+    sets = []
+    for i in range(nsets):
+        c = torch.empty(w.M, w.N, dtype=torch.bfloat16, device=dev)
+        if i == 0:
+            sets.append((A, SA.t(), B, SB, c))
+        else:
+            sets.append((A.clone(), SA.clone().t(), B.clone(), SB.clone(), c))
+
+    def step(i: int):
+        a, sa, b, sb, c = sets[i % nsets]
+        pkg.fp8_block_scaled_gemm(a, sa, b, sb, out=c)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize(dev)
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    for i in range(args.steps):
+        starts[i].record(stream)
+        step(i)
+        ends[i].record(stream)
+    torch.cuda.synchronize(dev)
+    durs = sorted(st.elapsed_time(en) for st, en in zip(starts, ends))
+    kern_ms = sum(durs) / len(durs)
+    flops = w.flops()
+    value = flops / (wall_ms * 1e-3) / 1e12
+    achieved = flops / (kern_ms * 1e-3) / 1e12
+    traffic = None
+    tfile = REPO_DIR / "profiles" / f"traffic_{w.name}.json"
+    if tfile.exists():
+        try:
+            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+        except (ValueError, OSError):
+            traffic = None
+    out = {
+        "metric": "fp8 block-scaled GEMM TFLOP/s (% of 5.0 PFLOP/s dense fp8), consumer of "
+                  "the quantizer's codes and scales",
+        "value": round(value, 1),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8e4m3 (fp32 accumulate)",
+        "data": "synthetic",
+        "config": {"workload": w.name, "M": w.M, "N": w.N, "K": w.K,
+                   "a_scale": w.a_scale + " col-major 1x128", "b_scale": w.b_scale + " 128x128",
+                   "flops": flops, "min_hbm_bytes": set_bytes, "buffer_sets": nsets,
+                   "route": pkg.gemm_route(w.M, w.N, w.K)},
+        "us_per_call": round(kern_ms * 1e3, 2),
+        "us_per_call_median": round(durs[len(durs) // 2] * 1e3, 2),
+        "us_per_call_host_wall": round(wall_ms * 1e3, 2),
+        "pct_of_peak": round(100.0 * achieved / PEAK_FP8_TFLOPS, 2),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_FP8_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP8_TFLOPS, 4),
+                     "traffic": traffic},
+        "cpu_baseline": None,
+    }
+    if args.cpu_seconds > 0:
+        out["cpu_baseline"] = gemm_cpu_baseline(w, a_q, a_s, b_q, b_s, sets[0][4], args, torch)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def gemm_cpu_baseline(w, a_q, a_s, b_q, b_s, c_gpu, args, torch) -> dict:
+    """Times the C oracle (oracle/gemm_oracle.c, float64, OpenMP) on the first
+    rows of the workload and checks those rows of the GPU's output against it."""
+    import numpy as np
+    import oracle
+    threads = max(1, min(16, os.cpu_count() or 1))
+    rows = max(1, min(16, w.M))
+    u8 = lambda t: t.contiguous().view(torch.uint8).numpy()
+    aq, bq = u8(a_q[:rows]), u8(b_q)
+    sa = np.ascontiguousarray(a_s[:, :rows].numpy())
+    sb = b_s.numpy()
+    ref, bound = oracle.gemm(aq, sa, bq, sb, nthreads=threads)       # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 2 or (time.perf_counter() - t_start < args.cpu_seconds and len(times) < 100):
+        t0 = time.perf_counter()
+        oracle.gemm(aq, sa, bq, sb, nthreads=threads)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    t = times[len(times) // 2]
+    torch.cuda.synchronize()
+    got = c_gpu[:rows].float().cpu().numpy()
+    tol = 2.0 ** -8 * np.abs(ref) + 2 * (w.K // 128 + 130) * 2.0 ** -23 * bound
+    bad = int((np.abs(got - ref) > tol).sum())
+    return {"value": round(2.0 * rows * w.N * w.K / t / 1e12, 6), "unit": "TFLOP/s",
+            "cores": threads, "kind": "port", "us_per_call": round(t * 1e6, 1),
+            "sample": f"first {rows} of {w.M} rows of {w.name}, C oracle (float64, OpenMP), "
+                      f"median of {len(times)} runs",
+            "parity_vs_gpu_rows": {"ok": bad == 0, "outside_tolerance": bad}}
 
 
 if __name__ == "__main__":

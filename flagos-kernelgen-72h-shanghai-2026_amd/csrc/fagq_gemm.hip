@@ -7,22 +7,26 @@
 // src/task01_fused_add_rmsnorm_group_quant.py:1731-1851, stops at the
 // quantized tensor and scales); this is the layer those formats feed.
 //
-// Work mapping.  A workgroup of 8 waves computes a 256 x 256 tile of C; wave
-// (wm, wn) owns rows 64 wm .. +64 and columns 128 wn .. +128, i.e. 4 x 8
-// tiles of 16 x 16, each one v_mfma_scale_f32_16x16x128_f8f6f4 per 128-deep
-// k-block.  The weight tile is the MFMA's first operand and the activation
+// Work mapping.  A workgroup computes a 256 x 256 tile of C: 8 waves of
+// 64 x 128 (fp32 scales) or 4 waves of 128 x 128 (UE8M0 scales), each wave a
+// grid of 16 x 16 tiles, each one v_mfma_scale_f32_16x16x128_f8f6f4 per
+// 128-deep k-block.  The weight tile is the MFMA's first operand and the activation
 // tile its second, so each lane's four results are four consecutive columns
 // of one row of C (lane l: row l % 16, columns 4 (l / 16) .. +4) and the
 // activation scale a lane needs is that of its own row.
 //
 // Operand staging.  Per k-block, the 256 x 128-byte tiles of A and B go from
 // global memory straight into LDS (buffer_load_dwordx4 ... lds: each
-// instruction writes 1 KB, 16 bytes per lane, in lane order).  A lane fetches
-// 16-byte chunk (lane % 8) ^ (row % 8) of its row, so LDS holds each row with
-// its chunks XOR-swizzled by the row index: the MFMA operand reads (two
-// ds_read_b128 per lane, 16 consecutive rows at one chunk) then hit distinct
-// banks.  Two LDS stages (2 x 64 KB): the next k-block's copies are issued
-// before the current one is consumed.
+// instruction writes 1 KB, 16 bytes per lane, in lane order).  LDS holds
+// each 128-byte row with its eight 16-byte chunks XOR-swizzled: logical chunk
+// c of row r sits at position c ^ ((r / 2) % 8), so a lane fetches the
+// logical chunk (lane % 8) ^ ((r / 2) % 8).  A ds_read_b128 is served 16
+// lanes (256 bytes, all 64 banks) at a time, and an MFMA operand read has 16
+// consecutive rows at one logical chunk: rows of equal parity then land in
+// distinct 16-byte slots of the 256-byte bank window (a swizzle by r % 8
+// maps rows r and r + 8 to the same banks, which measured as a 2-way
+// conflict on every read).  Two LDS stages (2 x 64 KB): the next k-block's
+// copies are issued before the current one is consumed.
 //
 // Scales.  fp32 (or mixed) scales: each k-block's 16 x 16 x 128 product goes
 // to a temporary and is added to the accumulator as t * (sa * sb) with fmaf.
@@ -53,13 +57,30 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 constexpr int kBM = 256;                 // rows of C per workgroup
 constexpr int kBN = 256;                 // columns of C per workgroup
 constexpr int kBK = 128;                 // k per block (one MFMA deep, one scale block)
-constexpr int kWaves = 8;
-constexpr int kThreads = 64 * kWaves;
 constexpr int kTileBytes = 256 * kBK;    // one operand tile in LDS
 constexpr int kStageBytes = 2 * kTileBytes;
-constexpr int kTM = 4;                   // 16-row tiles per wave
-constexpr int kTN = 8;                   // 16-column tiles per wave
+constexpr int kCopyInsts = kTileBytes / 1024;   // 1 KB copy instructions per operand tile
 constexpr int kGroupM = 4;               // row tiles per group of the tile order
+
+// Wave layouts of the 256 x 256 tile.  WAVES_M x WAVES_N waves, each owning
+// TM x TN tiles of 16 x 16.  8 waves of 64 x 128 for every format: with two
+// waves per SIMD one wave's MFMAs cover the other's LDS reads.  (4 waves of
+// 128 x 128, accumulators in AGPRs, read a third less from LDS per MFMA but
+// measured 15 % slower with UE8M0 scales: one wave per SIMD leaves the
+// operand reads after each barrier exposed.)
+template <int WAVES_M_, int WAVES_N_>
+struct Layout {
+  static constexpr int WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
+  static constexpr int WAVES = WAVES_M * WAVES_N;
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int TM = kBM / 16 / WAVES_M;
+  static constexpr int TN = kBN / 16 / WAVES_N;
+  static constexpr int COPY_PER_WAVE = kCopyInsts / WAVES;
+  static_assert(16 * TN == 128, "a wave's columns must be one 128-column weight block");
+  static_assert(COPY_PER_WAVE % 2 == 0, "copy instructions alternate swizzle parity");
+};
+using LayoutF32 = Layout<4, 2>;
+using LayoutE8 = Layout<4, 2>;
 constexpr int kVmcnt0 = 0x0F70;          // s_waitcnt vmcnt(0) (other counters not waited)
 
 struct GArgs {
@@ -92,11 +113,14 @@ __device__ __forceinline__ void tile_coords(int b, int m_tiles, int n_tiles, int
   nt = w / gm;
 }
 
+// Position of logical 16-byte chunk c of LDS row r.
+__device__ __forceinline__ int swz(int c, int r) { return c ^ ((r >> 1) & 7); }
+
 // One 16 x 128-byte MFMA operand: lane l gets row (r0 + l % 16), k bytes
 // 32 (l / 16) .. +32, from a swizzled LDS tile.
 __device__ __forceinline__ i32x8 lds_frag(const uint8_t* tile, int row, int lane) {
   const int c0 = (lane >> 4) * 2;
-  const int sw = row & 7;
+  const int sw = (row >> 1) & 7;
   const uint8_t* r = tile + row * kBK;
   const i32x4 lo = *reinterpret_cast<const i32x4*>(r + ((c0 ^ sw) << 4));
   const i32x4 hi = *reinterpret_cast<const i32x4*>(r + (((c0 + 1) ^ sw) << 4));
@@ -108,14 +132,15 @@ __device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
   return e ? __uint_as_float(e << 23) : __uint_as_float(0x00400000u);
 }
 
-template <int ASF, int BSF>
-__global__ void __launch_bounds__(kThreads, 1) fagq_gemm_kernel(const GArgs g) {
+template <int ASF, int BSF, class L>
+__global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g) {
   constexpr bool kHwScale = ASF == SF_UE8M0 && BSF == SF_UE8M0;
+  constexpr int kTM = L::TM, kTN = L::TN;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStageBytes];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave & 3, wn = wave >> 2;
+  const int wm = wave % L::WAVES_M, wn = wave / L::WAVES_M;
   int mt, nt;
   tile_coords((int)blockIdx.x, g.m_tiles, g.n_tiles, mt, nt);
   const int m0 = mt * kBM, n0 = nt * kBN;
@@ -126,22 +151,29 @@ __global__ void __launch_bounds__(kThreads, 1) fagq_gemm_kernel(const GArgs g) {
   const rsrc_t ras = make_rsrc(g.as, g.as_bytes);
   const rsrc_t rbs = make_rsrc(g.bs, g.bs_bytes);
 
-  // Copy geometry: instruction u of this wave fills LDS rows (4 wave + u) * 8
-  // .. +8; the lane's row within them is lane / 8 and its chunk is swizzled.
+  // Copy geometry: instruction u of this wave is copy instruction i = wave *
+  // COPY_PER_WAVE + u of each operand tile and fills LDS rows 8 i .. +8; the
+  // lane's row within them is lane / 8, its position lane % 8, and it fetches
+  // the logical chunk stored there.  For row 8 i + lane / 8, (row / 2) % 8 =
+  // 4 (i % 2) + lane / 16, so even and odd instructions (i has the parity of
+  // u) need one lane offset each.
   // The whole offset goes in the VGPR offset and the scalar offset is zero:
   // the hardware range-checks only the VGPR offset (plus the immediate), so
   // this is what turns rows past M or N into zero reads.  The lane part is
   // kept in one VGPR and the uniform part added per instruction.
   const int crow = lane >> 3;
-  const uint32_t cvoff = (uint32_t)crow * (uint32_t)g.K + (uint32_t)((lane & 7) ^ crow) * 16u;
+  const uint32_t cvoff[2] = {
+      (uint32_t)crow * (uint32_t)g.K + (uint32_t)swz(lane & 7, crow) * 16u,
+      (uint32_t)crow * (uint32_t)g.K + (uint32_t)swz(lane & 7, crow + 8) * 16u};
 
   auto issue = [&](int kb, int stage) {
     uint8_t* sa_tile = lds + stage * kStageBytes;
     uint8_t* sb_tile = sa_tile + kTileBytes;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int inst = wave * 4 + u;
-      const uint32_t off = cvoff + (uint32_t)__builtin_amdgcn_readfirstlane(inst * 8 * g.K + kb * kBK);
+    for (int u = 0; u < L::COPY_PER_WAVE; ++u) {
+      const int inst = wave * L::COPY_PER_WAVE + u;
+      const uint32_t off = cvoff[u & 1] +
+                           (uint32_t)__builtin_amdgcn_readfirstlane(inst * 8 * g.K + kb * kBK);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(sa_tile + inst * 1024), 16, off,
                                                0, 0, 0);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(sb_tile + inst * 1024), 16, off,
@@ -149,12 +181,12 @@ __global__ void __launch_bounds__(kThreads, 1) fagq_gemm_kernel(const GArgs g) {
     }
   };
 
-  // Scales of this lane's rows (m0 + 64 wm + 16 i + lane % 16) and of the
+  // Scales of this lane's rows (m0 + 16 (TM wm + i) + lane % 16) and of the
   // wave's 128-column weight block (n0 / 128 + wn) for k-block kb, as loaded
   // bits: they are converted only after the barrier that ends the k-block,
   // so no wait for them (and, the counter being in order, for the LDS copies
   // issued before them) lands inside the MFMA loop.
-  const int arow = m0 + wm * 64 + (lane & 15);
+  const int arow = m0 + wm * 16 * kTM + (lane & 15);
   const int wblk = (n0 >> 7) + wn;
   struct Scales {
     uint32_t a[kTM], b;
@@ -208,7 +240,7 @@ __global__ void __launch_bounds__(kThreads, 1) fagq_gemm_kernel(const GArgs g) {
     const uint8_t* tb = ta + kTileBytes;
     i32x8 af[kTM];
 #pragma unroll
-    for (int i = 0; i < kTM; ++i) af[i] = lds_frag(ta, wm * 64 + 16 * i + (lane & 15), lane);
+    for (int i = 0; i < kTM; ++i) af[i] = lds_frag(ta, wm * 16 * kTM + 16 * i + (lane & 15), lane);
 #pragma unroll
     for (int j = 0; j < kTN; ++j) {
       const i32x8 bf = lds_frag(tb, wn * 128 + 16 * j + (lane & 15), lane);
@@ -239,7 +271,7 @@ __global__ void __launch_bounds__(kThreads, 1) fagq_gemm_kernel(const GArgs g) {
     if (ncol >= g.N) continue;   // uniform over the wave
 #pragma unroll
     for (int i = 0; i < kTM; ++i) {
-      const uint32_t row = (uint32_t)(wm * 64 + 16 * i + (lane & 15));
+      const uint32_t row = (uint32_t)(wm * 16 * kTM + 16 * i + (lane & 15));
       u32x2 v;
       v[0] = pack_bf16x2(acc[j][i][0], acc[j][i][1]);
       v[1] = pack_bf16x2(acc[j][i][2], acc[j][i][3]);
@@ -286,12 +318,15 @@ int validate(const void* a_q, const void* a_scale, const void* b_q, const void* 
   return FAGQ_OK;
 }
 
-const void* kernel_for(int asf, int bsf) {
+// Kernel and workgroup size for a pair of scale formats.
+const void* kernel_for(int asf, int bsf, int* threads) {
   const bool au = asf == FAGQ_SCALE_UE8M0, bu = bsf == FAGQ_SCALE_UE8M0;
-  if (au && bu) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_UE8M0, SF_UE8M0>);
-  if (au) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_UE8M0, SF_F32>);
-  if (bu) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_F32, SF_UE8M0>);
-  return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_F32, SF_F32>);
+  *threads = au && bu ? LayoutE8::THREADS : LayoutF32::THREADS;
+  if (au && bu)
+    return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_UE8M0, SF_UE8M0, LayoutE8>);
+  if (au) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_UE8M0, SF_F32, LayoutF32>);
+  if (bu) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_F32, SF_UE8M0, LayoutF32>);
+  return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_F32, SF_F32, LayoutF32>);
 }
 
 }  // namespace
@@ -330,9 +365,11 @@ FAGQ_API int fagq_gemm_launch(const void* a_q, const void* a_scale, const void* 
   g.as_bytes = (uint32_t)(M * g.kblocks * (a_scale_format == FAGQ_SCALE_F32 ? 4 : 1));
   g.bs_bytes = (uint32_t)(ceil_div(N, 128) * g.kblocks * (b_scale_format == FAGQ_SCALE_F32 ? 4 : 1));
   void* args[] = {&g};
-  const hipError_t e = hipLaunchKernel(kernel_for(a_scale_format, b_scale_format),
-                                       dim3((unsigned)(g.m_tiles * g.n_tiles)), dim3(kThreads),
-                                       args, 0, static_cast<hipStream_t>(stream));
+  int threads = 0;
+  const void* kernel = kernel_for(a_scale_format, b_scale_format, &threads);
+  const hipError_t e = hipLaunchKernel(kernel, dim3((unsigned)(g.m_tiles * g.n_tiles)),
+                                       dim3((unsigned)threads), args, 0,
+                                       static_cast<hipStream_t>(stream));
   return e == hipSuccess ? FAGQ_OK : -(int)e;
 }
 
@@ -341,7 +378,7 @@ FAGQ_API int fagq_gemm_query_route(int64_t M, int64_t N, int64_t K, fagq_gemm_ro
   if (M < 0 || N <= 0 || K <= 0 || N % 16 != 0 || K % kBK != 0) return FAGQ_E_SHAPE;
   route->block_m = kBM;
   route->block_n = kBN;
-  route->block_threads = kThreads;
+  route->block_threads = LayoutF32::THREADS;   // LayoutE8::THREADS when both scales are UE8M0
   route->group_m = kGroupM;
   route->grid_blocks = ceil_div(M, kBM) * ceil_div(N, kBN);
   return FAGQ_OK;
