@@ -237,6 +237,8 @@ int launch_with(const Mapping& m, const void* x, const void* residual, const voi
   a.rpb = m.rpb;
   a.col_major = scale_layout == FAGQ_LAYOUT_COL_MAJOR;
   a.remap = remap;
+  a.remap_shift = remap >= 2 ? __builtin_ctz((unsigned)remap) : 0;
+  a.wpr_magic = (65536 + m.wpr - 1) / m.wpr;
   const LaunchFn fn = lookup(q_format, scale_format, rounding, lpg_index((int)G), m.ns,
                              norm_out != nullptr, m.rseq);
   const hipError_t e = fn(a, dim3((unsigned)m.grid), dim3((unsigned)m.block),

@@ -69,6 +69,8 @@ struct KArgs {
   int32_t rpb;         // row groups per workgroup (each wpr waves)
   int32_t col_major;   // scale layout: 0 -> [M, groups], 1 -> [groups, M]
   int32_t remap;       // workgroup -> row-tile order, see tile_of_block
+  int32_t remap_shift; // log2(remap) when remap >= 2 (remap is a power of two)
+  int32_t wpr_magic;   // ceil(2^16 / wpr): wave / wpr == (wave * wpr_magic) >> 16 for wave < 64
 };
 
 // ---------------------------------------------------------------- helpers
@@ -185,17 +187,17 @@ __device__ __forceinline__ float row_inv_rms(double ss, int D, float eps) {
 //     dispatch order).  The tiles in flight stay one contiguous window, and
 //     n neighbouring rows' column-major scale words meet in one L2, so they
 //     leave it as one full 32-byte write instead of n partial ones.
-__device__ __forceinline__ int tile_of_block(int b, int nb, int remap) {
-  if (remap == 0) return b;
-  if (remap == 1) {
-    const int x = b & 7, i = b >> 3, per = nb >> 3, rem = nb & 7;
-    return x * per + (x < rem ? x : rem) + i;
-  }
-  const int chunk = 8 * remap;
-  const int c = b / chunk;
-  if ((c + 1) * chunk > nb) return b;
-  const int w = b - c * chunk;
-  return c * chunk + (w & 7) * remap + (w >> 3);
+//   All three are computed with shifts and masks (the chunk is a power of
+//   two) and one is selected, so the prologue has no branch and no integer
+//   division.
+__device__ __forceinline__ int tile_of_block(int b, int nb, int remap, int remap_shift) {
+  const int x = b & 7, i = b >> 3, per = nb >> 3, rem = nb & 7;
+  const int contiguous = x * per + (x < rem ? x : rem) + i;
+  const int cs = 3 + remap_shift;                       // log2(chunk), chunk = 8 * remap
+  const int c = b >> cs;
+  const int w = b & ((1 << cs) - 1);
+  const int chunked = ((c + 1) << cs) > nb ? b : (c << cs) + ((w & 7) << remap_shift) + (w >> 3);
+  return remap == 0 ? b : remap == 1 ? contiguous : chunked;
 }
 
 // ceil(log2(s)) for a positive normal fp32 s, exactly, from its bits.
@@ -248,31 +250,38 @@ struct RowRsrc {
   uint32_t scale_step;   // byte distance between the scales of consecutive steps
 };
 
-template <int SF, bool NORM>
-__device__ __forceinline__ RowRsrc row_rsrc(const KArgs& a, const WaveCtx& w, int64_t row, int G) {
-  constexpr uint32_t sb = SF == SF_F32 ? 4u : 1u;
+// The input descriptors (x, residual) are built first and their loads
+// issued before the output descriptors are computed.
+__device__ __forceinline__ void row_rsrc_in(const KArgs& a, const WaveCtx& w, int64_t row,
+                                            RowRsrc& r) {
   const bool ok = row < a.M;
   const int64_t e = (ok ? row : 0) * (int64_t)a.D + w.c0;
   const uint32_t cols = ok ? w.cols : 0u;
-  RowRsrc r;
   r.x = make_rsrc(a.x + e, cols * 2u);
   r.res = make_rsrc(a.res + e, cols * 2u);
+}
+
+template <int SF, bool NORM>
+__device__ __forceinline__ void row_rsrc_out(const KArgs& a, const WaveCtx& w, int64_t row, int G,
+                                             RowRsrc& r) {
+  constexpr uint32_t sb = SF == SF_F32 ? 4u : 1u;
+  const bool ok = row < a.M;
+  const int64_t rr = ok ? row : 0;
+  const int64_t e = rr * (int64_t)a.D + w.c0;
+  const uint32_t cols = ok ? w.cols : 0u;
   r.res_out = make_rsrc(a.res_out + e, cols * 2u);
   if constexpr (NORM) r.norm = make_rsrc(a.norm_out + e, cols * 2u);
   r.q = make_rsrc(a.q + e, cols);
   const int g0 = w.c0 / G;                                  // first group of this wave
   const uint32_t ng = ok && w.cols ? (uint32_t)(a.groups - g0) : 0u;
-  if (a.col_major) {
-    // scale[g * M + row]: this wave's groups start at g0; the descriptor ends
-    // just after the row's last group.
-    r.scale = make_rsrc(a.scale + ((int64_t)g0 * a.M + (ok ? row : 0)) * sb,
-                        ng ? (uint32_t)(((int64_t)(ng - 1) * a.M + 1) * sb) : 0u);
-    r.scale_step = (uint32_t)((int64_t)(kStepCols / G) * a.M * sb);
-  } else {
-    r.scale = make_rsrc(a.scale + ((ok ? row : 0) * (int64_t)a.groups + g0) * sb, ng * sb);
-    r.scale_step = (uint32_t)(kStepCols / G) * sb;
-  }
-  return r;
+  // Column-major: scale[g * M + row]; this wave's groups start at g0 and the
+  // descriptor ends just after the row's last group.  Row-major:
+  // scale[row * groups + g].  Both are computed and one selected.
+  const bool col = a.col_major != 0;
+  const int64_t base = col ? (int64_t)g0 * a.M + rr : rr * (int64_t)a.groups + g0;
+  const uint32_t span = col ? (ng ? (uint32_t)((int64_t)(ng - 1) * a.M + 1) : 0u) : ng;
+  r.scale = make_rsrc(a.scale + base * sb, span * sb);
+  r.scale_step = (uint32_t)(kStepCols / G) * sb * (col ? (uint32_t)a.M : 1u);
 }
 
 // Phase 1 for one row: issue the loads of x and residual for NS steps.
@@ -387,18 +396,10 @@ fagq_rows(const KArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wpr = a.wpr;
-  const int blk = tile_of_block((int)blockIdx.x, (int)gridDim.x, a.remap);
-  int rib, part;                            // row group within the workgroup, wave within the row
-  if (a.rpb == 1) {
-    rib = 0;
-    part = wave;
-  } else if (wpr == 1) {
-    rib = wave;
-    part = 0;
-  } else {
-    rib = wave / wpr;
-    part = wave - rib * wpr;
-  }
+  const int blk = tile_of_block((int)blockIdx.x, (int)gridDim.x, a.remap, a.remap_shift);
+  // Row group within the workgroup and wave within the row (wpr * rpb waves).
+  const int rib = (wave * a.wpr_magic) >> 16;
+  const int part = wave - rib * wpr;
   const int64_t row0 = ((int64_t)blk * a.rpb + rib) * RSEQ;
   WaveCtx wc;
   wc.lane = lane;
@@ -408,7 +409,13 @@ fagq_rows(const KArgs a) {
   const uint32_t scale_voff =
       (uint32_t)wc.gl * (a.col_major ? (uint32_t)(a.M * (int64_t)sb) : sb);
 
-  // gamma for this wave's columns, once for all RSEQ rows.
+  // The first row's inputs go out first, then gamma for this wave's columns
+  // (an L2 hit, needed at the same time; loaded once for all RSEQ rows), then
+  // the output descriptors are computed.
+  u32x4 xv[NS], rv[NS];
+  RowRsrc rr;
+  row_rsrc_in(a, wc, row0, rr);
+  load_row<NS>(rr, lane, xv, rv);
   u32x4 gv[NS];
   {
     const rsrc_t rg = make_rsrc(a.gamma + wc.c0, wc.cols * 2u);
@@ -416,10 +423,7 @@ fagq_rows(const KArgs a) {
     for (int k = 0; k < NS; ++k)
       gv[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, lane * 16 + k * 1024, 0, 0);
   }
-
-  u32x4 xv[NS], rv[NS];
-  RowRsrc rr = row_rsrc<SF, NORM>(a, wc, row0, G);
-  load_row<NS>(rr, lane, xv, rv);
+  row_rsrc_out<SF, NORM>(a, wc, row0, G, rr);
 
 #pragma unroll
   for (int i = 0; i < RSEQ; ++i) {
@@ -429,8 +433,9 @@ fagq_rows(const KArgs a) {
     RowRsrc rn;
     if (i + 1 < RSEQ) {
       // The next row's inputs go out now, behind this row's reduction and stores.
-      rn = row_rsrc<SF, NORM>(a, wc, row0 + i + 1, G);
+      row_rsrc_in(a, wc, row0 + i + 1, rn);
       load_row<NS>(rn, lane, xv, rv);
+      row_rsrc_out<SF, NORM>(a, wc, row0 + i + 1, G, rn);
     }
 
     // Phase 3: row sum of squares -> inv_rms.  With several waves per row, the
