@@ -21,6 +21,10 @@ Prints one JSON line:
               of the same workload on the host cores (and checked against the
               GPU's rows)
 
+--config tp*_shard_*: the multi-input form (fagq_launch_parts) at one rank's
+shard of a tensor-parallel layer: nparts partial sums reduced, normalized and
+quantized (fp8, fp32 column-major scales); cpu_baseline = the C oracle.
+
 --config gemm_*: the fp8 block-scaled GEMM that consumes the operator's
 output (fagq_gemm_launch); value and roofline in TFLOP/s against MI355X's
 5.0 PFLOP/s dense fp8 peak, cpu_baseline = the C oracle (oracle/gemm_oracle.c)
@@ -114,9 +118,11 @@ def main() -> int:
     if args.copy:
         return copy_bench(args, torch, pkg)
     name = args.config or HEADLINE
-    from fagq_mi355x.workloads import GEMM_CONFIGS
+    from fagq_mi355x.workloads import GEMM_CONFIGS, PARTS_CONFIGS
     if name in GEMM_CONFIGS:
         return gemm_bench(args, torch, pkg, GEMM_CONFIGS[name])
+    if name in PARTS_CONFIGS:
+        return parts_bench(args, torch, pkg, PARTS_CONFIGS[name])
     w = CONFIGS[name]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -294,6 +300,135 @@ def cpu_baseline(w, x, res, gamma, gpu_set, args, torch) -> dict:
             "kind": "port", "us_per_call": round(t * 1e6, 1),
             "sample": f"first {rows} of {w.M} rows of {w.name}, eager PyTorch CPU "
                       f"restatement (oracle/torch_eager.py), median of {len(times)} runs",
+            "parity_vs_gpu_rows": parity}
+
+
+def parts_bench(args, torch, pkg, w) -> int:
+    """Times fagq_launch_parts on a shard workload (inputs resident in HBM,
+    buffer sets rotated past the MALL), kernel time by HIP events."""
+    import ctypes
+    from fagq_mi355x import _lib
+    from fagq_mi355x.workloads import make_parts_inputs
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = _lib.load()
+    parts, res, gamma = make_parts_inputs(w)
+    set_bytes = w.algorithmic_bytes()
+    nsets = max(2, min(16, math.ceil(ROTATE_BYTES / set_bytes) + 1))
+    gd = gamma.to(dev)
+    pd0 = [p.to(dev) for p in parts]
+    rd0 = res.to(dev)
+    sets = []
+    for i in range(nsets):
+        pd = pd0 if i == 0 else [p.clone() for p in pd0]
+        rd = rd0 if i == 0 else rd0.clone()
+        ro = torch.empty_like(rd)
+        q = torch.empty(w.M, w.D, dtype=torch.float8_e4m3fn, device=dev)
+        sc = pkg.empty_scales(w.M, w.D // w.group_size, col_major=True, device=dev)
+        arr = (ctypes.c_void_p * w.nparts)(*[t.data_ptr() for t in pd])
+        sets.append((pd, arr, rd, ro, q, sc))
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+
+    def step(i: int):
+        _, arr, rd, ro, q, sc = sets[i % nsets]
+        st = lib.fagq_launch_parts(ctypes.cast(arr, ctypes.c_void_p), w.nparts, P(rd), P(gd),
+                                   P(ro), P(q), P(sc), w.M, w.D, w.group_size, 1e-6,
+                                   _lib.Q_FP8_E4M3FN, _lib.SCALE_F32, _lib.LAYOUT_COL_MAJOR,
+                                   _lib.ROUND_RNE, sp)
+        if st:
+            _lib.check(st, "fagq_launch_parts")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize(dev)
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    for i in range(args.steps):
+        starts[i].record(stream)
+        step(i)
+        ends[i].record(stream)
+    torch.cuda.synchronize(dev)
+    durs = sorted(st.elapsed_time(en) for st, en in zip(starts, ends))
+    kern_ms = sum(durs) / len(durs)
+    value = set_bytes / (wall_ms * 1e-3) / 1e9
+    achieved = set_bytes / (kern_ms * 1e-3) / 1e9
+    out = {
+        "metric": "achieved HBM GB/s (% of 8 TB/s), multi-input form at one rank's shard",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": w.name, "M": w.M, "D": w.D, "nparts": w.nparts,
+                   "group_size": w.group_size, "q": "float8_e4m3fn", "scale": "f32 col-major",
+                   "algorithmic_bytes": set_bytes, "buffer_sets": nsets},
+        "us_per_call": round(kern_ms * 1e3, 2),
+        "us_per_call_median": round(durs[len(durs) // 2] * 1e3, 2),
+        "us_per_call_host_wall": round(wall_ms * 1e3, 2),
+        "pct_of_peak": round(100.0 * achieved / PEAK_HBM_GBS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None},
+        "cpu_baseline": None,
+    }
+    if args.cpu_seconds > 0:
+        out["cpu_baseline"] = parts_cpu_baseline(w, parts, res, gamma, sets[0], args, torch)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def parts_cpu_baseline(w, parts, res, gamma, gpu_set, args, torch) -> dict:
+    """Times the C oracle (oracle.fagq_parts, OpenMP) on the first rows of the
+    shard and checks those rows of the GPU's output against it."""
+    import numpy as np
+    import oracle
+    from oracle.compare import compare
+    threads = max(1, min(16, os.cpu_count() or 1))
+    rows = max(1, min(args.cpu_rows, w.M))
+    u16 = lambda t: t[:rows].contiguous().view(torch.uint16).numpy()
+    pr = [u16(p) for p in parts]
+    rr, gg = u16(res), gamma.contiguous().view(torch.uint16).numpy()
+
+    def run():
+        return oracle.fagq_parts(pr, rr, gg, 1e-6, w.group_size, oracle.Q_FP8, oracle.S_F32,
+                                 oracle.L_COL, oracle.R_RNE, nthreads=threads)
+
+    ref = run()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < args.cpu_seconds and len(times) < 1000):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    t = times[len(times) // 2]
+    _, _, _, ro, q, sc = gpu_set
+    torch.cuda.synchronize()
+    gpu = {"residual_out": ro[:rows].cpu().view(torch.uint16).numpy(),
+           "q": q[:rows].cpu().view(torch.uint8).numpy(),
+           "scale": np.ascontiguousarray(sc[:rows].t().cpu().numpy())}
+    try:
+        st = compare(gpu, ref, fp8=True, ue8m0=False)
+        parity = {"ok": True, "exact": st["exact"], "q_mismatch": st["q_mismatch"]}
+    except AssertionError as e:
+        parity = {"ok": False, "error": str(e)[:200]}
+    nbytes = w.algorithmic_bytes() * rows // w.M
+    return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "us_per_call": round(t * 1e6, 1),
+            "sample": f"first {rows} of {w.M} rows of {w.name}, C oracle (oracle.fagq_parts, "
+                      f"OpenMP), median of {len(times)} runs",
             "parity_vs_gpu_rows": parity}
 
 

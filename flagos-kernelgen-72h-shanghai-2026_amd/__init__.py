@@ -10,7 +10,7 @@ from . import _lib
 from ._lib import FagqError, load as load_library
 from .gemm import fp8_block_scaled_gemm, gemm_route
 from .ops import (empty_scales, fused_add_rmsnorm_group_quant, fused_add_rmsnorm_group_quant_fn,
-                  route_for)
+                  fused_reduce_add_rmsnorm_group_quant, route_for)
 
 __all__ = [
     "FagqError",
@@ -18,6 +18,7 @@ __all__ = [
     "fp8_block_scaled_gemm",
     "fused_add_rmsnorm_group_quant",
     "fused_add_rmsnorm_group_quant_fn",
+    "fused_reduce_add_rmsnorm_group_quant",
     "gemm_route",
     "load_library",
     "route_for",

@@ -23,6 +23,7 @@ SCALE_F32, SCALE_UE8M0 = 0, 1
 LAYOUT_ROW_MAJOR, LAYOUT_COL_MAJOR = 0, 1
 ROUND_RNE, ROUND_TRUNC = 0, 1
 MAX_D = 32768
+MAX_PARTS, MAX_D_PARTS = 8, 16384
 
 STATUS_NAMES = {
     0: "FAGQ_OK", 1: "FAGQ_E_NULL", 2: "FAGQ_E_SHAPE", 3: "FAGQ_E_GROUP", 4: "FAGQ_E_ALIGN",
@@ -49,6 +50,7 @@ class GemmRoute(ctypes.Structure):
 
 SIGNATURES = {
     "fagq_launch": ([_P] * 7 + [_I64, _I64, _I64, _F, _I, _I, _I, _I, _P], _I),
+    "fagq_launch_parts": ([_P, _I] + [_P] * 5 + [_I64, _I64, _I64, _F, _I, _I, _I, _I, _P], _I),
     "fagq_launch_mapped": ([_P] * 7 + [_I64, _I64, _I64, _F, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "fagq_query_route": ([_I64, _I64, _I64, ctypes.POINTER(Route)], _I),
     "fagq_status_string": ([_I], ctypes.c_char_p),

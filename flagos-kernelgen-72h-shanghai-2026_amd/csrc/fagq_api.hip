@@ -215,6 +215,61 @@ LaunchFn lookup(int q_format, int scale_format, int rounding, int lpg_idx, int s
   }
 }
 
+LaunchFn lookup_parts(int q_format, int scale_format, int rounding, int lpg_idx, int steps) {
+  const int qf = q_format == FAGQ_Q_FP8_E4M3FN ? QF_FP8
+                 : rounding == FAGQ_ROUND_RNE  ? QF_I8_RNE
+                                               : QF_I8_TRUNC;
+  const bool ue = scale_format == FAGQ_SCALE_UE8M0;
+  switch (qf) {
+    case QF_FP8: return ue ? lookup_parts_q0_s1(lpg_idx, steps) : lookup_parts_q0_s0(lpg_idx, steps);
+    case QF_I8_RNE: return ue ? lookup_parts_q1_s1(lpg_idx, steps) : lookup_parts_q1_s0(lpg_idx, steps);
+    default: return ue ? lookup_parts_q2_s1(lpg_idx, steps) : lookup_parts_q2_s0(lpg_idx, steps);
+  }
+}
+
+int parts_steps() {
+  static const int v = env_int("FAGQ_PARTS_STEPS", 2);
+  return v;
+}
+
+// The multi-input form's mapping: FAGQ_PARTS_STEPS (default 2; 1 measured
+// 5 % slower at D = 7168) steps per wave, 2 whenever the row would need more
+// than 16 waves; one row per row group; small rows share a workgroup as in
+// choose_mapping.
+void choose_mapping_parts(int64_t M, int D, Mapping* m) {
+  const int steps = ceil_div(D, kStepCols);
+  int ns = parts_steps() >= kMaxStepsParts ? kMaxStepsParts : 1;
+  if (ceil_div(steps, ns) > kMaxWavesPerBlock) ns = kMaxStepsParts;
+  if (ns > steps) ns = steps;
+  const int wpr = ceil_div(steps, ns);
+  const int rpb = wpr >= 4 ? 1 : 4 / wpr;
+  finish_mapping(M, D, wpr, rpb, 1, m);
+}
+
+void fill_args(KArgs* a, const Mapping& m, const void* x, const void* residual, const void* gamma,
+               void* residual_out, void* norm_out, void* q, void* scale, int64_t M, int64_t D,
+               int64_t G, float eps, int scale_layout, int remap) {
+  a->x = static_cast<const uint16_t*>(x);
+  a->res = static_cast<const uint16_t*>(residual);
+  a->gamma = static_cast<const uint16_t*>(gamma);
+  a->res_out = static_cast<uint16_t*>(residual_out);
+  a->norm_out = static_cast<uint16_t*>(norm_out);
+  a->q = static_cast<uint8_t*>(q);
+  a->scale = static_cast<uint8_t*>(scale);
+  a->M = M;
+  a->D = (int32_t)D;
+  a->groups = (int32_t)(D / G);
+  a->eps = eps;
+  a->wpr = m.wpr;
+  a->rpb = m.rpb;
+  a->col_major = scale_layout == FAGQ_LAYOUT_COL_MAJOR;
+  a->remap = remap;
+  a->remap_shift = remap >= 2 ? __builtin_ctz((unsigned)remap) : 0;
+  a->wpr_magic = (65536 + m.wpr - 1) / m.wpr;
+  a->nparts = 0;
+  for (int p = 0; p < kMaxParts; ++p) a->xparts[p] = nullptr;
+}
+
 int launch_with(const Mapping& m, const void* x, const void* residual, const void* gamma,
                 void* residual_out, void* norm_out, void* q, void* scale, int64_t M, int64_t D,
                 int64_t G, float eps, int q_format, int scale_format, int scale_layout,
@@ -222,23 +277,8 @@ int launch_with(const Mapping& m, const void* x, const void* residual, const voi
   const int dc = device_check();
   if (dc != FAGQ_OK) return dc;
   KArgs a;
-  a.x = static_cast<const uint16_t*>(x);
-  a.res = static_cast<const uint16_t*>(residual);
-  a.gamma = static_cast<const uint16_t*>(gamma);
-  a.res_out = static_cast<uint16_t*>(residual_out);
-  a.norm_out = static_cast<uint16_t*>(norm_out);
-  a.q = static_cast<uint8_t*>(q);
-  a.scale = static_cast<uint8_t*>(scale);
-  a.M = M;
-  a.D = (int32_t)D;
-  a.groups = (int32_t)(D / G);
-  a.eps = eps;
-  a.wpr = m.wpr;
-  a.rpb = m.rpb;
-  a.col_major = scale_layout == FAGQ_LAYOUT_COL_MAJOR;
-  a.remap = remap;
-  a.remap_shift = remap >= 2 ? __builtin_ctz((unsigned)remap) : 0;
-  a.wpr_magic = (65536 + m.wpr - 1) / m.wpr;
+  fill_args(&a, m, x, residual, gamma, residual_out, norm_out, q, scale, M, D, G, eps,
+            scale_layout, remap);
   const LaunchFn fn = lookup(q_format, scale_format, rounding, lpg_index((int)G), m.ns,
                              norm_out != nullptr, m.rseq);
   const hipError_t e = fn(a, dim3((unsigned)m.grid), dim3((unsigned)m.block),
@@ -283,6 +323,49 @@ FAGQ_API int fagq_launch_mapped(const void* x, const void* residual, const void*
   if (M == 0) return FAGQ_OK;
   return launch_with(m, x, residual, gamma, residual_out, norm_out, q, scale, M, D, group_size,
                      eps, q_format, scale_format, scale_layout, rounding, xcd_remap, stream);
+}
+
+FAGQ_API int fagq_launch_parts(const void* const* x_parts, int nparts, const void* residual,
+                               const void* gamma, void* residual_out, void* q, void* scale,
+                               int64_t M, int64_t D, int64_t group_size, float eps,
+                               int q_format, int scale_format, int scale_layout, int rounding,
+                               void* stream) {
+  if (!x_parts) return FAGQ_E_NULL;
+  if (nparts < 1 || nparts > FAGQ_MAX_PARTS) return FAGQ_E_SHAPE;
+  for (int p = 0; p < nparts; ++p)
+    if (!x_parts[p]) return FAGQ_E_NULL;
+  // Common checks with part 0 standing for x (residual_out == x is not
+  // allowed here: it is checked below against every part).
+  const int v = validate(x_parts[0], residual, gamma, residual_out, nullptr, q, scale, M, D,
+                         group_size, eps, q_format, scale_format, scale_layout, rounding);
+  if (v != FAGQ_OK) return v;
+  if (D > FAGQ_MAX_D_PARTS) return FAGQ_E_TOO_LARGE;
+  if (M == 0) return FAGQ_OK;
+  const uintptr_t nb = (uintptr_t)(M * D * 2);
+  const uintptr_t sbytes =
+      (uintptr_t)(M * (D / group_size) * (scale_format == FAGQ_SCALE_F32 ? 4 : 1));
+  auto rng = [](const void* p, uintptr_t n) {
+    return Range{reinterpret_cast<uintptr_t>(p), reinterpret_cast<uintptr_t>(p) + n};
+  };
+  const Range ro = rng(residual_out, nb), qo = rng(q, nb / 2), so = rng(scale, sbytes);
+  for (int p = 0; p < nparts; ++p) {
+    if (!aligned(x_parts[p], 16)) return FAGQ_E_ALIGN;
+    const Range xp = rng(x_parts[p], nb);
+    if (overlap(xp, ro) || overlap(xp, qo) || overlap(xp, so)) return FAGQ_E_ALIAS;
+  }
+  const int dc = device_check();
+  if (dc != FAGQ_OK) return dc;
+  Mapping m;
+  choose_mapping_parts(M, (int)D, &m);
+  KArgs a;
+  fill_args(&a, m, x_parts[0], residual, gamma, residual_out, nullptr, q, scale, M, D, group_size,
+            eps, scale_layout, remap_for(scale_layout, scale_format, m.rpb));
+  a.nparts = nparts;
+  for (int p = 0; p < nparts; ++p) a.xparts[p] = static_cast<const uint16_t*>(x_parts[p]);
+  const LaunchFn fn = lookup_parts(q_format, scale_format, rounding, lpg_index((int)group_size), m.ns);
+  const hipError_t e = fn(a, dim3((unsigned)m.grid), dim3((unsigned)m.block),
+                          static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? FAGQ_OK : -(int)e;
 }
 
 FAGQ_API int fagq_query_route(int64_t M, int64_t D, int64_t group_size, fagq_route* route) {

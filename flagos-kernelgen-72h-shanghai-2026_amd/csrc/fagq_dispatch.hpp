@@ -33,4 +33,13 @@ LaunchFn lookup_q1_s1(int lpg_idx, int steps, bool norm, int rseq_idx);   // int
 LaunchFn lookup_q2_s0(int lpg_idx, int steps, bool norm, int rseq_idx);   // int8 trunc, f32
 LaunchFn lookup_q2_s1(int lpg_idx, int steps, bool norm, int rseq_idx);   // int8 trunc, ue8m0
 
+// Multi-input form (fagq_rows_parts): lookup_parts_q<code>_s<scale>(lpg index,
+// steps per wave in [1, kMaxStepsParts]).
+LaunchFn lookup_parts_q0_s0(int lpg_idx, int steps);
+LaunchFn lookup_parts_q0_s1(int lpg_idx, int steps);
+LaunchFn lookup_parts_q1_s0(int lpg_idx, int steps);
+LaunchFn lookup_parts_q1_s1(int lpg_idx, int steps);
+LaunchFn lookup_parts_q2_s0(int lpg_idx, int steps);
+LaunchFn lookup_parts_q2_s1(int lpg_idx, int steps);
+
 }  // namespace fagq

@@ -1,7 +1,8 @@
 // fagq_inst.hip - instantiates fagq_rows for one (code format, scale format)
 // pair, selected with -DFAGQ_QF=<0|1|2> -DFAGQ_SF=<0|1>, for every supported
 // group size, steps per wave, norm_out choice and rows-in-sequence count,
-// and exports its launch lookup.
+// and fagq_rows_parts for every group size and steps per wave, and exports
+// their launch lookups.
 #include "fagq_dispatch.hpp"
 
 #ifndef FAGQ_QF
@@ -13,6 +14,7 @@
 
 #define FAGQ_CAT4(a, b, c, d) a##b##c##d
 #define FAGQ_LOOKUP(q, s) FAGQ_CAT4(lookup_q, q, _s, s)
+#define FAGQ_LOOKUP_PARTS(q, s) FAGQ_CAT4(lookup_parts_q, q, _s, s)
 
 namespace fagq {
 namespace {
@@ -23,6 +25,14 @@ hipError_t launch_rows(const KArgs& a, dim3 grid, dim3 block, hipStream_t stream
   return hipLaunchKernel(
       reinterpret_cast<const void*>(&fagq_rows<NS, LPG, FAGQ_QF, FAGQ_SF, NORM, RSEQ>), grid,
       block, args, 0, stream);
+}
+
+template <int NS, int LPG>
+hipError_t launch_rows_parts(const KArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
+  void* args[] = {const_cast<KArgs*>(&a)};
+  return hipLaunchKernel(
+      reinterpret_cast<const void*>(&fagq_rows_parts<NS, LPG, FAGQ_QF, FAGQ_SF>), grid, block,
+      args, 0, stream);
 }
 
 }  // namespace
@@ -40,6 +50,16 @@ LaunchFn FAGQ_LOOKUP(FAGQ_QF, FAGQ_SF)(int lpg_idx, int steps, bool norm, int rs
   static const LaunchFn table[kNumLpg][kMaxStepsPerWave][2][kNumRseq] = {
       FAGQ_S(8), FAGQ_S(16), FAGQ_S(32)};
   return table[lpg_idx][steps - 1][norm ? 1 : 0][rseq_idx];
+}
+
+static_assert(kMaxStepsParts == 2, "the parts table lists 2 step counts");
+
+LaunchFn FAGQ_LOOKUP_PARTS(FAGQ_QF, FAGQ_SF)(int lpg_idx, int steps) {
+  static const LaunchFn table[kNumLpg][kMaxStepsParts] = {
+      {&launch_rows_parts<1, 8>, &launch_rows_parts<2, 8>},
+      {&launch_rows_parts<1, 16>, &launch_rows_parts<2, 16>},
+      {&launch_rows_parts<1, 32>, &launch_rows_parts<2, 32>}};
+  return table[lpg_idx][steps - 1];
 }
 
 }  // namespace fagq

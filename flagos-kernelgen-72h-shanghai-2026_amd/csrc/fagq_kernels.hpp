@@ -51,6 +51,8 @@ enum SFormat { SF_F32 = 0, SF_UE8M0 = 1 };
 constexpr int kStepCols = 512;      // columns per wave step (64 lanes x 8)
 constexpr int kMaxWavesPerBlock = 16;
 constexpr int kMaxStepsPerWave = 4;
+constexpr int kMaxParts = 8;        // partial sums of x in the multi-input form
+constexpr int kMaxStepsParts = 2;   // steps per wave in the multi-input form
 
 // Kernel arguments (element pointers; the kernels build buffer descriptors).
 struct KArgs {
@@ -71,6 +73,9 @@ struct KArgs {
   int32_t remap;       // workgroup -> row-tile order, see tile_of_block
   int32_t remap_shift; // log2(remap) when remap >= 2 (remap is a power of two)
   int32_t wpr_magic;   // ceil(2^16 / wpr): wave / wpr == (wave * wpr_magic) >> 16 for wave < 64
+  // Multi-input form only (fagq_rows_parts): x = x_parts[0] + ... + x_parts[nparts - 1].
+  int32_t nparts;
+  const uint16_t* xparts[kMaxParts];
 };
 
 // ---------------------------------------------------------------- helpers
@@ -297,11 +302,12 @@ __device__ __forceinline__ void load_row(const RowRsrc& r, int lane, u32x4 (&xv)
 
 // Phase 2 for one row: r = x + residual, w = r * gamma, the fp64 sum of
 // squares, the group max of |w|; then the residual_out stores (after every
-// use of loaded data).
+// use of loaded data).  xs holds x in fp32 (one bf16 tensor, or the fp32 sum
+// of the partial tensors in the multi-input form).
 template <int NS, int LPG>
-__device__ __forceinline__ double row_in(const RowRsrc& rr, int lane, const u32x4 (&xv)[NS],
-                                         const u32x4 (&rv)[NS], const u32x4 (&gv)[NS],
-                                         float (&w)[NS][8], uint32_t (&gmax)[NS]) {
+__device__ __forceinline__ double row_in_f(const RowRsrc& rr, int lane, const float (&xs)[NS][8],
+                                           const u32x4 (&rv)[NS], const u32x4 (&gv)[NS],
+                                           float (&w)[NS][8], uint32_t (&gmax)[NS]) {
   double ss = 0.0;
   u32x4 ro[NS];
 #pragma unroll
@@ -309,8 +315,8 @@ __device__ __forceinline__ double row_in(const RowRsrc& rr, int lane, const u32x
     float r[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      r[2 * j] = bf16_lo(xv[k][j]) + bf16_lo(rv[k][j]);
-      r[2 * j + 1] = bf16_hi(xv[k][j]) + bf16_hi(rv[k][j]);
+      r[2 * j] = xs[k][2 * j] + bf16_lo(rv[k][j]);
+      r[2 * j + 1] = xs[k][2 * j + 1] + bf16_hi(rv[k][j]);
       w[k][2 * j] = r[2 * j] * bf16_lo(gv[k][j]);
       w[k][2 * j + 1] = r[2 * j + 1] * bf16_hi(gv[k][j]);
     }
@@ -330,6 +336,72 @@ __device__ __forceinline__ double row_in(const RowRsrc& rr, int lane, const u32x
   for (int k = 0; k < NS; ++k)
     __builtin_amdgcn_raw_buffer_store_b128(ro[k], rr.res_out, lane * 16 + k * 1024, 0, kNonTemporal);
   return ss;
+}
+
+template <int NS, int LPG>
+__device__ __forceinline__ double row_in(const RowRsrc& rr, int lane, const u32x4 (&xv)[NS],
+                                         const u32x4 (&rv)[NS], const u32x4 (&gv)[NS],
+                                         float (&w)[NS][8], uint32_t (&gmax)[NS]) {
+  float xs[NS][8];
+#pragma unroll
+  for (int k = 0; k < NS; ++k)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      xs[k][2 * j] = bf16_lo(xv[k][j]);
+      xs[k][2 * j + 1] = bf16_hi(xv[k][j]);
+    }
+  return row_in_f<NS, LPG>(rr, lane, xs, rv, gv, w, gmax);
+}
+
+// Multi-input form, phase 1: the row's partial tensors of x (the same row
+// and columns of each) and residual.  Parts past nparts are not loaded.
+template <int NS>
+__device__ __forceinline__ void load_row_parts(const KArgs& a, const WaveCtx& w, int64_t row,
+                                               const RowRsrc& rr, int lane,
+                                               u32x4 (&xv)[kMaxParts][NS], u32x4 (&rv)[NS]) {
+  const bool ok = row < a.M;
+  const int64_t e = (ok ? row : 0) * (int64_t)a.D + w.c0;
+  const uint32_t cols = ok ? w.cols : 0u;
+#pragma unroll
+  for (int p = 0; p < kMaxParts; ++p) {
+    if (p < a.nparts) {
+      const rsrc_t rp = make_rsrc(a.xparts[p] + e, cols * 2u);
+#pragma unroll
+      for (int k = 0; k < NS; ++k)
+        xv[p][k] = __builtin_amdgcn_raw_buffer_load_b128(rp, lane * 16 + k * 1024, 0, kNonTemporal);
+    } else {
+#pragma unroll
+      for (int k = 0; k < NS; ++k) xv[p][k] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NS; ++k)
+    rv[k] = __builtin_amdgcn_raw_buffer_load_b128(rr.res, lane * 16 + k * 1024, 0, kNonTemporal);
+}
+
+// x = ((x_0 + x_1) + ... + x_{nparts-1}) in fp32, in part order.
+template <int NS>
+__device__ __forceinline__ void sum_parts(int nparts, const u32x4 (&xv)[kMaxParts][NS],
+                                          float (&xs)[NS][8]) {
+#pragma unroll
+  for (int k = 0; k < NS; ++k)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      xs[k][2 * j] = bf16_lo(xv[0][k][j]);
+      xs[k][2 * j + 1] = bf16_hi(xv[0][k][j]);
+    }
+#pragma unroll
+  for (int p = 1; p < kMaxParts; ++p) {
+    if (p < nparts) {
+#pragma unroll
+      for (int k = 0; k < NS; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          xs[k][2 * j] = xs[k][2 * j] + bf16_lo(xv[p][k][j]);
+          xs[k][2 * j + 1] = xs[k][2 * j + 1] + bf16_hi(xv[p][k][j]);
+        }
+    }
+  }
 }
 
 // Phase 4 for one row: scales, codes, optional norm_out.
@@ -380,6 +452,39 @@ __device__ __forceinline__ void row_out(const RowRsrc& rr, int lane, uint32_t sc
   }
 }
 
+// Phase 3: a wave's partial sum of squares -> the row's inv_rms and
+// inv_rms / QMAX.  With several waves per row, the row's first wave adds the
+// partial sums (in wave order) and evaluates inv_rms once; a second barrier
+// hands it to the others.  Both barriers are fenced for LDS only, so no
+// global store has to complete before them.  Every wave of the workgroup
+// calls this (the barriers are workgroup-wide).
+template <int QF>
+__device__ __forceinline__ void row_scale(double ss, const KArgs& a, int wave, int rib, int part,
+                                          int wpr, int lane, double* s_part, float (*s_inv)[2],
+                                          float& inv, float& inv_q) {
+  constexpr float QMAX = (QF == QF_FP8) ? 448.0f : 127.0f;
+  ss = wave_sum(ss);
+  if (wpr > 1) {
+    if (lane == 0) s_part[wave] = ss;
+    lds_barrier();
+    if (part == 0) {
+      double t = 0.0;
+      for (int p = 0; p < wpr; ++p) t += s_part[rib * wpr + p];
+      const float v = row_inv_rms(t, a.D, a.eps);
+      if (lane == 0) {
+        s_inv[rib][0] = v;
+        s_inv[rib][1] = v / QMAX;
+      }
+    }
+    lds_barrier();
+    inv = s_inv[rib][0];
+    inv_q = s_inv[rib][1];
+  } else {
+    inv = row_inv_rms(ss, a.D, a.eps);
+    inv_q = inv / QMAX;
+  }
+}
+
 // Workgroup = rpb row groups of wpr waves.  Row group j of workgroup b owns
 // rows [(b * rpb + j) * RSEQ, ... + RSEQ) and processes them one after the
 // other (RSEQ is unrolled, so every wait for a load is exact).
@@ -387,7 +492,6 @@ template <int NS, int LPG, int QF, int SF, bool NORM, int RSEQ>
 __global__ void __launch_bounds__(1024)
 fagq_rows(const KArgs a) {
   static_assert(NS >= 1 && NS <= kMaxStepsPerWave, "steps per wave");
-  constexpr float QMAX = (QF == QF_FP8) ? 448.0f : 127.0f;
   constexpr int G = LPG * 8;
   constexpr uint32_t sb = SF == SF_F32 ? 4u : 1u;
   __shared__ double s_part[kMaxWavesPerBlock];
@@ -438,36 +542,64 @@ fagq_rows(const KArgs a) {
       row_rsrc_out<SF, NORM>(a, wc, row0 + i + 1, G, rn);
     }
 
-    // Phase 3: row sum of squares -> inv_rms.  With several waves per row, the
-    // row's first wave adds the partial sums (in wave order) and evaluates
-    // inv_rms once; a second barrier hands it to the others.  Both barriers
-    // are fenced for LDS only, so no global store has to complete before them.
-    ss = wave_sum(ss);
     float inv, inv_q;
-    if (wpr > 1) {
-      if (lane == 0) s_part[wave] = ss;
-      lds_barrier();
-      if (part == 0) {
-        double t = 0.0;
-        for (int p = 0; p < wpr; ++p) t += s_part[rib * wpr + p];
-        inv = row_inv_rms(t, a.D, a.eps);
-        inv_q = inv / QMAX;
-        if (lane == 0) {
-          s_inv[rib][0] = inv;
-          s_inv[rib][1] = inv_q;
-        }
-      }
-      lds_barrier();
-      inv = s_inv[rib][0];
-      inv_q = s_inv[rib][1];
-    } else {
-      inv = row_inv_rms(ss, a.D, a.eps);
-      inv_q = inv / QMAX;
-    }
+    row_scale<QF>(ss, a, wave, rib, part, wpr, lane, s_part, s_inv, inv, inv_q);
 
     row_out<NS, LPG, QF, SF, NORM>(rr, lane, scale_voff, w, gmax, inv, inv_q);
     if (i + 1 < RSEQ) rr = rn;
   }
+}
+
+// Multi-input form (the epilogue of a tensor-parallel reduction): x is the
+// sum of nparts partial tensors, one per rank, added in fp32 in rank order
+// before the residual; everything after is the operator above.  One row per
+// row group, no norm_out, at most kMaxStepsParts steps per wave (the partial
+// loads of a wave's steps are all in flight at once).
+template <int NS, int LPG, int QF, int SF>
+__global__ void __launch_bounds__(1024)
+fagq_rows_parts(const KArgs a) {
+  static_assert(NS >= 1 && NS <= kMaxStepsParts, "steps per wave");
+  constexpr int G = LPG * 8;
+  constexpr uint32_t sb = SF == SF_F32 ? 4u : 1u;
+  __shared__ double s_part[kMaxWavesPerBlock];
+  __shared__ float s_inv[kMaxWavesPerBlock][2];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wpr = a.wpr;
+  const int blk = tile_of_block((int)blockIdx.x, (int)gridDim.x, a.remap, a.remap_shift);
+  const int rib = (wave * a.wpr_magic) >> 16;
+  const int part = wave - rib * wpr;
+  const int64_t row = (int64_t)blk * a.rpb + rib;
+  WaveCtx wc;
+  wc.lane = lane;
+  wc.c0 = part * (NS * kStepCols);
+  wc.cols = a.D > wc.c0 ? (uint32_t)(a.D - wc.c0) : 0u;
+  wc.gl = lane / LPG;
+  const uint32_t scale_voff =
+      (uint32_t)wc.gl * (a.col_major ? (uint32_t)(a.M * (int64_t)sb) : sb);
+
+  u32x4 xv[kMaxParts][NS], rv[NS];
+  RowRsrc rr;
+  row_rsrc_in(a, wc, row, rr);
+  load_row_parts<NS>(a, wc, row, rr, lane, xv, rv);
+  u32x4 gv[NS];
+  {
+    const rsrc_t rg = make_rsrc(a.gamma + wc.c0, wc.cols * 2u);
+#pragma unroll
+    for (int k = 0; k < NS; ++k)
+      gv[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, lane * 16 + k * 1024, 0, 0);
+  }
+  row_rsrc_out<SF, false>(a, wc, row, G, rr);
+
+  float xs[NS][8];
+  sum_parts<NS>(a.nparts, xv, xs);
+  float w[NS][8];
+  uint32_t gmax[NS];
+  const double ss = row_in_f<NS, LPG>(rr, lane, xs, rv, gv, w, gmax);
+  float inv, inv_q;
+  row_scale<QF>(ss, a, wave, rib, part, wpr, lane, s_part, s_inv, inv, inv_q);
+  row_out<NS, LPG, QF, SF, false>(rr, lane, scale_voff, w, gmax, inv, inv_q);
 }
 
 // ---------------------------------------------------------------- diagnostics

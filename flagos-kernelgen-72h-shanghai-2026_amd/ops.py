@@ -179,6 +179,67 @@ def fused_add_rmsnorm_group_quant_fn(
     return residual_out, q, scale
 
 
+def fused_reduce_add_rmsnorm_group_quant(
+    x_parts,
+    residual: torch.Tensor,
+    weight: torch.Tensor,
+    eps: float = 1e-6,
+    group_size: int = 128,
+    out_dtype: torch.dtype = _FP8,
+    *,
+    scale_col_major: bool = False,
+    scale_ue8m0: bool = False,
+    rounding: str = "rne",
+    inplace_residual: bool = False,
+):
+    """Multi-input form (the epilogue of a tensor-parallel reduction): x is the
+    sum of the partial tensors in ``x_parts`` (1 to 8 bf16 [M, D] tensors, one per
+    rank), added in fp32 in list order before the residual and never rounded to
+    bf16.  Returns ``(residual_out, q, scale)`` like the functional form; with one
+    part the outputs equal it bit for bit.  C ABI: ``fagq_launch_parts``.
+
+    No counterpart in the reference (its operator takes one x,
+    src/task01_fused_add_rmsnorm_group_quant.py:1731-1741).
+    """
+    parts = list(x_parts)
+    if not 1 <= len(parts) <= 8:
+        raise ValueError(f"x_parts must hold 1 to 8 tensors, got {len(parts)}")
+    x0 = parts[0]
+    if x0.dim() != 2:
+        raise ValueError(f"x_parts[0] must be 2-D [M, D], got shape {tuple(x0.shape)}")
+    if not x0.is_cuda:
+        raise ValueError("x_parts must be GPU (HIP) tensors; this operator has no CPU path")
+    M, D = (int(s) for s in x0.shape)
+    device = x0.device
+    for i, t in enumerate(parts):
+        _check_rows(f"x_parts[{i}]", t, (M, D), device)
+    _check_rows("residual", residual, (M, D), device)
+    _check_rows("weight", weight, (D,), device)
+    group_size = int(group_size)
+    if group_size <= 0 or D % group_size != 0:
+        raise ValueError(f"group_size {group_size} must divide D = {D}")
+    residual_out = residual if inplace_residual else torch.empty_like(residual)
+    q = torch.empty((M, D), dtype=out_dtype, device=device)
+    scale = empty_scales(M, D // group_size, ue8m0=scale_ue8m0, col_major=scale_col_major,
+                         device=device)
+    qf = _q_format(q)
+    sf = _scale_format(scale)
+    layout = _scale_layout(scale, M, D // group_size)
+    rnd = _rounding(None if out_dtype == _FP8 else rounding, qf)
+    if M == 0:
+        return residual_out, q, scale
+    lib = _lib.load()
+    arr = (ctypes.c_void_p * len(parts))(*[t.data_ptr() for t in parts])
+    stream = torch.cuda.current_stream(device).cuda_stream
+    with torch.cuda.device(device):
+        st = lib.fagq_launch_parts(ctypes.cast(arr, ctypes.c_void_p), len(parts), _ptr(residual),
+                                   _ptr(weight), _ptr(residual_out), _ptr(q), _ptr(scale), M, D,
+                                   group_size, float(eps), qf, sf, layout, rnd,
+                                   ctypes.c_void_p(stream))
+    _lib.check(st, "fagq_launch_parts")
+    return residual_out, q, scale
+
+
 def route_for(M: int, D: int, group_size: int = 128) -> dict:
     """The launch mapping the library chooses for a shape."""
     return _lib.query_route(M, D, group_size)

@@ -147,3 +147,44 @@ def make_gemm_inputs(w: GemmWorkload, M: int | None = None):
     a_s = scales((kb, M), w.a_scale)
     b_s = scales((nb, kb), w.b_scale)
     return a_q, a_s, b_q, b_s
+
+
+# --------------------------------------------- multi-input form (TP epilogue)
+
+@dataclass(frozen=True)
+class PartsWorkload:
+    """The multi-input form at one rank's shard of a tensor-parallel layer: nparts
+    partial tensors [M, D] (one per rank) summed before the residual."""
+    name: str
+    M: int
+    D: int
+    nparts: int
+    group_size: int = 128
+    seed: int = 0
+
+    def algorithmic_bytes(self) -> int:
+        """Read nparts partials, residual (bf16) and gamma; write residual_out
+        (bf16), fp8 codes and fp32 scales."""
+        N = self.M * self.D
+        return (2 * self.nparts * N + 2 * N + 2 * self.D + 2 * N + N
+                + 4 * self.M * (self.D // self.group_size))
+
+
+# DeepSeek-V3 width at the headline batch, sharded over 8 ranks: each rank
+# reduces and normalizes 16384 / 8 = 2048 rows from 8 partial sums.
+PARTS_CONFIGS = {
+    "tp8_shard_2048x7168": PartsWorkload("tp8_shard_2048x7168", 2048, 7168, 8),
+    "tp4_shard_4096x7168": PartsWorkload("tp4_shard_4096x7168", 4096, 7168, 4),
+}
+
+
+def make_parts_inputs(w: PartsWorkload):
+    """(parts, residual, weight) bf16 CPU tensors: partial sums N(0, 1/nparts)
+    (so their sum is ~N(0, 1)), residual N(0, 1), weight 1 + 0.1 N(0, 1)."""
+    g = torch.Generator(device="cpu").manual_seed(w.seed)
+    sd = 1.0 / w.nparts ** 0.5
+    parts = [(sd * torch.randn(w.M, w.D, generator=g)).to(torch.bfloat16)
+             for _ in range(w.nparts)]
+    res = torch.randn(w.M, w.D, generator=g).to(torch.bfloat16)
+    weight = (1.0 + 0.1 * torch.randn(w.D, generator=g)).to(torch.bfloat16)
+    return parts, res, weight

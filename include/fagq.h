@@ -110,6 +110,36 @@ FAGQ_API int fagq_launch(const void* x, const void* residual, const void* gamma,
                          int q_format, int scale_format, int scale_layout,
                          int rounding, void* stream);
 
+/* Multi-input form: the epilogue of a tensor-parallel reduction.  x is the
+ * sum of nparts partial tensors (one per rank of a row-parallel layer, e.g.
+ * the contributions a reduce-scatter gathers for this rank's rows), added in
+ * fp32 in index order before the residual:
+ *
+ *   r = ((x_parts[0] + x_parts[1]) + ... + x_parts[nparts - 1]) + residual
+ *
+ * and everything after r is fagq_launch's definition.  The sum is never
+ * rounded to bf16.  With nparts == 1 the outputs equal
+ * fagq_launch(x_parts[0], ...) bit for bit.
+ *
+ * No counterpart in the reference: its operator takes one x
+ * (src/task01_fused_add_rmsnorm_group_quant.py:1731-1741).  This is the
+ * producer side of the path for tensor-parallel layers.
+ *
+ *   x_parts          host array of nparts device pointers, each bf16 [M, D],
+ *                    16-byte aligned; 1 <= nparts <= FAGQ_MAX_PARTS
+ *   residual_out     may be exactly residual; must not overlap any part
+ *   3-output form (no norm_out); D <= FAGQ_MAX_D_PARTS; other arguments as
+ *   for fagq_launch.
+ */
+#define FAGQ_MAX_PARTS 8
+#define FAGQ_MAX_D_PARTS 16384
+
+FAGQ_API int fagq_launch_parts(const void* const* x_parts, int nparts, const void* residual,
+                               const void* gamma, void* residual_out, void* q, void* scale,
+                               int64_t M, int64_t D, int64_t group_size, float eps,
+                               int q_format, int scale_format, int scale_layout, int rounding,
+                               void* stream);
+
 /* Route description chosen by fagq_launch for a shape (for tests and the
  * benchmark).  waves_per_row * steps_per_wave * 512 >= D. */
 typedef struct fagq_route {

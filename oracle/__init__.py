@@ -55,6 +55,8 @@ def lib() -> ctypes.CDLL:
         L.orc_ceil_log2.restype = None
         L.orc_fagq.argtypes = [P, P, P, P, P, P, P, I64, I64, I64, F, I, I, I, I, I]
         L.orc_fagq.restype = I
+        L.orc_fagq_parts.argtypes = [P, I] + [P] * 6 + [I64, I64, I64, F, I, I, I, I, I]
+        L.orc_fagq_parts.restype = I
         L.orc_e4m3fn_to_f64.argtypes = [P, P, I64]
         L.orc_e4m3fn_to_f64.restype = None
         L.orc_gemm.argtypes = [P, P, P, P, P, P, I64, I64, I64, I, I, I, I]
@@ -165,3 +167,29 @@ def gemm(a_q: np.ndarray, a_scale: np.ndarray, b_q: np.ndarray, b_scale: np.ndar
     if st != 0:
         raise ValueError(f"oracle rejected the arguments (status {st})")
     return c, bound
+
+
+def fagq_parts(x_parts, residual: np.ndarray, gamma: np.ndarray, eps: float, group_size: int,
+               q_format: int = Q_FP8, scale_format: int = S_F32, scale_layout: int = L_ROW,
+               rounding: int = R_RNE, nthreads: int = 0) -> dict:
+    """The multi-input form: x is the sum of the partial tensors in x_parts
+    (uint16 bf16 bits, each [M, D]), added in fp32 in list order before the
+    residual.  Returns residual_out, q and scale like fagq()."""
+    parts = [np.ascontiguousarray(p, dtype=np.uint16) for p in x_parts]
+    residual = np.ascontiguousarray(residual, dtype=np.uint16)
+    gamma = np.ascontiguousarray(gamma, dtype=np.uint16)
+    M, D = residual.shape
+    assert all(p.shape == (M, D) for p in parts) and gamma.shape == (D,)
+    groups = D // group_size
+    res_out = np.empty((M, D), np.uint16)
+    q = np.empty((M, D), np.uint8)
+    sdt = np.float32 if scale_format == S_F32 else np.uint8
+    scale = np.empty((groups, M) if scale_layout == L_COL else (M, groups), sdt)
+    arr = (ctypes.c_void_p * len(parts))(*[p.ctypes.data for p in parts])
+    st = lib().orc_fagq_parts(ctypes.cast(arr, ctypes.c_void_p), len(parts), _ptr(residual),
+                              _ptr(gamma), _ptr(res_out), None, _ptr(q), _ptr(scale), M, D,
+                              group_size, float(eps), q_format, scale_format, scale_layout,
+                              rounding, nthreads)
+    if st != 0:
+        raise ValueError(f"oracle rejected the arguments (status {st})")
+    return {"residual_out": res_out, "q": q, "scale": scale}

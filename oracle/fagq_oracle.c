@@ -119,14 +119,19 @@ ORC_API void orc_ceil_log2(const float* in, int32_t* out, int64_t n) {
 /* ---- the operator ---- */
 
 /*
- * Same argument meaning as fagq_launch (include/fagq.h), host pointers.
+ * Same argument meaning as fagq_launch_parts (include/fagq.h), host pointers:
+ * x is the sum of nparts partial tensors x_parts[0..nparts-1], added in fp32
+ * in index order, r = ((x_0 + x_1) + ... + x_{P-1}) + residual.  With one part
+ * this is the operator's r = fp32(x) + fp32(residual) (task01.py:88-89).
  * norm_out may be NULL.  nthreads <= 0 uses the OpenMP default.
  * Returns 0, or 1 on an argument this restatement does not accept.
  */
-ORC_API int orc_fagq(const uint16_t* x, const uint16_t* residual, const uint16_t* gamma,
-                     uint16_t* residual_out, uint16_t* norm_out, uint8_t* q, void* scale,
-                     int64_t M, int64_t D, int64_t G, float eps, int q_format,
-                     int scale_format, int scale_layout, int rounding, int nthreads) {
+ORC_API int orc_fagq_parts(const uint16_t* const* x_parts, int nparts, const uint16_t* residual,
+                           const uint16_t* gamma, uint16_t* residual_out, uint16_t* norm_out,
+                           uint8_t* q, void* scale, int64_t M, int64_t D, int64_t G, float eps,
+                           int q_format, int scale_format, int scale_layout, int rounding,
+                           int nthreads) {
+  if (nparts < 1 || nparts > 8) return 1;
   if (M < 0 || D <= 0 || G <= 0 || D % G != 0) return 1;
   if (q_format == Q_FP8 && rounding != R_RNE) return 1;
   const float qmax = q_format == Q_FP8 ? 448.0f : 127.0f;
@@ -141,12 +146,13 @@ ORC_API int orc_fagq(const uint16_t* x, const uint16_t* residual, const uint16_t
     } else {
 #pragma omp for schedule(static)
       for (int64_t m = 0; m < M; ++m) {
-        const uint16_t* xr = x + m * D;
         const uint16_t* rr = residual + m * D;
         uint16_t* ro = residual_out + m * D;
         double ss = 0.0;
         for (int64_t j = 0; j < D; ++j) {
-          const float r = bf16_to_f32(xr[j]) + bf16_to_f32(rr[j]);
+          float xs = bf16_to_f32(x_parts[0][m * D + j]);
+          for (int p = 1; p < nparts; ++p) xs = xs + bf16_to_f32(x_parts[p][m * D + j]);
+          const float r = xs + bf16_to_f32(rr[j]);
           ro[j] = f32_to_bf16(r);
           ss += (double)r * (double)r;
           w[j] = r * bf16_to_f32(gamma[j]);
@@ -183,4 +189,14 @@ ORC_API int orc_fagq(const uint16_t* x, const uint16_t* residual, const uint16_t
     }
   }
   return ok;
+}
+
+/* The operator (task01.py:1731-1741 semantics): one x tensor. */
+ORC_API int orc_fagq(const uint16_t* x, const uint16_t* residual, const uint16_t* gamma,
+                     uint16_t* residual_out, uint16_t* norm_out, uint8_t* q, void* scale,
+                     int64_t M, int64_t D, int64_t G, float eps, int q_format,
+                     int scale_format, int scale_layout, int rounding, int nthreads) {
+  const uint16_t* parts[1] = {x};
+  return orc_fagq_parts(parts, 1, residual, gamma, residual_out, norm_out, q, scale, M, D, G,
+                        eps, q_format, scale_format, scale_layout, rounding, nthreads);
 }
