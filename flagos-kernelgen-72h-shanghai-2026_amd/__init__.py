@@ -8,12 +8,14 @@ registers it as ``fagq_mi355x``.
 """
 from . import _lib
 from ._lib import FagqError, load as load_library
+from .dsa_topk import dsa_topk_page_table_transform
 from .gemm import fp8_block_scaled_gemm, gemm_route
 from .ops import (empty_scales, fused_add_rmsnorm_group_quant, fused_add_rmsnorm_group_quant_fn,
                   fused_reduce_add_rmsnorm_group_quant, route_for)
 
 __all__ = [
     "FagqError",
+    "dsa_topk_page_table_transform",
     "empty_scales",
     "fp8_block_scaled_gemm",
     "fused_add_rmsnorm_group_quant",

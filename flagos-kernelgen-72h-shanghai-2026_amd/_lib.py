@@ -1,5 +1,5 @@
 """ctypes binding of libfagq.so (the C ABI declared in include/fagq.h,
-include/fagq_gemm.h and include/fagq_diag.h).
+include/fagq_gemm.h, include/fagq_dsa.h and include/fagq_diag.h).
 
 The library is loaded after ``import torch`` so that its libamdhip64.so.7
 dependency resolves to the HIP runtime torch already loaded (same soname);
@@ -57,6 +57,7 @@ SIGNATURES = {
     "fagq_version": ([], _I),
     "fagq_diag_encode": ([_P, _P, _I64, _I, _I, _P], _I),
     "fagq_diag_copy": ([_P, _P, _I64, _P], _I),
+    "fagq_dsa_topk_launch": ([_P, _I, _P, _P, _P, _I, _P, _P] + [_I64] * 6 + [_P], _I),
     "fagq_gemm_launch": ([_P] * 5 + [_I64, _I64, _I64, _I, _I, _I, _P], _I),
     "fagq_gemm_query_route": ([_I64, _I64, _I64, ctypes.POINTER(GemmRoute)], _I),
 }

@@ -188,3 +188,76 @@ def make_parts_inputs(w: PartsWorkload):
     res = torch.randn(w.M, w.D, generator=g).to(torch.bfloat16)
     weight = (1.0 + 0.1 * torch.randn(w.D, generator=g)).to(torch.bfloat16)
     return parts, res, weight
+
+
+# ------------------------------------------ Task 02: DSA top-k page table
+
+@dataclass(frozen=True)
+class DsaWorkload:
+    """scores[B, H, Q, NB] -> top_k block ids and pages per query row."""
+    name: str
+    B: int
+    H: int
+    Q: int
+    NB: int
+    top_k: int
+    block_size: int
+    dtype: torch.dtype = torch.float32
+    seed: int = 0
+
+    @property
+    def rows(self) -> int:
+        return self.B * self.H * self.Q
+
+    def algorithmic_bytes(self, valid_blocks_total: int) -> int:
+        """Scores of the valid prefixes (read once), two int32 outputs per
+        rank, one int32 page-table read per written page, q_pos/kv_lens."""
+        esz = 2 if self.dtype == torch.bfloat16 else 4
+        return (esz * valid_blocks_total + 12 * self.rows * self.top_k
+                + 4 * self.B * self.Q + 4 * self.B)
+
+
+def _dsa(B, H, Q, NB, K, BS, dtype=torch.float32):
+    tag = "bf16" if dtype == torch.bfloat16 else "f32"
+    name = f"dsa_{tag}_b{B}h{H}q{Q}_nb{NB}_k{K}_bs{BS}"
+    return name, DsaWorkload(name, B, H, Q, NB, K, BS, dtype)
+
+
+# The (B, H, Q, NB, top_k, block_size) shapes the reference routes
+# (src/task02_dsa_topk_page_table_transform.py:1668-1672), fp32 scores.
+DSA_CONFIGS = dict(_dsa(*c) for c in [
+    (2, 32, 512, 4096, 128, 64), (1, 32, 1024, 4096, 128, 64), (4, 16, 512, 4096, 128, 64),
+    (1, 32, 512, 2048, 64, 128), (2, 16, 512, 2048, 64, 128), (1, 32, 1024, 2048, 64, 64),
+    (1, 8, 128, 512, 32, 128), (2, 8, 128, 512, 32, 128), (1, 16, 256, 1024, 32, 128),
+    (2, 16, 256, 1024, 64, 128),
+])
+DSA_CONFIGS.update(dict([_dsa(2, 32, 512, 4096, 128, 64, torch.bfloat16)]))
+DSA_HEADLINE = "dsa_f32_b2h32q512_nb4096_k128_bs64"
+
+
+def make_dsa_inputs(w: DsaWorkload):
+    """(scores, page_table, q_pos, kv_lens) CPU tensors.  Scores N(0, 1) in the
+    workload's dtype; kv_len[b] = NB * block_size - 3 b block_size (at least 1);
+    query q of batch b at position (q + 1) kv_len / Q - 1, so the causal prefixes
+    of a batch's rows spread evenly from ~kv_len/Q to kv_len tokens;
+    page_table[b] a random permutation of physical pages b * NB ...  int32."""
+    g = torch.Generator(device="cpu").manual_seed(w.seed)
+    scores = torch.randn(w.B, w.H, w.Q, w.NB, generator=g).to(w.dtype)
+    kv = torch.tensor([max(1, w.NB * w.block_size - 3 * b * w.block_size) for b in range(w.B)],
+                      dtype=torch.int32)
+    q = torch.arange(w.Q, dtype=torch.int64)
+    q_pos = torch.stack([((q + 1) * int(kv[b]) // w.Q - 1) for b in range(w.B)]).to(torch.int32)
+    page_table = torch.stack([b * w.NB + torch.randperm(w.NB, generator=g)
+                              for b in range(w.B)]).to(torch.int32)
+    return scores, page_table, q_pos, kv
+
+
+def dsa_valid_blocks(w: DsaWorkload, q_pos: torch.Tensor, kv_lens: torch.Tensor) -> int:
+    """Total selectable-prefix length over all rows (the blocks a kernel must read)."""
+    kv = kv_lens.to(torch.int64)
+    vb = torch.clamp((kv + w.block_size - 1) // w.block_size, max=w.NB)          # [B]
+    pos = q_pos.to(torch.int64)
+    last = torch.minimum(torch.where(pos >= 0, pos // w.block_size, torch.full_like(pos, -1)),
+                         (vb - 1)[:, None])
+    per_row = torch.clamp(last + 1, min=0)                                         # [B, Q]
+    return int(per_row.sum()) * w.H

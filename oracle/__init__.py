@@ -16,6 +16,8 @@ src/task01_fused_add_rmsnorm_group_quant.py:65-121 and :1066-1348):
 * ``gemm`` - gemm_oracle.c, the fp8 block-scaled GEMM that consumes the
   operator's codes and scales (no reference counterpart; its definition is
   in include/fagq_gemm.h).
+* ``dsa_topk`` - dsa_topk_oracle.c, the Task 02 DSA top-k page-table
+  transform (src/task02_dsa_topk_page_table_transform.py:154-175).
 
 bf16 tensors are passed as their uint16 bit patterns.
 """
@@ -61,6 +63,8 @@ def lib() -> ctypes.CDLL:
         L.orc_e4m3fn_to_f64.restype = None
         L.orc_gemm.argtypes = [P, P, P, P, P, P, I64, I64, I64, I, I, I, I]
         L.orc_gemm.restype = I
+        L.orc_dsa_topk.argtypes = [P, I, P, P, P, I, P, P, I64, I64, I64, I64, I64, I64, I]
+        L.orc_dsa_topk.restype = I
         _lib = L
     return _lib
 
@@ -193,3 +197,29 @@ def fagq_parts(x_parts, residual: np.ndarray, gamma: np.ndarray, eps: float, gro
     if st != 0:
         raise ValueError(f"oracle rejected the arguments (status {st})")
     return {"residual_out": res_out, "q": q, "scale": scale}
+
+
+def dsa_topk(scores: np.ndarray, page_table: np.ndarray, q_pos: np.ndarray, kv_lens: np.ndarray,
+             block_size: int, top_k: int, nthreads: int = 0) -> tuple[np.ndarray, np.ndarray]:
+    """scores [B, H, Q, NB] float32, or uint16 holding bf16 bits; page_table int32
+    [B, NB]; q_pos [B, Q] and kv_lens [B] int32 or int64.  Returns (out_blocks,
+    out_pages), int32 [B, H, Q, top_k]."""
+    import os
+    scores = np.ascontiguousarray(scores)
+    assert scores.dtype in (np.float32, np.uint16) and scores.ndim == 4
+    B, H, Q, NB = scores.shape
+    page_table = np.ascontiguousarray(page_table, dtype=np.int32)
+    assert page_table.shape == (B, NB)
+    idx64 = q_pos.dtype == np.int64
+    idt = np.int64 if idx64 else np.int32
+    q_pos = np.ascontiguousarray(q_pos, dtype=idt)
+    kv_lens = np.ascontiguousarray(kv_lens, dtype=idt)
+    assert q_pos.shape == (B, Q) and kv_lens.shape == (B,)
+    ob = np.empty((B, H, Q, top_k), np.int32)
+    op = np.empty((B, H, Q, top_k), np.int32)
+    st = lib().orc_dsa_topk(_ptr(scores), int(scores.dtype == np.uint16), _ptr(page_table),
+                            _ptr(q_pos), _ptr(kv_lens), int(idx64), _ptr(ob), _ptr(op), B, H, Q,
+                            NB, block_size, top_k, nthreads or min(8, os.cpu_count() or 1))
+    if st != 0:
+        raise ValueError(f"oracle rejected the arguments (status {st})")
+    return ob, op

@@ -1,6 +1,7 @@
 """Builds the C oracle (test infrastructure) into oracle/libfagq_oracle.so:
-fagq_oracle.c (the operator) and gemm_oracle.c (the fp8 block-scaled GEMM
-that consumes the operator's output).
+fagq_oracle.c (the operator), gemm_oracle.c (the fp8 block-scaled GEMM that
+consumes the operator's output) and dsa_topk_oracle.c (the Task 02 DSA top-k
+page-table transform).
 
 The oracle restates the reference's algorithm on the CPU and is used only as
 the checker by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
@@ -14,7 +15,7 @@ import subprocess
 from pathlib import Path
 
 ORACLE_DIR = Path(__file__).resolve().parent
-SRCS = [ORACLE_DIR / "fagq_oracle.c", ORACLE_DIR / "gemm_oracle.c"]
+SRCS = [ORACLE_DIR / "fagq_oracle.c", ORACLE_DIR / "gemm_oracle.c", ORACLE_DIR / "dsa_topk_oracle.c"]
 LIB = ORACLE_DIR / "libfagq_oracle.so"
 
 CFLAGS = ["-O2", "-std=gnu11", "-fPIC", "-shared", "-fopenmp", "-ffp-contract=off",
