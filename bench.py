@@ -25,6 +25,10 @@ Prints one JSON line:
 shard of a tensor-parallel layer: nparts partial sums reduced, normalized and
 quantized (fp8, fp32 column-major scales); cpu_baseline = the C oracle.
 
+--config dsa_*: the Task 02 DSA top-k page-table transform
+(fagq_dsa_topk_launch); value = algorithmic GB/s (valid score prefixes read
+once, outputs and page gathers), also rows/s; cpu_baseline = the C oracle.
+
 --config gemm_*: the fp8 block-scaled GEMM that consumes the operator's
 output (fagq_gemm_launch); value and roofline in TFLOP/s against MI355X's
 5.0 PFLOP/s dense fp8 peak, cpu_baseline = the C oracle (oracle/gemm_oracle.c)
@@ -118,7 +122,9 @@ def main() -> int:
     if args.copy:
         return copy_bench(args, torch, pkg)
     name = args.config or HEADLINE
-    from fagq_mi355x.workloads import GEMM_CONFIGS, PARTS_CONFIGS
+    from fagq_mi355x.workloads import DSA_CONFIGS, GEMM_CONFIGS, PARTS_CONFIGS
+    if name in DSA_CONFIGS:
+        return dsa_bench(args, torch, pkg, DSA_CONFIGS[name])
     if name in GEMM_CONFIGS:
         return gemm_bench(args, torch, pkg, GEMM_CONFIGS[name])
     if name in PARTS_CONFIGS:
@@ -430,6 +436,123 @@ def parts_cpu_baseline(w, parts, res, gamma, gpu_set, args, torch) -> dict:
             "sample": f"first {rows} of {w.M} rows of {w.name}, C oracle (oracle.fagq_parts, "
                       f"OpenMP), median of {len(times)} runs",
             "parity_vs_gpu_rows": parity}
+
+
+def dsa_bench(args, torch, pkg, w) -> int:
+    """Times fagq_dsa_topk_launch (inputs resident in HBM, sets rotated past the
+    MALL), kernel time by HIP events on the launch stream."""
+    import ctypes
+    from fagq_mi355x import _lib
+    from fagq_mi355x.workloads import dsa_valid_blocks, make_dsa_inputs
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = _lib.load()
+    scores, pt, pos, kv = make_dsa_inputs(w)
+    nbytes = w.algorithmic_bytes(dsa_valid_blocks(w, pos, kv))
+    full = scores.numel() * scores.element_size()
+    nsets = max(2, min(16, math.ceil(ROTATE_BYTES / full) + 1))
+    s0, pt_d, pos_d, kv_d = scores.to(dev), pt.to(dev), pos.to(dev), kv.to(dev)
+    sets = []
+    for i in range(nsets):
+        s = s0 if i == 0 else s0.clone()
+        ob = torch.empty(w.B, w.H, w.Q, w.top_k, dtype=torch.int32, device=dev)
+        sets.append((s, ob, torch.empty_like(ob)))
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    sdt = 1 if w.dtype == torch.bfloat16 else 0
+
+    def step(i: int):
+        s, ob, op = sets[i % nsets]
+        st = lib.fagq_dsa_topk_launch(P(s), sdt, P(pt_d), P(pos_d), P(kv_d), 0, P(ob), P(op),
+                                      w.B, w.H, w.Q, w.NB, w.block_size, w.top_k, sp)
+        if st:
+            _lib.check(st, "fagq_dsa_topk_launch")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize(dev)
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    for i in range(args.steps):
+        starts[i].record(stream)
+        step(i)
+        ends[i].record(stream)
+    torch.cuda.synchronize(dev)
+    durs = sorted(a.elapsed_time(b) for a, b in zip(starts, ends))
+    kern_ms = sum(durs) / len(durs)
+    value = nbytes / (wall_ms * 1e-3) / 1e9
+    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    out = {
+        "metric": "DSA top-k page-table transform: algorithmic GB/s (% of 8 TB/s) + us/call",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32" if w.dtype == torch.float32 else "bf16 (compared as f32)",
+        "data": "synthetic",
+        "config": {"workload": w.name, "B": w.B, "H": w.H, "Q": w.Q, "NB": w.NB,
+                   "top_k": w.top_k, "block_size": w.block_size, "rows": w.rows,
+                   "algorithmic_bytes": nbytes, "buffer_sets": nsets},
+        "us_per_call": round(kern_ms * 1e3, 2),
+        "us_per_call_median": round(durs[len(durs) // 2] * 1e3, 2),
+        "us_per_call_host_wall": round(wall_ms * 1e3, 2),
+        "rows_per_s": round(w.rows / (kern_ms * 1e-3), 1),
+        "pct_of_peak": round(100.0 * achieved / PEAK_HBM_GBS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None},
+        "cpu_baseline": None,
+    }
+    if args.cpu_seconds > 0:
+        out["cpu_baseline"] = dsa_cpu_baseline(w, scores, pt, pos, kv, sets[0], nbytes, args, torch)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def dsa_cpu_baseline(w, scores, pt, pos, kv, gpu_set, nbytes, args, torch) -> dict:
+    """Times the C oracle on the rows of the first (b, h) head block and
+    checks those GPU rows against it."""
+    import numpy as np
+    import oracle
+    threads = max(1, min(16, os.cpu_count() or 1))
+    rows = min(w.Q, w.rows)
+    sub = scores[:1, :1]
+    s_np = sub.contiguous().view(torch.uint16).numpy() if w.dtype == torch.bfloat16 else \
+        sub.contiguous().numpy()
+    pt_np, pos_np, kv_np = pt[:1].numpy(), pos[:1].numpy(), kv[:1].numpy()
+
+    def run():
+        return oracle.dsa_topk(s_np, pt_np, pos_np, kv_np, w.block_size, w.top_k, nthreads=threads)
+
+    rb, rp = run()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < args.cpu_seconds and len(times) < 1000):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    t = times[len(times) // 2]
+    _, ob, op = gpu_set
+    torch.cuda.synchronize()
+    ok = bool(np.array_equal(ob[:1, :1].cpu().numpy(), rb) and np.array_equal(op[:1, :1].cpu().numpy(), rp))
+    sample_bytes = nbytes * rows / w.rows
+    return {"value": round(sample_bytes / t / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port", "us_per_call": round(t * 1e6, 1),
+            "sample": f"the {rows} query rows of head (0, 0) of {w.name} ({rows} of {w.rows} rows), "
+                      f"C oracle (OpenMP), median of {len(times)} runs; GB/s scaled by the rows' "
+                      f"share of the algorithmic bytes",
+            "parity_vs_gpu_rows": {"ok": ok}}
 
 
 def gemm_bench(args, torch, pkg, w) -> int:

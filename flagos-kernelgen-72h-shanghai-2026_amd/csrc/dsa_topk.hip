@@ -8,26 +8,30 @@
 // and the first top_k block ids and their page_table[b, id] entries are
 // written (-1 past the number of selectable blocks).
 //
-// Work mapping.  One wave per row, four rows per workgroup.  A lane holds
-// EPL scores of the row in VGPRs (NB <= 64 * EPL), loaded as 16-byte vectors
-// through a buffer descriptor sized to the row's valid prefix: blocks past
-// it are never fetched.
+// Work mapping.  One workgroup per row, one wave per 1024 blocks of it (up
+// to 4 waves); a lane holds 16 scores in VGPRs, loaded as 16-byte vectors
+// through a buffer descriptor sized to the row's valid prefix, so blocks past
+// it are never fetched.  Cross-lane steps use DPP and v_permlane16/32_swap
+// (VALU, no LDS round trip); the waves of a row combine through a few LDS
+// words and workgroup barriers, and every decision is computed identically
+// by all of them.
 //
 // Selection is exact and never sorts the whole row:
-//   * Every selectable block has a 64-bit composite key, (ordered score bits
-//     << 32) | (0xffffffff - id): larger is better, so the order is score
-//     descending then id ascending, -0 and +0 mapped to one key.
+//   * Every selectable block has a 32-bit ordered key of its score (larger
+//     is better, -0 and +0 one key, 0 for blocks that are not selectable)
+//     and a 64-bit composite key (key << 32) | (0xffffffff - id): the order
+//     is score descending, then id ascending.
 //   * If at most CAP (512) blocks are selectable they are all candidates.
-//   * Otherwise a 256-bin histogram in LDS, over the scores' fp32 range (the
-//     bin is a monotone function of the score), locates the bin holding the
-//     top_k-th block; the blocks above it are in the result and the bin is
-//     the new search range, kept as [lo, hi] bounds on the composite key.
-//     While more than CAP blocks lie at or above the range, the range is
-//     split again by a 256-bin histogram on the composite key itself, which
-//     always separates its smallest and largest keys, so the loop ends.
-//   * The candidates (composite key >= lo, at most CAP) are compacted to
-//     LDS, bitonic-sorted in registers across the wave (descending), and the
-//     first top_k are written together with their page-table entries.
+//   * Otherwise a 256-bin histogram in LDS over the scores' fp32 range (the
+//     bin is a monotone function of the score) locates the bin holding the
+//     top_k-th block; with that bin and all higher ones at most CAP blocks,
+//     those are the candidates.  Otherwise the bin becomes a search range
+//     [lo, hi] on the composite key and is split again by 256-bin histograms
+//     on the composite key, which always separate the range's smallest and
+//     largest keys, so the loop ends.
+//   * The candidates are compacted to LDS, bitonic-sorted in registers
+//     across one wave (descending), and the first top_k are written with
+//     their page-table entries.
 // For Gaussian-like scores the fp32 histogram leaves a handful of blocks in
 // the boundary bin, so a row costs one histogram and a sort of about top_k
 // keys.
@@ -42,11 +46,13 @@ namespace fagq {
 namespace dsa {
 namespace {
 
-constexpr int kRowsPerBlock = 4;
-constexpr int kThreads = 64 * kRowsPerBlock;
+constexpr int kEPL = 16;                    // scores per lane
+constexpr int kChunk = 64 * kEPL;            // blocks per wave
+constexpr int kMaxWaves = FAGQ_DSA_MAX_NB / kChunk;
 constexpr int kBins = 256;
-constexpr int kCap = 512;            // candidates sorted at most
+constexpr int kCap = 512;                    // candidates sorted at most
 constexpr int kMaxTopK = FAGQ_DSA_MAX_TOP_K;
+static_assert(kMaxWaves * kChunk == FAGQ_DSA_MAX_NB, "waves per row");
 
 struct DArgs {
   const void* scores;
@@ -55,7 +61,6 @@ struct DArgs {
   const void* kv_lens;
   int32_t* out_blocks;
   int32_t* out_pages;
-  int64_t rows;          // B * H * Q
   int32_t H, Q, NB;
   int32_t block_size;
   int32_t top_k;
@@ -63,49 +68,71 @@ struct DArgs {
 };
 
 struct Lds {
-  uint32_t hist[kRowsPerBlock][kBins];
-  uint64_t cand[kRowsPerBlock][kCap];
+  uint32_t hist[kBins];
+  uint64_t cand[kCap];
+  uint32_t slot[2][kMaxWaves][4];   // per-wave partials (two sets, alternating)
 };
 
 // --------------------------------------------------------- wave primitives
 
-__device__ __forceinline__ uint32_t shfl_xor_u32(uint32_t v, int m) {
-  return (uint32_t)__shfl_xor((int)v, m, 64);
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
 }
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-  return (uint64_t)shfl_xor_u32((uint32_t)v, m) | ((uint64_t)shfl_xor_u32((uint32_t)(v >> 32), m) << 32);
+
+// Value of lane (lane ^ m), m a power of two below 64.
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v, int m, int lane) {
+  switch (m) {
+    case 1: return dpp<0xB1>(v);                      // quad_perm [1,0,3,2]
+    case 2: return dpp<0x4E>(v);                      // quad_perm [2,3,0,1]
+    case 4: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (4 << 10));
+    case 8: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (8 << 10));
+    case 16: {
+      const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+      return (lane & 16) ? r[0] : r[1];
+    }
+    default: {
+      const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+      return (lane & 32) ? r[0] : r[1];
+    }
+  }
 }
-__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) v += shfl_xor_u32(v, m);
-  return v;
+__device__ __forceinline__ uint64_t xor_lane64(uint64_t v, int m, int lane) {
+  return (uint64_t)xor_lane((uint32_t)v, m, lane) |
+         ((uint64_t)xor_lane((uint32_t)(v >> 32), m, lane) << 32);
 }
-__device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) v = __builtin_fmaxf(v, __uint_as_float(shfl_xor_u32(__float_as_uint(v), m)));
-  return v;
-}
-__device__ __forceinline__ float wave_min_f32(float v) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) v = __builtin_fminf(v, __uint_as_float(shfl_xor_u32(__float_as_uint(v), m)));
-  return v;
-}
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    const uint64_t o = shfl_xor_u64(v, m);
-    v = o > v ? o : v;
+
+// Reductions over the wave; every lane receives the result.  The first four
+// steps reduce each 16-lane row (xor 1, xor 2, mirror in 8, mirror in 16),
+// then the two permlane swaps join rows.
+template <class Op>
+__device__ __forceinline__ uint32_t wave_reduce(uint32_t v, Op op) {
+  v = op(v, dpp<0xB1>(v));
+  v = op(v, dpp<0x4E>(v));
+  v = op(v, dpp<0x141>(v));
+  v = op(v, dpp<0x140>(v));
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = op(r[0], r[1]);
+  }
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    v = op(r[0], r[1]);
   }
   return v;
 }
-__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+template <class Op>
+__device__ __forceinline__ uint64_t wave_reduce64(uint64_t v, Op op, int lane) {
 #pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    const uint64_t o = shfl_xor_u64(v, m);
-    v = o < v ? o : v;
-  }
+  for (int m = 1; m < 64; m <<= 1) v = op(v, xor_lane64(v, m, lane));
   return v;
 }
+struct Add { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a + b; } };
+struct Max { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; } };
+struct Min { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a < b ? a : b; } };
+struct Max64 { __device__ uint64_t operator()(uint64_t a, uint64_t b) const { return a > b ? a : b; } };
+struct Min64 { __device__ uint64_t operator()(uint64_t a, uint64_t b) const { return a < b ? a : b; } };
+
 // Exclusive prefix sum over lanes 0..63.
 __device__ __forceinline__ uint32_t wave_excl_scan(uint32_t v, int lane) {
   uint32_t x = v;
@@ -120,23 +147,26 @@ __device__ __forceinline__ uint32_t wave_excl_scan(uint32_t v, int lane) {
 // ------------------------------------------------------------- row data
 
 // Ordered key of an fp32 score: larger score -> larger key; -0 and +0 share
-// one key.  (NaN is outside the contract.)
+// one key; every finite or infinite score except -inf maps above 0x007fffff.
 __device__ __forceinline__ uint32_t score_key(float v) {
   uint32_t u = __float_as_uint(v);
   u = v == 0.0f ? 0u : u;
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_score(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
 }
 
 __device__ __forceinline__ uint64_t composite(uint32_t key, int id) {
   return ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)id);
 }
 
-// Element e of a lane: 16-byte vector e / VEC covers 64 * VEC consecutive
-// blocks, the lane's VEC of them at lane * VEC.
+// Block id of score e of a lane in wave w: 16-byte vector e / VEC covers
+// 64 * VEC consecutive blocks, the lane's VEC of them at lane * VEC.
 template <bool BF16>
-__device__ __forceinline__ int elem_id(int e, int lane) {
+__device__ __forceinline__ int elem_id(int e, int lane, int w) {
   constexpr int VEC = BF16 ? 8 : 4;
-  return (e / VEC) * (64 * VEC) + lane * VEC + (e % VEC);
+  return w * kChunk + (e / VEC) * (64 * VEC) + lane * VEC + (e % VEC);
 }
 
 // ----------------------------------------------------------- bitonic sort
@@ -156,8 +186,7 @@ __device__ __forceinline__ void bitonic_sort_desc(uint64_t (&a)[EPS], int lane) 
         for (int e = 0; e < EPS; ++e) {
           const int f = e ^ d;
           if (f > e) {
-            const int i = lane * EPS + e;
-            const bool desc = (i & size) == 0;
+            const bool desc = ((lane * EPS + e) & size) == 0;
             const uint64_t x = a[e], y = a[f];
             const bool sw = desc ? (x < y) : (x > y);
             a[e] = sw ? y : x;
@@ -169,10 +198,9 @@ __device__ __forceinline__ void bitonic_sort_desc(uint64_t (&a)[EPS], int lane) 
         const bool lower = (lane & m) == 0;
 #pragma unroll
         for (int e = 0; e < EPS; ++e) {
-          const int i = lane * EPS + e;
-          const bool desc = (i & size) == 0;
+          const bool desc = ((lane * EPS + e) & size) == 0;
           const uint64_t mine = a[e];
-          const uint64_t other = shfl_xor_u64(mine, m);
+          const uint64_t other = xor_lane64(mine, m, lane);
           const bool take_max = lower == desc;
           a[e] = take_max ? (other > mine ? other : mine) : (other < mine ? other : mine);
         }
@@ -215,15 +243,27 @@ __device__ __forceinline__ void sort_and_write(const uint64_t* cand, int nc, int
 
 // ----------------------------------------------------------------- kernel
 
-template <int EPL, bool BF16>
-__global__ void __launch_bounds__(kThreads) dsa_topk_rows(const DArgs g) {
+// Workgroup-wide combine of one value per wave (all lanes of a wave hold
+// it): lane 0 of each wave writes slot i of set `set`, a barrier, and every
+// wave reads the nw values.
+template <class Op>
+__device__ __forceinline__ uint32_t group_combine(Lds& lds, int set, int i, uint32_t v, int w,
+                                                  int nw, int lane, Op op, uint32_t ident) {
+  if (lane == 0) lds.slot[set][w][i] = v;
+  __syncthreads();
+  uint32_t r = ident;
+  for (int x = 0; x < nw; ++x) r = op(r, lds.slot[set][x][i]);
+  return r;
+}
+
+template <bool BF16>
+__global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
   constexpr int VEC = BF16 ? 8 : 4;
-  static_assert(EPL % VEC == 0, "elements per lane");
   __shared__ Lds lds;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + w;
-  if (row >= g.rows) return;                 // whole wave leaves; no workgroup barrier below
+  const int nw = (int)(blockDim.x >> 6);
+  const int64_t row = blockIdx.x;
   const int K = g.top_k;
   const int q = (int)(row % g.Q);
   const int b = (int)((row / g.Q) / g.H);
@@ -237,195 +277,251 @@ __global__ void __launch_bounds__(kThreads) dsa_topk_rows(const DArgs g) {
   last = last < vb - 1 ? last : vb - 1;
   const int nvalid = pos >= 0 && last >= 0 ? (int)(last + 1) : 0;
 
-  // Scores of the valid prefix, rounded up to whole 16-byte vectors (inside
-  // the row: NB is a multiple of VEC) so that no vector straddles the
-  // descriptor's end; vectors past it read as zero.  Blocks past the prefix
-  // are masked by id.
+  // Keys of the valid prefix.  The descriptor covers the prefix rounded up
+  // to whole 16-byte vectors (inside the row: NB is a multiple of VEC), so no
+  // vector straddles its end; vectors past it read as zero and blocks past
+  // the prefix are masked by id.
   constexpr uint32_t esz = BF16 ? 2u : 4u;
   const uint32_t nload = ((uint32_t)nvalid + VEC - 1) / VEC * VEC;
   const rsrc_t rs = make_rsrc((const uint8_t*)g.scores + row * (int64_t)g.NB * esz, nload * esz);
-  float v[EPL];
+  uint32_t key[kEPL];
 #pragma unroll
-  for (int i = 0; i < EPL / VEC; ++i) {
-    const u32x4 d = __builtin_amdgcn_raw_buffer_load_b128(rs, (uint32_t)(i * 64 + lane) * 16u, 0, 0);
+  for (int i = 0; i < kEPL / VEC; ++i) {
+    const u32x4 d = __builtin_amdgcn_raw_buffer_load_b128(
+        rs, (uint32_t)(w * kChunk * esz) + (uint32_t)(i * 64 + lane) * 16u, 0, 0);
+    float v[VEC];
     if constexpr (BF16) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        v[i * 8 + 2 * c] = bf16_lo(d[c]);
-        v[i * 8 + 2 * c + 1] = bf16_hi(d[c]);
+        v[2 * c] = bf16_lo(d[c]);
+        v[2 * c + 1] = bf16_hi(d[c]);
       }
     } else {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) v[i * 4 + c] = __uint_as_float(d[c]);
+      for (int c = 0; c < 4; ++c) v[c] = __uint_as_float(d[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      const int e = i * VEC + c;
+      const bool sel = elem_id<BF16>(e, lane, w) < nvalid && v[c] != -__builtin_inff();
+      key[e] = sel ? score_key(v[c]) : 0u;
     }
   }
-  auto selectable = [&](int e) {
-    return elem_id<BF16>(e, lane) < nvalid && v[e] != -__builtin_inff();
-  };
 
+  // Row totals: selectable count, largest key, smallest selectable key.
+  uint32_t cnt = 0, kmax = 0, kmin = 0xffffffffu;
+#pragma unroll
+  for (int e = 0; e < kEPL; ++e) {
+    cnt += key[e] != 0u;
+    kmax = key[e] > kmax ? key[e] : kmax;
+    kmin = key[e] != 0u && key[e] < kmin ? key[e] : kmin;
+  }
+  cnt = wave_reduce(cnt, Add());
+  kmax = wave_reduce(kmax, Max());
+  kmin = wave_reduce(kmin, Min());
+  if (lane == 0) {
+    lds.slot[0][w][0] = cnt;
+    lds.slot[0][w][1] = kmax;
+    lds.slot[0][w][2] = kmin;
+  }
+  __syncthreads();
   uint32_t nsel = 0;
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) nsel += selectable(e) ? 1u : 0u;
-  nsel = wave_sum_u32(nsel);
+  kmax = 0;
+  kmin = 0xffffffffu;
+  for (int x = 0; x < nw; ++x) {
+    nsel += lds.slot[0][x][0];
+    kmax = lds.slot[0][x][1] > kmax ? lds.slot[0][x][1] : kmax;
+    kmin = lds.slot[0][x][2] < kmin ? lds.slot[0][x][2] : kmin;
+  }
 
-  uint32_t* hist = lds.hist[w];
-  uint64_t* cand = lds.cand[w];
-  uint64_t lo = 0;                           // candidates: composite key >= lo
-
+  // Candidate rule: mode 0 all selectable; 1 fp32 bin >= bstar; 2 composite >= lo.
+  int mode = 0, bstar = 0;
+  float vmin = 0.0f, scale = 0.0f;
+  uint64_t lo = 0;
+  int set = 1;
   if (nsel > (uint32_t)kCap) {
-    // First split: 256 bins over the fp32 range of the selectable scores.
-    float vmax = -__builtin_inff(), vmin = __builtin_inff();
-#pragma unroll
-    for (int e = 0; e < EPL; ++e)
-      if (selectable(e)) {
-        vmax = __builtin_fmaxf(vmax, v[e]);
-        vmin = __builtin_fminf(vmin, v[e]);
-      }
-    vmax = wave_max_f32(vmax);
-    vmin = wave_min_f32(vmin);
-    const float scale = (float)kBins / (vmax - vmin);
-    uint64_t hi = ~0ull;                     // search range [lo, hi] on the composite key
-    uint32_t need = (uint32_t)K;             // still to find inside the range
-    bool float_pass = vmax > vmin && __builtin_isfinite(scale) && __builtin_isfinite(vmin) &&
-                      __builtin_isfinite(vmax);
+    const float fmax = key_score(kmax), fmin = key_score(kmin);
+    vmin = fmin;
+    scale = (float)kBins / (fmax - fmin);
+    const bool float_ok = fmax > fmin && __builtin_isfinite(scale) && __builtin_isfinite(fmin) &&
+                          __builtin_isfinite(fmax);
+    uint64_t hi = ~0ull, kbase = 0, width = 1;
+    uint32_t need = (uint32_t)K;
+    bool float_pass = float_ok;
     for (;;) {
-      // Histogram of the in-range blocks (float bins on the first pass,
-      // composite-key bins afterwards).
-      uint64_t kmin = 0, width = 1;
+      auto fbin = [&](uint32_t k) {
+        const float f = (key_score(k) - vmin) * scale;
+        return f >= (float)(kBins - 1) ? (uint32_t)(kBins - 1) : (uint32_t)f;
+      };
       if (!float_pass) {
+        // Composite-key bins over the range [lo, hi].
         uint64_t mn = ~0ull, mx = 0;
 #pragma unroll
-        for (int e = 0; e < EPL; ++e)
-          if (selectable(e)) {
-            const uint64_t c = composite(score_key(v[e]), elem_id<BF16>(e, lane));
+        for (int e = 0; e < kEPL; ++e)
+          if (key[e] != 0u) {
+            const uint64_t c = composite(key[e], elem_id<BF16>(e, lane, w));
             if (c >= lo && c <= hi) {
               mn = c < mn ? c : mn;
               mx = c > mx ? c : mx;
             }
           }
-        kmin = wave_min_u64(mn);
-        const uint64_t range = wave_max_u64(mx) - kmin;
-        width = range / kBins + 1;           // bins 0 .. range / width (<= 255)
-      }
-#pragma unroll
-      for (int i = 0; i < kBins / 64; ++i) hist[i * 64 + lane] = 0u;
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-#pragma unroll
-      for (int e = 0; e < EPL; ++e)
-        if (selectable(e)) {
-          uint32_t bin;
-          bool in = true;
-          if (float_pass) {
-            const float f = (v[e] - vmin) * scale;
-            bin = f >= (float)(kBins - 1) ? (uint32_t)(kBins - 1) : (uint32_t)f;
-          } else {
-            const uint64_t c = composite(score_key(v[e]), elem_id<BF16>(e, lane));
-            in = c >= lo && c <= hi;
-            bin = in ? (uint32_t)((c - kmin) / width) : 0u;
-          }
-          if (in) __hip_atomic_fetch_add(&hist[bin], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+        mn = wave_reduce64(mn, Min64(), lane);
+        mx = wave_reduce64(mx, Max64(), lane);
+        if (lane == 0) {
+          lds.slot[set][w][0] = (uint32_t)mn;
+          lds.slot[set][w][1] = (uint32_t)(mn >> 32);
+          lds.slot[set][w][2] = (uint32_t)mx;
+          lds.slot[set][w][3] = (uint32_t)(mx >> 32);
         }
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        __syncthreads();
+        mn = ~0ull;
+        mx = 0;
+        for (int x = 0; x < nw; ++x) {
+          const uint64_t a = (uint64_t)lds.slot[set][x][0] | ((uint64_t)lds.slot[set][x][1] << 32);
+          const uint64_t c = (uint64_t)lds.slot[set][x][2] | ((uint64_t)lds.slot[set][x][3] << 32);
+          mn = a < mn ? a : mn;
+          mx = c > mx ? c : mx;
+        }
+        set ^= 1;
+        kbase = mn;
+        width = (mx - mn) / kBins + 1;         // bins 0 .. (mx - mn) / width <= 255
+      }
+      auto bin_of = [&](int e, uint32_t& bin) {  // false: not in range
+        if (key[e] == 0u) return false;
+        if (float_pass) {
+          bin = fbin(key[e]);
+          return true;
+        }
+        const uint64_t c = composite(key[e], elem_id<BF16>(e, lane, w));
+        if (c < lo || c > hi) return false;
+        bin = (uint32_t)((c - kbase) / width);
+        return true;
+      };
+      if (w == 0) {
+#pragma unroll
+        for (int i = 0; i < kBins / 64; ++i) lds.hist[i * 64 + lane] = 0u;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int e = 0; e < kEPL; ++e) {
+        uint32_t bin;
+        if (bin_of(e, bin))
+          __hip_atomic_fetch_add(&lds.hist[bin], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+      __syncthreads();
       // Boundary bin: above(b) < need <= above(b) + hist[b], above(b) = blocks in higher bins.
       uint32_t hb[kBins / 64], lane_sum = 0;
 #pragma unroll
       for (int i = 0; i < kBins / 64; ++i) {
-        hb[i] = hist[lane * (kBins / 64) + i];
+        hb[i] = lds.hist[lane * (kBins / 64) + i];
         lane_sum += hb[i];
       }
-      uint32_t rev = 0;   // blocks in the bins of higher lanes (exclusive suffix sum)
-      {
-        uint32_t x = lane_sum;
+      uint32_t incl = lane_sum;   // inclusive suffix sum over lanes >= lane
 #pragma unroll
-        for (int dd = 1; dd < 64; dd <<= 1) {
-          const uint32_t o = (uint32_t)__shfl_down((int)x, dd, 64);
-          if (lane + dd < 64) x += o;
-        }
-        rev = x - lane_sum;
+      for (int dd = 1; dd < 64; dd <<= 1) {
+        const uint32_t o = (uint32_t)__shfl_down((int)incl, dd, 64);
+        if (lane + dd < 64) incl += o;
       }
-      int bstar = -1;
-      uint32_t above_star = 0, cnt_star = 0;
+      int bs = -1;
+      uint32_t above_s = 0, cnt_s = 0;
       {
-        uint32_t above = rev;
+        uint32_t above = incl - lane_sum;
 #pragma unroll
         for (int i = kBins / 64 - 1; i >= 0; --i) {
-          if (bstar < 0 && above < need && need <= above + hb[i]) {
-            bstar = lane * (kBins / 64) + i;
-            above_star = above;
-            cnt_star = hb[i];
+          if (bs < 0 && above < need && need <= above + hb[i]) {
+            bs = lane * (kBins / 64) + i;
+            above_s = above;
+            cnt_s = hb[i];
           }
           above += hb[i];
         }
       }
-      const uint64_t ball = __ballot(bstar >= 0);
-      const int src = __builtin_ctzll(ball);
-      bstar = __shfl(bstar, src, 64);
-      above_star = (uint32_t)__shfl((int)above_star, src, 64);
-      cnt_star = (uint32_t)__shfl((int)cnt_star, src, 64);
-      // New range: the composite keys of the boundary bin's blocks.
+      const int src = __builtin_ctzll(__ballot(bs >= 0));
+      bs = __shfl(bs, src, 64);
+      above_s = (uint32_t)__shfl((int)above_s, src, 64);
+      cnt_s = (uint32_t)__shfl((int)cnt_s, src, 64);
+      const uint32_t found = (uint32_t)K - need + above_s;   // blocks above the boundary bin
+      if (float_pass && found + cnt_s <= (uint32_t)kCap) {
+        mode = 1;
+        bstar = bs;
+        break;
+      }
+      // The boundary bin's composite-key range.
       uint64_t mn = ~0ull, mx = 0;
 #pragma unroll
-      for (int e = 0; e < EPL; ++e)
-        if (selectable(e)) {
-          const uint64_t c = composite(score_key(v[e]), elem_id<BF16>(e, lane));
-          uint32_t bin;
-          bool in = true;
-          if (float_pass) {
-            const float f = (v[e] - vmin) * scale;
-            bin = f >= (float)(kBins - 1) ? (uint32_t)(kBins - 1) : (uint32_t)f;
-          } else {
-            in = c >= lo && c <= hi;
-            bin = in ? (uint32_t)((c - kmin) / width) : 0u;
-          }
-          if (in && (int)bin == bstar) {
-            mn = c < mn ? c : mn;
-            mx = c > mx ? c : mx;
-          }
+      for (int e = 0; e < kEPL; ++e) {
+        uint32_t bin;
+        if (bin_of(e, bin) && (int)bin == bs) {
+          const uint64_t c = composite(key[e], elem_id<BF16>(e, lane, w));
+          mn = c < mn ? c : mn;
+          mx = c > mx ? c : mx;
         }
-      const uint64_t new_lo = wave_min_u64(mn);
-      const uint64_t new_hi = wave_max_u64(mx);
-      // Blocks strictly above the new range are in the result: K - need
-      // found before this pass plus above_star in this one.
-      const uint32_t found = (uint32_t)K - need + above_star;
-      lo = new_lo;
-      hi = new_hi;
-      if (found + cnt_star <= (uint32_t)kCap) break;
-      need -= above_star;
+      }
+      mn = wave_reduce64(mn, Min64(), lane);
+      mx = wave_reduce64(mx, Max64(), lane);
+      if (lane == 0) {
+        lds.slot[set][w][0] = (uint32_t)mn;
+        lds.slot[set][w][1] = (uint32_t)(mn >> 32);
+        lds.slot[set][w][2] = (uint32_t)mx;
+        lds.slot[set][w][3] = (uint32_t)(mx >> 32);
+      }
+      __syncthreads();
+      mn = ~0ull;
+      mx = 0;
+      for (int x = 0; x < nw; ++x) {
+        const uint64_t a = (uint64_t)lds.slot[set][x][0] | ((uint64_t)lds.slot[set][x][1] << 32);
+        const uint64_t c = (uint64_t)lds.slot[set][x][2] | ((uint64_t)lds.slot[set][x][3] << 32);
+        mn = a < mn ? a : mn;
+        mx = c > mx ? c : mx;
+      }
+      set ^= 1;
+      lo = mn;
+      hi = mx;
+      if (found + cnt_s <= (uint32_t)kCap) {
+        mode = 2;
+        break;
+      }
+      need -= above_s;
       float_pass = false;
     }
   }
 
-  // Compaction of the candidates (selectable, composite key >= lo).
+  // Compaction of the candidates into LDS.
+  auto is_cand = [&](int e) {
+    if (key[e] == 0u) return false;
+    if (mode == 0) return true;
+    if (mode == 1) {
+      const float f = (key_score(key[e]) - vmin) * scale;
+      const uint32_t bin = f >= (float)(kBins - 1) ? (uint32_t)(kBins - 1) : (uint32_t)f;
+      return (int)bin >= bstar;
+    }
+    return composite(key[e], elem_id<BF16>(e, lane, w)) >= lo;
+  };
   uint32_t mine = 0;
 #pragma unroll
-  for (int e = 0; e < EPL; ++e)
-    if (selectable(e) && composite(score_key(v[e]), elem_id<BF16>(e, lane)) >= lo) ++mine;
+  for (int e = 0; e < kEPL; ++e) mine += is_cand(e);
   uint32_t off = wave_excl_scan(mine, lane);
-  const uint32_t nc = wave_sum_u32(mine);
+  const uint32_t wtot = wave_reduce(mine, Add());
+  if (lane == 0) lds.slot[set][w][0] = wtot;
+  __syncthreads();
+  uint32_t base = 0, nc = 0;
+  for (int x = 0; x < nw; ++x) {
+    const uint32_t t = lds.slot[set][x][0];
+    base += x < w ? t : 0u;
+    nc += t;
+  }
+  off += base;
 #pragma unroll
-  for (int e = 0; e < EPL; ++e)
-    if (selectable(e)) {
-      const uint64_t c = composite(score_key(v[e]), elem_id<BF16>(e, lane));
-      if (c >= lo) cand[off++] = c;
-    }
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  for (int e = 0; e < kEPL; ++e)
+    if (is_cand(e)) lds.cand[off++] = composite(key[e], elem_id<BF16>(e, lane, w));
+  __syncthreads();
+  if (w != 0) return;
 
   const int n = (int)nc;
-  if (n <= 64) sort_and_write<1>(cand, n, lane, g, row, b);
-  else if (n <= 128) sort_and_write<2>(cand, n, lane, g, row, b);
-  else if (n <= 256) sort_and_write<4>(cand, n, lane, g, row, b);
-  else sort_and_write<8>(cand, n, lane, g, row, b);
-}
-
-using Kernel = void (*)(DArgs);
-
-const void* kernel_for(int epl, bool bf16) {
-  switch (epl) {
-    case 8: return bf16 ? (const void*)&dsa_topk_rows<8, true> : (const void*)&dsa_topk_rows<8, false>;
-    case 16: return bf16 ? (const void*)&dsa_topk_rows<16, true> : (const void*)&dsa_topk_rows<16, false>;
-    case 32: return bf16 ? (const void*)&dsa_topk_rows<32, true> : (const void*)&dsa_topk_rows<32, false>;
-    default: return bf16 ? (const void*)&dsa_topk_rows<64, true> : (const void*)&dsa_topk_rows<64, false>;
-  }
+  if (n <= 64) sort_and_write<1>(lds.cand, n, lane, g, row, b);
+  else if (n <= 128) sort_and_write<2>(lds.cand, n, lane, g, row, b);
+  else if (n <= 256) sort_and_write<4>(lds.cand, n, lane, g, row, b);
+  else sort_and_write<8>(lds.cand, n, lane, g, row, b);
 }
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
@@ -453,7 +549,7 @@ FAGQ_API int fagq_dsa_topk_launch(const void* scores, int scores_dtype, const vo
   if (NB > FAGQ_DSA_MAX_NB || top_k > kMaxTopK || block_size > INT32_MAX) return FAGQ_E_TOO_LARGE;
   const int64_t rows = B * H * Q;
   const int64_t esz = scores_dtype == FAGQ_DSA_BF16 ? 2 : 4;
-  if (rows > (int64_t)INT32_MAX * kRowsPerBlock || NB * esz > (int64_t)UINT32_MAX)
+  if (rows > (int64_t)INT32_MAX || NB * esz > (int64_t)UINT32_MAX)
     return FAGQ_E_TOO_LARGE;
   if (!aligned(scores, 16) || (NB * esz) % 16 != 0 || !aligned(page_table, 4) ||
       !aligned(out_blocks, 4) || !aligned(out_pages, 4) ||
@@ -473,7 +569,6 @@ FAGQ_API int fagq_dsa_topk_launch(const void* scores, int scores_dtype, const vo
   g.kv_lens = kv_lens;
   g.out_blocks = static_cast<int32_t*>(out_blocks);
   g.out_pages = static_cast<int32_t*>(out_pages);
-  g.rows = rows;
   g.H = (int32_t)H;
   g.Q = (int32_t)Q;
   g.NB = (int32_t)NB;
@@ -481,13 +576,11 @@ FAGQ_API int fagq_dsa_topk_launch(const void* scores, int scores_dtype, const vo
   g.top_k = (int32_t)top_k;
   g.index64 = index_dtype == FAGQ_DSA_I64;
   const bool bf16 = scores_dtype == FAGQ_DSA_BF16;
-  const int64_t per_lane = (NB + 63) / 64;
-  int epl = 8;
-  while (epl < per_lane) epl <<= 1;
+  const int waves = (int)((NB + kChunk - 1) / kChunk);
   void* args[] = {&g};
-  const hipError_t e = hipLaunchKernel(kernel_for(epl, bf16),
-                                       dim3((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock)),
-                                       dim3(kThreads), args, 0, static_cast<hipStream_t>(stream));
+  const void* k = bf16 ? (const void*)&dsa_topk_rows<true> : (const void*)&dsa_topk_rows<false>;
+  const hipError_t e = hipLaunchKernel(k, dim3((unsigned)rows), dim3((unsigned)(64 * waves)), args,
+                                       0, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? FAGQ_OK : -(int)e;
 }
 
