@@ -11,30 +11,30 @@
 // Work mapping.  One workgroup per row, one wave per 1024 blocks of it (up
 // to 4 waves); a lane holds 16 scores in VGPRs, loaded as 16-byte vectors
 // through a buffer descriptor sized to the row's valid prefix, so blocks past
-// it are never fetched.  Cross-lane steps use DPP and v_permlane16/32_swap
-// (VALU, no LDS round trip); the waves of a row combine through a few LDS
-// words and workgroup barriers, and every decision is computed identically
-// by all of them.
+// it are never fetched, and waves wholly past the prefix exit at once (a
+// workgroup barrier waits only for the waves still running).  Cross-lane
+// steps use DPP and v_permlane32_swap; the waves of a row combine through LDS
+// and three workgroup barriers.
 //
-// Selection is exact and never sorts the whole row:
-//   * Every selectable block has a 32-bit ordered key of its score (larger
-//     is better, -0 and +0 one key, 0 for blocks that are not selectable)
-//     and a 64-bit composite key (key << 32) | (0xffffffff - id): the order
-//     is score descending, then id ascending.
-//   * If at most CAP (512) blocks are selectable they are all candidates.
-//   * Otherwise a 256-bin histogram in LDS over the scores' fp32 range (the
-//     bin is a monotone function of the score) locates the bin holding the
-//     top_k-th block; with that bin and all higher ones at most CAP blocks,
-//     those are the candidates.  Otherwise the bin becomes a search range
-//     [lo, hi] on the composite key and is split again by 256-bin histograms
-//     on the composite key, which always separate the range's smallest and
-//     largest keys, so the loop ends.
-//   * The candidates are compacted to LDS, bitonic-sorted in registers
-//     across one wave (descending), and the first top_k are written with
-//     their page-table entries.
-// For Gaussian-like scores the fp32 histogram leaves a handful of blocks in
-// the boundary bin, so a row costs one histogram and a sort of about top_k
-// keys.
+// Selection is exact and never runs a sorting network:
+//   1. The fp32 range [vmin, vmax] of the selectable scores (non-selectable
+//      blocks hold -inf) defines 256 bins, bin(v) = clamp(v * s + o, 0, 255)
+//      with s = 256 / (vmax - vmin): a monotone function of the score.
+//   2. An LDS histogram of the bins; its suffix sums above(b) (blocks in
+//      higher bins) give the boundary bin b* holding the top_k-th block.
+//      The candidates are the blocks of bins >= b*: found = above(b*) of them
+//      are certainly selected, and all of them fit in CAP = 512.
+//   3. Counting sort: a candidate is stored at above(bin) plus a per-bin
+//      cursor, so each bin owns one segment of the candidate array, bins in
+//      descending order.  A candidate's rank is above(bin) plus the number of
+//      candidates in its own segment that precede it (64-bit composite key:
+//      (ordered score bits << 32) | (0xffffffff - id)); for Gaussian-like
+//      scores a segment holds a few blocks.  Ranks below top_k are written
+//      with their page-table entries.
+//   If the boundary bin leaves more than CAP candidates (ties, outliers that
+//   stretch the range), a refinement finds a threshold on the composite key
+//   by 8-bit radix passes over the key range that remains, and the rank is
+//   then counted over all candidates.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -50,7 +50,7 @@ constexpr int kEPL = 16;                    // scores per lane
 constexpr int kChunk = 64 * kEPL;            // blocks per wave
 constexpr int kMaxWaves = FAGQ_DSA_MAX_NB / kChunk;
 constexpr int kBins = 256;
-constexpr int kCap = 512;                    // candidates sorted at most
+constexpr uint32_t kCap = 512;               // candidates held at most
 constexpr int kMaxTopK = FAGQ_DSA_MAX_TOP_K;
 static_assert(kMaxWaves * kChunk == FAGQ_DSA_MAX_NB, "waves per row");
 
@@ -68,17 +68,47 @@ struct DArgs {
 };
 
 struct Lds {
-  uint32_t hist[kBins];
+  uint32_t hist[kBins + 64];        // bin counts, then one discard word per lane
+  uint32_t fill[kBins];             // per-bin scatter cursors
+  uint32_t above[kBins];            // candidates in higher bins (segment starts)
   uint64_t cand[kCap];
-  uint32_t slot[2][kMaxWaves][4];   // per-wave partials (two sets, alternating)
+  float fslot[kMaxWaves][2];        // per-wave max / min
+  uint32_t uslot[2][kMaxWaves][4];  // per-wave partials of the refinement
+  uint32_t ncur;                    // refinement scatter cursor
 };
+constexpr int kZeroWords = kBins + 64 + kBins;   // hist and fill, cleared per row
+static_assert(kZeroWords % 4 == 0, "cleared with 16-byte stores");
 
 // --------------------------------------------------------- wave primitives
 
-template <int CTRL>
+template <int CTRL, int ROW_MASK = 0xf>
 __device__ __forceinline__ uint32_t dpp(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, true);
 }
+
+// All-lane reduction: xor 1, xor 2 (quad permutes), mirror in 8, mirror in
+// 16 reduce each 16-lane row; v_permlane16_swap and v_permlane32_swap join
+// the rows.
+template <class Op>
+__device__ __forceinline__ uint32_t wave_reduce(uint32_t v, Op op) {
+  v = op(v, dpp<0xB1>(v));
+  v = op(v, dpp<0x4E>(v));
+  v = op(v, dpp<0x141>(v));
+  v = op(v, dpp<0x140>(v));
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = op(r[0], r[1]);
+  }
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    v = op(r[0], r[1]);
+  }
+  return v;
+}
+struct FMax { __device__ uint32_t operator()(uint32_t a, uint32_t b) const {
+  return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b))); } };
+struct FMin { __device__ uint32_t operator()(uint32_t a, uint32_t b) const {
+  return __float_as_uint(fminf(__uint_as_float(a), __uint_as_float(b))); } };
 
 // Value of lane (lane ^ m), m a power of two below 64.
 __device__ __forceinline__ uint32_t xor_lane(uint32_t v, int m, int lane) {
@@ -97,57 +127,34 @@ __device__ __forceinline__ uint32_t xor_lane(uint32_t v, int m, int lane) {
     }
   }
 }
-__device__ __forceinline__ uint64_t xor_lane64(uint64_t v, int m, int lane) {
-  return (uint64_t)xor_lane((uint32_t)v, m, lane) |
-         ((uint64_t)xor_lane((uint32_t)(v >> 32), m, lane) << 32);
-}
-
-// Reductions over the wave; every lane receives the result.  The first four
-// steps reduce each 16-lane row (xor 1, xor 2, mirror in 8, mirror in 16),
-// then the two permlane swaps join rows.
-template <class Op>
-__device__ __forceinline__ uint32_t wave_reduce(uint32_t v, Op op) {
-  v = op(v, dpp<0xB1>(v));
-  v = op(v, dpp<0x4E>(v));
-  v = op(v, dpp<0x141>(v));
-  v = op(v, dpp<0x140>(v));
-  {
-    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-    v = op(r[0], r[1]);
-  }
-  {
-    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    v = op(r[0], r[1]);
+template <bool MAX>
+__device__ __forceinline__ uint64_t wave_reduce64(uint64_t v, int lane) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const uint64_t o = (uint64_t)xor_lane((uint32_t)v, m, lane) |
+                       ((uint64_t)xor_lane((uint32_t)(v >> 32), m, lane) << 32);
+    v = MAX ? (o > v ? o : v) : (o < v ? o : v);
   }
   return v;
 }
-template <class Op>
-__device__ __forceinline__ uint64_t wave_reduce64(uint64_t v, Op op, int lane) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) v = op(v, xor_lane64(v, m, lane));
-  return v;
-}
-struct Add { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a + b; } };
-struct Max { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; } };
-struct Min { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a < b ? a : b; } };
-struct Max64 { __device__ uint64_t operator()(uint64_t a, uint64_t b) const { return a > b ? a : b; } };
-struct Min64 { __device__ uint64_t operator()(uint64_t a, uint64_t b) const { return a < b ? a : b; } };
 
-// Exclusive prefix sum over lanes 0..63.
-__device__ __forceinline__ uint32_t wave_excl_scan(uint32_t v, int lane) {
-  uint32_t x = v;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t o = (uint32_t)__shfl_up((int)x, d, 64);
-    if (lane >= d) x += o;
-  }
-  return x - v;
+// Inclusive prefix sum over lanes 0..63: shifts 1, 2, 4, 8 inside each
+// 16-lane row, then row_bcast:15 (rows 1 and 3 add the last lane of rows 0
+// and 2) and row_bcast:31 (rows 2 and 3 add lane 31).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+  x += dpp<0x111>(x);
+  x += dpp<0x112>(x);
+  x += dpp<0x114>(x);
+  x += dpp<0x118>(x);
+  x += dpp<0x142, 0xa>(x);
+  x += dpp<0x143, 0xc>(x);
+  return x;
 }
 
 // ------------------------------------------------------------- row data
 
 // Ordered key of an fp32 score: larger score -> larger key; -0 and +0 share
-// one key; every finite or infinite score except -inf maps above 0x007fffff.
+// one key; every score except -inf maps above 0x007fffff.
 __device__ __forceinline__ uint32_t score_key(float v) {
   uint32_t u = __float_as_uint(v);
   u = v == 0.0f ? 0u : u;
@@ -156,105 +163,65 @@ __device__ __forceinline__ uint32_t score_key(float v) {
 __device__ __forceinline__ float key_score(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
 }
+__device__ __forceinline__ uint64_t composite(float v, uint32_t id) {
+  return ((uint64_t)score_key(v) << 32) | (uint64_t)(0xffffffffu - id);
+}
 
-__device__ __forceinline__ uint64_t composite(uint32_t key, int id) {
-  return ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)id);
+// Histogram bin of a score.  fmaxf/fminf return the non-NaN operand, so the
+// result is in [0, 255] for every input, and it is non-decreasing in v.
+__device__ __forceinline__ uint32_t fbin(float v, float s, float o) {
+  return (uint32_t)fminf(fmaxf(fmaf(v, s, o), 0.0f), (float)(kBins - 1));
 }
 
 // Block id of score e of a lane in wave w: 16-byte vector e / VEC covers
 // 64 * VEC consecutive blocks, the lane's VEC of them at lane * VEC.
 template <bool BF16>
-__device__ __forceinline__ int elem_id(int e, int lane, int w) {
+__device__ __forceinline__ int elem_off(int e) {
   constexpr int VEC = BF16 ? 8 : 4;
-  return w * kChunk + (e / VEC) * (64 * VEC) + lane * VEC + (e % VEC);
+  return (e / VEC) * (64 * VEC) + (e % VEC);
 }
 
-// ----------------------------------------------------------- bitonic sort
-
-// Sorts the wave's 64 * EPS keys descending; lane l holds keys l * EPS ..
-// l * EPS + EPS - 1 (strides below EPS are compared inside a lane, larger
-// ones with the lane l ^ (stride / EPS)).
-template <int EPS>
-__device__ __forceinline__ void bitonic_sort_desc(uint64_t (&a)[EPS], int lane) {
-  constexpr int N = 64 * EPS;
+// Boundary of a histogram in hist[0..255]: the bin b with
+// above(b) < need <= above(b) + hist[b], above(b) = count in bins > b.
+// Every lane receives bin, above(bin), hist[bin] and the histogram total;
+// with STORE, above(b) is also written to lds.above (identical values from
+// every wave).
+struct Boundary {
+  uint32_t bin, above, cnt, total;
+};
+template <bool STORE>
+__device__ __forceinline__ Boundary find_boundary(Lds& lds, uint32_t k, int lane) {
+  const u32x4 h = reinterpret_cast<const u32x4*>(lds.hist)[lane];   // bins 4 lane .. 4 lane + 3
+  const uint32_t sum = h[0] + h[1] + h[2] + h[3];
+  const uint32_t incl = wave_incl_scan(sum);
+  Boundary r;
+  r.total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+  const uint32_t need = k < r.total ? k : r.total;
+  u32x4 a;
+  a[3] = r.total - incl;
+  a[2] = a[3] + h[3];
+  a[1] = a[2] + h[2];
+  a[0] = a[1] + h[1];
+  if constexpr (STORE) reinterpret_cast<u32x4*>(lds.above)[lane] = a;
+  uint32_t bin = 0, ab = 0, cb = 0;
+  bool hit = false;
 #pragma unroll
-  for (int size = 2; size <= N; size <<= 1) {
-#pragma unroll
-    for (int d = size >> 1; d > 0; d >>= 1) {
-      if (d < EPS) {
-#pragma unroll
-        for (int e = 0; e < EPS; ++e) {
-          const int f = e ^ d;
-          if (f > e) {
-            const bool desc = ((lane * EPS + e) & size) == 0;
-            const uint64_t x = a[e], y = a[f];
-            const bool sw = desc ? (x < y) : (x > y);
-            a[e] = sw ? y : x;
-            a[f] = sw ? x : y;
-          }
-        }
-      } else {
-        const int m = d / EPS;
-        const bool lower = (lane & m) == 0;
-#pragma unroll
-        for (int e = 0; e < EPS; ++e) {
-          const bool desc = ((lane * EPS + e) & size) == 0;
-          const uint64_t mine = a[e];
-          const uint64_t other = xor_lane64(mine, m, lane);
-          const bool take_max = lower == desc;
-          a[e] = take_max ? (other > mine ? other : mine) : (other < mine ? other : mine);
-        }
-      }
-    }
+  for (int i = 0; i < 4; ++i) {
+    const bool c = a[i] < need && need <= a[i] + h[i];
+    bin = c ? (uint32_t)(4 * lane + i) : bin;
+    ab = c ? a[i] : ab;
+    cb = c ? h[i] : cb;
+    hit = hit || c;
   }
-}
-
-template <int EPS>
-__device__ __forceinline__ void sort_and_write(const uint64_t* cand, int nc, int lane,
-                                               const DArgs& g, int64_t row, int b) {
-  uint64_t a[EPS];
-#pragma unroll
-  for (int e = 0; e < EPS; ++e) {
-    const int i = lane * EPS + e;
-    a[e] = i < nc ? cand[i] : 0ull;     // 0 sorts below every selectable key
-  }
-  bitonic_sort_desc<EPS>(a, lane);
-  const int K = g.top_k;
-  const int take = nc < K ? nc : K;
-#pragma unroll
-  for (int e = 0; e < EPS; ++e) {
-    const int t = lane * EPS + e;
-    if (t < K) {
-      int32_t blk = -1, page = -1;
-      if (t < take) {
-        blk = (int32_t)(0xffffffffu - (uint32_t)a[e]);
-        page = g.page_table[(int64_t)b * g.NB + blk];
-      }
-      g.out_blocks[row * K + t] = blk;
-      g.out_pages[row * K + t] = page;
-    }
-  }
-  // Ranks past the sorted width (top_k > 64 * EPS >= the candidate count) are empty.
-  for (int t = 64 * EPS + lane; t < K; t += 64) {
-    g.out_blocks[row * K + t] = -1;
-    g.out_pages[row * K + t] = -1;
-  }
+  const uint64_t m = __ballot(hit);
+  const int src = m ? __builtin_ctzll(m) : 0;
+  r.bin = (uint32_t)__builtin_amdgcn_readlane((int)bin, src);
+  r.above = m ? (uint32_t)__builtin_amdgcn_readlane((int)ab, src) : 0u;
+  r.cnt = m ? (uint32_t)__builtin_amdgcn_readlane((int)cb, src) : 0u;
+  return r;
 }
 
 // ----------------------------------------------------------------- kernel
-
-// Workgroup-wide combine of one value per wave (all lanes of a wave hold
-// it): lane 0 of each wave writes slot i of set `set`, a barrier, and every
-// wave reads the nw values.
-template <class Op>
-__device__ __forceinline__ uint32_t group_combine(Lds& lds, int set, int i, uint32_t v, int w,
-                                                  int nw, int lane, Op op, uint32_t ident) {
-  if (lane == 0) lds.slot[set][w][i] = v;
-  __syncthreads();
-  uint32_t r = ident;
-  for (int x = 0; x < nw; ++x) r = op(r, lds.slot[set][x][i]);
-  return r;
-}
 
 template <bool BF16>
 __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
@@ -262,7 +229,6 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
   __shared__ Lds lds;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nw = (int)(blockDim.x >> 6);
   const int64_t row = blockIdx.x;
   const int K = g.top_k;
   const int q = (int)(row % g.Q);
@@ -276,19 +242,30 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
   int64_t last = pos >= 0 ? pos / g.block_size : -1;
   last = last < vb - 1 ? last : vb - 1;
   const int nvalid = pos >= 0 && last >= 0 ? (int)(last + 1) : 0;
+  const int nwv = nvalid > kChunk ? (nvalid + kChunk - 1) / kChunk : 1;   // waves with work
+  if (w >= nwv) return;
 
-  // Keys of the valid prefix.  The descriptor covers the prefix rounded up
-  // to whole 16-byte vectors (inside the row: NB is a multiple of VEC), so no
-  // vector straddles its end; vectors past it read as zero and blocks past
-  // the prefix are masked by id.
+  if (w == 0) {
+    u32x4* z = reinterpret_cast<u32x4*>(lds.hist);
+    for (int i = lane; i < kZeroWords / 4; i += 64) z[i] = u32x4{0u, 0u, 0u, 0u};
+    if (lane == 0) lds.ncur = 0u;
+  }
+
+  // Scores of the valid prefix; non-selectable blocks hold -inf.  The
+  // descriptor covers the prefix rounded up to whole 16-byte vectors (inside
+  // the row: NB is a multiple of VEC), so no vector straddles its end.
   constexpr uint32_t esz = BF16 ? 2u : 4u;
   const uint32_t nload = ((uint32_t)nvalid + VEC - 1) / VEC * VEC;
   const rsrc_t rs = make_rsrc((const uint8_t*)g.scores + row * (int64_t)g.NB * esz, nload * esz);
-  uint32_t key[kEPL];
+  const int lbase = lane * VEC;                  // lane's first block inside a vector span
+  const int wbase = w * kChunk;
+  const float ninf = -__builtin_inff();
+  float sv[kEPL];
+  float vmax = ninf, vmin = __builtin_inff();
 #pragma unroll
   for (int i = 0; i < kEPL / VEC; ++i) {
     const u32x4 d = __builtin_amdgcn_raw_buffer_load_b128(
-        rs, (uint32_t)(w * kChunk * esz) + (uint32_t)(i * 64 + lane) * 16u, 0, 0);
+        rs, (uint32_t)(wbase * esz) + (uint32_t)(i * 64 + lane) * 16u, 0, 0);
     float v[VEC];
     if constexpr (BF16) {
 #pragma unroll
@@ -303,225 +280,164 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
       const int e = i * VEC + c;
-      const bool sel = elem_id<BF16>(e, lane, w) < nvalid && v[c] != -__builtin_inff();
-      key[e] = sel ? score_key(v[c]) : 0u;
+      const bool ok = lbase < nvalid - wbase - elem_off<BF16>(e) && v[c] != ninf;
+      sv[e] = ok ? v[c] : ninf;
+      vmax = fmaxf(vmax, sv[e]);
+      vmin = fminf(vmin, ok ? v[c] : __builtin_inff());
     }
   }
-
-  // Row totals: selectable count, largest key, smallest selectable key.
-  uint32_t cnt = 0, kmax = 0, kmin = 0xffffffffu;
-#pragma unroll
-  for (int e = 0; e < kEPL; ++e) {
-    cnt += key[e] != 0u;
-    kmax = key[e] > kmax ? key[e] : kmax;
-    kmin = key[e] != 0u && key[e] < kmin ? key[e] : kmin;
-  }
-  cnt = wave_reduce(cnt, Add());
-  kmax = wave_reduce(kmax, Max());
-  kmin = wave_reduce(kmin, Min());
+  vmax = __uint_as_float(wave_reduce(__float_as_uint(vmax), FMax()));
+  vmin = __uint_as_float(wave_reduce(__float_as_uint(vmin), FMin()));
   if (lane == 0) {
-    lds.slot[0][w][0] = cnt;
-    lds.slot[0][w][1] = kmax;
-    lds.slot[0][w][2] = kmin;
+    lds.fslot[w][0] = vmax;
+    lds.fslot[w][1] = vmin;
   }
   __syncthreads();
-  uint32_t nsel = 0;
-  kmax = 0;
-  kmin = 0xffffffffu;
-  for (int x = 0; x < nw; ++x) {
-    nsel += lds.slot[0][x][0];
-    kmax = lds.slot[0][x][1] > kmax ? lds.slot[0][x][1] : kmax;
-    kmin = lds.slot[0][x][2] < kmin ? lds.slot[0][x][2] : kmin;
+  for (int x = 0; x < nwv; ++x) {
+    vmax = fmaxf(vmax, lds.fslot[x][0]);
+    vmin = fminf(vmin, lds.fslot[x][1]);
   }
 
-  // Candidate rule: mode 0 all selectable; 1 fp32 bin >= bstar; 2 composite >= lo.
-  int mode = 0, bstar = 0;
-  float vmin = 0.0f, scale = 0.0f;
-  uint64_t lo = 0;
-  int set = 1;
-  if (nsel > (uint32_t)kCap) {
-    const float fmax = key_score(kmax), fmin = key_score(kmin);
-    vmin = fmin;
-    scale = (float)kBins / (fmax - fmin);
-    const bool float_ok = fmax > fmin && __builtin_isfinite(scale) && __builtin_isfinite(fmin) &&
-                          __builtin_isfinite(fmax);
-    uint64_t hi = ~0ull, kbase = 0, width = 1;
-    uint32_t need = (uint32_t)K;
-    bool float_pass = float_ok;
+  // Bin map; a degenerate or non-finite range puts every score in bin 0.
+  float s = 0.0f, o = 0.0f;
+  if (vmax > vmin) {
+    s = (float)kBins / (vmax - vmin);
+    o = -vmin * s;
+    if (!__builtin_isfinite(s) || !__builtin_isfinite(o)) s = o = 0.0f;
+  }
+  uint32_t bin[kEPL];
+#pragma unroll
+  for (int e = 0; e < kEPL; ++e) {
+    bin[e] = sv[e] != ninf ? fbin(sv[e], s, o) : (uint32_t)(kBins + lane);
+    __hip_atomic_fetch_add(&lds.hist[bin[e]], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  __syncthreads();
+
+  const Boundary bd = find_boundary<true>(lds, (uint32_t)K, lane);
+  uint32_t nc = bd.total ? bd.above + bd.cnt : 0u;
+  const bool refine = nc > kCap;
+
+  if (!refine) {
+    // Counting-sort scatter of the blocks in bins >= b*.
+    const uint32_t bstar = bd.bin, span = (uint32_t)kBins - bd.bin;
+#pragma unroll
+    for (int e = 0; e < kEPL; ++e) {
+      if (bin[e] - bstar < span) {
+        const uint32_t p = lds.above[bin[e]] +
+            __hip_atomic_fetch_add(&lds.fill[bin[e]], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (p < kCap) lds.cand[p] = composite(sv[e], (uint32_t)(wbase + lbase + elem_off<BF16>(e)));
+      }
+    }
+  } else {
+    // Radix refinement on the composite key over [lo, hi]; found blocks lie
+    // above hi, need more are inside the range.
+    uint64_t lo = 1, hi = ~0ull, thr = 1;
+    uint32_t need = (uint32_t)K, found = 0;
+    int set = 0;
     for (;;) {
-      auto fbin = [&](uint32_t k) {
-        const float f = (key_score(k) - vmin) * scale;
-        return f >= (float)(kBins - 1) ? (uint32_t)(kBins - 1) : (uint32_t)f;
-      };
-      if (!float_pass) {
-        // Composite-key bins over the range [lo, hi].
-        uint64_t mn = ~0ull, mx = 0;
-#pragma unroll
-        for (int e = 0; e < kEPL; ++e)
-          if (key[e] != 0u) {
-            const uint64_t c = composite(key[e], elem_id<BF16>(e, lane, w));
-            if (c >= lo && c <= hi) {
-              mn = c < mn ? c : mn;
-              mx = c > mx ? c : mx;
-            }
-          }
-        mn = wave_reduce64(mn, Min64(), lane);
-        mx = wave_reduce64(mx, Max64(), lane);
-        if (lane == 0) {
-          lds.slot[set][w][0] = (uint32_t)mn;
-          lds.slot[set][w][1] = (uint32_t)(mn >> 32);
-          lds.slot[set][w][2] = (uint32_t)mx;
-          lds.slot[set][w][3] = (uint32_t)(mx >> 32);
-        }
-        __syncthreads();
-        mn = ~0ull;
-        mx = 0;
-        for (int x = 0; x < nw; ++x) {
-          const uint64_t a = (uint64_t)lds.slot[set][x][0] | ((uint64_t)lds.slot[set][x][1] << 32);
-          const uint64_t c = (uint64_t)lds.slot[set][x][2] | ((uint64_t)lds.slot[set][x][3] << 32);
-          mn = a < mn ? a : mn;
-          mx = c > mx ? c : mx;
-        }
-        set ^= 1;
-        kbase = mn;
-        width = (mx - mn) / kBins + 1;         // bins 0 .. (mx - mn) / width <= 255
-      }
-      auto bin_of = [&](int e, uint32_t& bin) {  // false: not in range
-        if (key[e] == 0u) return false;
-        if (float_pass) {
-          bin = fbin(key[e]);
-          return true;
-        }
-        const uint64_t c = composite(key[e], elem_id<BF16>(e, lane, w));
-        if (c < lo || c > hi) return false;
-        bin = (uint32_t)((c - kbase) / width);
-        return true;
-      };
-      if (w == 0) {
-#pragma unroll
-        for (int i = 0; i < kBins / 64; ++i) lds.hist[i * 64 + lane] = 0u;
-      }
-      __syncthreads();
-#pragma unroll
-      for (int e = 0; e < kEPL; ++e) {
-        uint32_t bin;
-        if (bin_of(e, bin))
-          __hip_atomic_fetch_add(&lds.hist[bin], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      }
-      __syncthreads();
-      // Boundary bin: above(b) < need <= above(b) + hist[b], above(b) = blocks in higher bins.
-      uint32_t hb[kBins / 64], lane_sum = 0;
-#pragma unroll
-      for (int i = 0; i < kBins / 64; ++i) {
-        hb[i] = lds.hist[lane * (kBins / 64) + i];
-        lane_sum += hb[i];
-      }
-      uint32_t incl = lane_sum;   // inclusive suffix sum over lanes >= lane
-#pragma unroll
-      for (int dd = 1; dd < 64; dd <<= 1) {
-        const uint32_t o = (uint32_t)__shfl_down((int)incl, dd, 64);
-        if (lane + dd < 64) incl += o;
-      }
-      int bs = -1;
-      uint32_t above_s = 0, cnt_s = 0;
-      {
-        uint32_t above = incl - lane_sum;
-#pragma unroll
-        for (int i = kBins / 64 - 1; i >= 0; --i) {
-          if (bs < 0 && above < need && need <= above + hb[i]) {
-            bs = lane * (kBins / 64) + i;
-            above_s = above;
-            cnt_s = hb[i];
-          }
-          above += hb[i];
-        }
-      }
-      const int src = __builtin_ctzll(__ballot(bs >= 0));
-      bs = __shfl(bs, src, 64);
-      above_s = (uint32_t)__shfl((int)above_s, src, 64);
-      cnt_s = (uint32_t)__shfl((int)cnt_s, src, 64);
-      const uint32_t found = (uint32_t)K - need + above_s;   // blocks above the boundary bin
-      if (float_pass && found + cnt_s <= (uint32_t)kCap) {
-        mode = 1;
-        bstar = bs;
-        break;
-      }
-      // The boundary bin's composite-key range.
       uint64_t mn = ~0ull, mx = 0;
 #pragma unroll
       for (int e = 0; e < kEPL; ++e) {
-        uint32_t bin;
-        if (bin_of(e, bin) && (int)bin == bs) {
-          const uint64_t c = composite(key[e], elem_id<BF16>(e, lane, w));
-          mn = c < mn ? c : mn;
-          mx = c > mx ? c : mx;
+        asm volatile("" : "+v"(sv[e]));     // keep the keys out of registers across passes
+        if (sv[e] != ninf) {
+          const uint64_t c = composite(sv[e], (uint32_t)(wbase + lbase + elem_off<BF16>(e)));
+          if (c >= lo && c <= hi) {
+            mn = c < mn ? c : mn;
+            mx = c > mx ? c : mx;
+          }
         }
       }
-      mn = wave_reduce64(mn, Min64(), lane);
-      mx = wave_reduce64(mx, Max64(), lane);
+      mn = wave_reduce64<false>(mn, lane);
+      mx = wave_reduce64<true>(mx, lane);
       if (lane == 0) {
-        lds.slot[set][w][0] = (uint32_t)mn;
-        lds.slot[set][w][1] = (uint32_t)(mn >> 32);
-        lds.slot[set][w][2] = (uint32_t)mx;
-        lds.slot[set][w][3] = (uint32_t)(mx >> 32);
+        lds.uslot[set][w][0] = (uint32_t)mn;
+        lds.uslot[set][w][1] = (uint32_t)(mn >> 32);
+        lds.uslot[set][w][2] = (uint32_t)mx;
+        lds.uslot[set][w][3] = (uint32_t)(mx >> 32);
       }
       __syncthreads();
       mn = ~0ull;
       mx = 0;
-      for (int x = 0; x < nw; ++x) {
-        const uint64_t a = (uint64_t)lds.slot[set][x][0] | ((uint64_t)lds.slot[set][x][1] << 32);
-        const uint64_t c = (uint64_t)lds.slot[set][x][2] | ((uint64_t)lds.slot[set][x][3] << 32);
+      for (int x = 0; x < nwv; ++x) {
+        const uint64_t a = (uint64_t)lds.uslot[set][x][0] | ((uint64_t)lds.uslot[set][x][1] << 32);
+        const uint64_t c = (uint64_t)lds.uslot[set][x][2] | ((uint64_t)lds.uslot[set][x][3] << 32);
         mn = a < mn ? a : mn;
         mx = c > mx ? c : mx;
       }
       set ^= 1;
-      lo = mn;
-      hi = mx;
-      if (found + cnt_s <= (uint32_t)kCap) {
-        mode = 2;
+      // 8-bit digit at the highest bit where mn and mx differ: they fall in
+      // different bins, so every pass shrinks the range.
+      const int hb = mn == mx ? 0 : 63 - __builtin_clzll(mn ^ mx);
+      const int shift = hb > 7 ? hb - 7 : 0;
+      const uint64_t base = mn >> shift;
+      if (w == 0) reinterpret_cast<u32x4*>(lds.hist)[lane] = u32x4{0u, 0u, 0u, 0u};
+      __syncthreads();
+#pragma unroll
+      for (int e = 0; e < kEPL; ++e) {
+        asm volatile("" : "+v"(sv[e]));
+        if (sv[e] != ninf) {
+          const uint64_t c = composite(sv[e], (uint32_t)(wbase + lbase + elem_off<BF16>(e)));
+          if (c >= lo && c <= hi)
+            __hip_atomic_fetch_add(&lds.hist[(uint32_t)((c >> shift) - base)], 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+      }
+      __syncthreads();
+      const Boundary r = find_boundary<false>(lds, need, lane);
+      thr = (base + r.bin) << shift;
+      if (found + r.above + r.cnt <= kCap) {
+        nc = found + r.above + r.cnt;
         break;
       }
-      need -= above_s;
-      float_pass = false;
+      const uint64_t top = base + r.bin + 1;
+      if (shift + (64 - __builtin_clzll(top)) <= 64) {
+        const uint64_t h2 = (top << shift) - 1;
+        hi = h2 < hi ? h2 : hi;
+      }
+      lo = thr;
+      need -= r.above;
+      found += r.above;
+    }
+#pragma unroll
+    for (int e = 0; e < kEPL; ++e) {
+      if (sv[e] != ninf) {
+        const uint64_t c = composite(sv[e], (uint32_t)(wbase + lbase + elem_off<BF16>(e)));
+        if (c >= thr) {
+          const uint32_t p = __hip_atomic_fetch_add(&lds.ncur, 1u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_WORKGROUP);
+          if (p < kCap) lds.cand[p] = c;
+        }
+      }
     }
   }
+  __syncthreads();
 
-  // Compaction of the candidates into LDS.
-  auto is_cand = [&](int e) {
-    if (key[e] == 0u) return false;
-    if (mode == 0) return true;
-    if (mode == 1) {
-      const float f = (key_score(key[e]) - vmin) * scale;
-      const uint32_t bin = f >= (float)(kBins - 1) ? (uint32_t)(kBins - 1) : (uint32_t)f;
-      return (int)bin >= bstar;
+  // Ranks: each candidate counts the candidates of its segment ahead of it.
+  const int stride = 64 * nwv;
+  const int t = w * 64 + lane;
+  const int64_t ob = row * K;
+  for (uint32_t i = (uint32_t)t; i < nc; i += (uint32_t)stride) {
+    const uint64_t mine = lds.cand[i];
+    uint32_t st = 0, len = nc;
+    if (!refine) {
+      const uint32_t bb = fbin(key_score((uint32_t)(mine >> 32)), s, o);
+      st = lds.above[bb];
+      len = lds.hist[bb];
     }
-    return composite(key[e], elem_id<BF16>(e, lane, w)) >= lo;
-  };
-  uint32_t mine = 0;
-#pragma unroll
-  for (int e = 0; e < kEPL; ++e) mine += is_cand(e);
-  uint32_t off = wave_excl_scan(mine, lane);
-  const uint32_t wtot = wave_reduce(mine, Add());
-  if (lane == 0) lds.slot[set][w][0] = wtot;
-  __syncthreads();
-  uint32_t base = 0, nc = 0;
-  for (int x = 0; x < nw; ++x) {
-    const uint32_t t = lds.slot[set][x][0];
-    base += x < w ? t : 0u;
-    nc += t;
+    st = st < nc ? st : nc;
+    const uint32_t end = len < nc - st ? st + len : nc;
+    uint32_t r = st;
+    for (uint32_t j = st; j < end; ++j) r += lds.cand[j] > mine ? 1u : 0u;
+    const uint32_t id = 0xffffffffu - (uint32_t)mine;
+    if (r < (uint32_t)K && id < (uint32_t)g.NB) {
+      g.out_blocks[ob + r] = (int32_t)id;
+      g.out_pages[ob + r] = g.page_table[(int64_t)b * g.NB + id];
+    }
   }
-  off += base;
-#pragma unroll
-  for (int e = 0; e < kEPL; ++e)
-    if (is_cand(e)) lds.cand[off++] = composite(key[e], elem_id<BF16>(e, lane, w));
-  __syncthreads();
-  if (w != 0) return;
-
-  const int n = (int)nc;
-  if (n <= 64) sort_and_write<1>(lds.cand, n, lane, g, row, b);
-  else if (n <= 128) sort_and_write<2>(lds.cand, n, lane, g, row, b);
-  else if (n <= 256) sort_and_write<4>(lds.cand, n, lane, g, row, b);
-  else sort_and_write<8>(lds.cand, n, lane, g, row, b);
+  for (int i = (int)nc + t; i < K; i += stride) {
+    g.out_blocks[ob + i] = -1;
+    g.out_pages[ob + i] = -1;
+  }
 }
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
