@@ -18,8 +18,9 @@
 //
 // Selection is exact and never runs a sorting network:
 //   1. The fp32 range [vmin, vmax] of the selectable scores (non-selectable
-//      blocks hold -inf) defines 256 bins, bin(v) = clamp(v * s + o, 0, 255)
-//      with s = 256 / (vmax - vmin): a monotone function of the score.
+//      blocks hold -inf) defines 255 bins, bin(v) = clamp((v - vmin) * s +
+//      1.5, 0, 255) with s = 255 / (vmax - vmin): a monotone function of the
+//      score, 0 only for -inf.
 //   2. An LDS histogram of the bins; its suffix sums above(b) (blocks in
 //      higher bins) give the boundary bin b* holding the top_k-th block.
 //      The candidates are the blocks of bins >= b*: found = above(b*) of them
@@ -52,6 +53,8 @@ constexpr int kMaxWaves = FAGQ_DSA_MAX_NB / kChunk;
 constexpr int kBins = 256;
 constexpr uint32_t kCap = 512;               // candidates held at most
 constexpr int kMaxTopK = FAGQ_DSA_MAX_TOP_K;
+constexpr int64_t kMaxGridYZ = 65535;        // H and B are grid dimensions y and z
+constexpr int64_t kMaxGridX = (1ll << 24) - 1;   // Q * 256 work-items < 2^32
 static_assert(kMaxWaves * kChunk == FAGQ_DSA_MAX_NB, "waves per row");
 
 struct DArgs {
@@ -65,13 +68,21 @@ struct DArgs {
   int32_t block_size;
   int32_t top_k;
   int32_t index64;       // q_pos / kv_lens are int64
+  // n / block_size for n < 2^32 (Granlund-Montgomery, unsigned):
+  // t = mulhi(bs_mul, n), n / block_size = (t + ((n - t) >> bs_sh1)) >> bs_sh2.
+  uint32_t bs_mul, bs_sh1, bs_sh2;
 };
+
+__device__ __forceinline__ uint32_t div_bs(const DArgs& g, uint32_t n) {
+  const uint32_t t = __umulhi(g.bs_mul, n);
+  return (t + ((n - t) >> g.bs_sh1)) >> g.bs_sh2;
+}
 
 struct Lds {
   uint32_t hist[kBins + 64];        // bin counts, then one discard word per lane
   uint32_t fill[kBins];             // per-bin scatter cursors
   uint32_t above[kBins];            // candidates in higher bins (segment starts)
-  uint64_t cand[kCap];
+  uint64_t cand[kCap + 4];           // 4 spare entries: the rank loop reads in fours
   float fslot[kMaxWaves][2];        // per-wave max / min
   uint32_t uslot[2][kMaxWaves][4];  // per-wave partials of the refinement
   uint32_t ncur;                    // refinement scatter cursor
@@ -167,11 +178,18 @@ __device__ __forceinline__ uint64_t composite(float v, uint32_t id) {
   return ((uint64_t)score_key(v) << 32) | (uint64_t)(0xffffffffu - id);
 }
 
-// Histogram bin of a score.  fmaxf/fminf return the non-NaN operand, so the
-// result is in [0, 255] for every input, and it is non-decreasing in v.
-__device__ __forceinline__ uint32_t fbin(float v, float s, float o) {
-  return (uint32_t)fminf(fmaxf(fmaf(v, s, o), 0.0f), (float)(kBins - 1));
+// Histogram bin of a score under the linear map of [vmin, vmax] (s = 255 /
+// (vmax - vmin), finite and positive): clamp(fma(v - vmin, s, 1.5), 0, 255)
+// truncated.  It is non-decreasing in v; a selectable score (v >= vmin) gets
+// a bin in [1, 255] and -inf gets bin 0.
+__device__ __forceinline__ uint32_t fbin(float v, float vmin, float s) {
+  return (uint32_t)fminf(fmaxf(fmaf(v - vmin, s, 1.5f), 0.0f), (float)(kBins - 1));
 }
+
+template <bool B>
+struct BoolC {
+  static constexpr bool value = B;
+};
 
 // Block id of score e of a lane in wave w: 16-byte vector e / VEC covers
 // 64 * VEC consecutive blocks, the lane's VEC of them at lane * VEC.
@@ -183,15 +201,17 @@ __device__ __forceinline__ int elem_off(int e) {
 
 // Boundary of a histogram in hist[0..255]: the bin b with
 // above(b) < need <= above(b) + hist[b], above(b) = count in bins > b.
-// Every lane receives bin, above(bin), hist[bin] and the histogram total;
-// with STORE, above(b) is also written to lds.above (identical values from
+// Every lane receives bin, above(bin), hist[bin] and the histogram total.
+// STORE marks the fp32-bin histogram: its bin 0 (non-selectable blocks) is
+// left out, and above(b) is written to lds.above (identical values from
 // every wave).
 struct Boundary {
   uint32_t bin, above, cnt, total;
 };
 template <bool STORE>
 __device__ __forceinline__ Boundary find_boundary(Lds& lds, uint32_t k, int lane) {
-  const u32x4 h = reinterpret_cast<const u32x4*>(lds.hist)[lane];   // bins 4 lane .. 4 lane + 3
+  u32x4 h = reinterpret_cast<const u32x4*>(lds.hist)[lane];   // bins 4 lane .. 4 lane + 3
+  if (STORE && lane == 0) h[0] = 0u;     // fp32 bins: bin 0 counts non-selectable blocks
   const uint32_t sum = h[0] + h[1] + h[2] + h[3];
   const uint32_t incl = wave_incl_scan(sum);
   Boundary r;
@@ -221,6 +241,13 @@ __device__ __forceinline__ Boundary find_boundary(Lds& lds, uint32_t k, int lane
   return r;
 }
 
+// Score c of a 16-byte vector (c < 8 for bf16, c < 4 for fp32).
+template <bool BF16>
+__device__ __forceinline__ float vec_elem(const u32x4& d, int c) {
+  if constexpr (BF16) return c % 2 ? bf16_hi(d[c / 2]) : bf16_lo(d[c / 2]);
+  else return __uint_as_float(d[c]);
+}
+
 // ----------------------------------------------------------------- kernel
 
 template <bool BF16>
@@ -229,19 +256,30 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
   __shared__ Lds lds;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t row = blockIdx.x;
+  // Grid (Q, H, B): row = (b * H + h) * Q + q.
+  const int q = (int)blockIdx.x;
+  const int b = (int)blockIdx.z;
+  const int64_t row = ((int64_t)b * g.H + (int64_t)blockIdx.y) * g.Q + q;
   const int K = g.top_k;
-  const int q = (int)(row % g.Q);
-  const int b = (int)((row / g.Q) / g.H);
   const int64_t pos = g.index64 ? ((const int64_t*)g.q_pos)[(int64_t)b * g.Q + q]
                                 : (int64_t)((const int32_t*)g.q_pos)[(int64_t)b * g.Q + q];
   const int64_t kv = g.index64 ? ((const int64_t*)g.kv_lens)[b]
                                : (int64_t)((const int32_t*)g.kv_lens)[b];
-  int64_t vb = (kv + g.block_size - 1) / g.block_size;     // valid_blocks (kv >= 0)
-  vb = vb < g.NB ? vb : g.NB;
-  int64_t last = pos >= 0 ? pos / g.block_size : -1;
-  last = last < vb - 1 ? last : vb - 1;
-  const int nvalid = pos >= 0 && last >= 0 ? (int)(last + 1) : 0;
+  // nvalid = last_block + 1, last_block = min(pos / bs, valid_blocks - 1),
+  // valid_blocks = min(ceil(kv / bs), NB); 0 when pos < 0 or kv == 0.
+  int nvalid = 0;
+  if (pos >= 0 && kv > 0) {
+    int64_t vb, lastp;
+    if (pos <= INT32_MAX && kv <= INT32_MAX) {      // 32-bit operands (bs < 2^31)
+      vb = div_bs(g, (uint32_t)kv + (uint32_t)g.block_size - 1u);
+      lastp = div_bs(g, (uint32_t)pos);
+    } else {
+      vb = (kv - 1) / g.block_size + 1;
+      lastp = pos / g.block_size;
+    }
+    vb = vb < g.NB ? vb : g.NB;
+    nvalid = (int)(lastp < vb - 1 ? lastp : vb - 1) + 1;
+  }
   const int nwv = nvalid > kChunk ? (nvalid + kChunk - 1) / kChunk : 1;   // waves with work
   if (w >= nwv) return;
 
@@ -253,39 +291,34 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
 
   // Scores of the valid prefix; non-selectable blocks hold -inf.  The
   // descriptor covers the prefix rounded up to whole 16-byte vectors (inside
-  // the row: NB is a multiple of VEC), so no vector straddles its end.
+  // the row: NB is a multiple of VEC), so no vector straddles its end.  A
+  // wave whose blocks all lie in the prefix skips the per-block id test.
   constexpr uint32_t esz = BF16 ? 2u : 4u;
   const uint32_t nload = ((uint32_t)nvalid + VEC - 1) / VEC * VEC;
   const rsrc_t rs = make_rsrc((const uint8_t*)g.scores + row * (int64_t)g.NB * esz, nload * esz);
   const int lbase = lane * VEC;                  // lane's first block inside a vector span
   const int wbase = w * kChunk;
+  const bool full = wbase + kChunk <= nvalid;
   const float ninf = -__builtin_inff();
   float sv[kEPL];
   float vmax = ninf, vmin = __builtin_inff();
+  auto load = [&](auto full_c) {
 #pragma unroll
-  for (int i = 0; i < kEPL / VEC; ++i) {
-    const u32x4 d = __builtin_amdgcn_raw_buffer_load_b128(
-        rs, (uint32_t)(wbase * esz) + (uint32_t)(i * 64 + lane) * 16u, 0, 0);
-    float v[VEC];
-    if constexpr (BF16) {
+    for (int i = 0; i < kEPL / VEC; ++i) {
+      const u32x4 d = __builtin_amdgcn_raw_buffer_load_b128(
+          rs, (uint32_t)(wbase * esz) + (uint32_t)(i * 64 + lane) * 16u, 0, 0);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        v[2 * c] = bf16_lo(d[c]);
-        v[2 * c + 1] = bf16_hi(d[c]);
+      for (int c = 0; c < VEC; ++c) {
+        const int e = i * VEC + c;
+        const float v = vec_elem<BF16>(d, c);
+        sv[e] = decltype(full_c)::value || lbase < nvalid - wbase - elem_off<BF16>(e) ? v : ninf;
+        vmax = fmaxf(vmax, sv[e]);
+        vmin = fminf(vmin, sv[e] != ninf ? sv[e] : __builtin_inff());
       }
-    } else {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) v[c] = __uint_as_float(d[c]);
     }
-#pragma unroll
-    for (int c = 0; c < VEC; ++c) {
-      const int e = i * VEC + c;
-      const bool ok = lbase < nvalid - wbase - elem_off<BF16>(e) && v[c] != ninf;
-      sv[e] = ok ? v[c] : ninf;
-      vmax = fmaxf(vmax, sv[e]);
-      vmin = fminf(vmin, ok ? v[c] : __builtin_inff());
-    }
-  }
+  };
+  if (full) load(BoolC<true>());
+  else load(BoolC<false>());
   vmax = __uint_as_float(wave_reduce(__float_as_uint(vmax), FMax()));
   vmin = __uint_as_float(wave_reduce(__float_as_uint(vmin), FMin()));
   if (lane == 0) {
@@ -298,18 +331,31 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
     vmin = fminf(vmin, lds.fslot[x][1]);
   }
 
-  // Bin map; a degenerate or non-finite range puts every score in bin 0.
-  float s = 0.0f, o = 0.0f;
-  if (vmax > vmin) {
-    s = (float)kBins / (vmax - vmin);
-    o = -vmin * s;
-    if (!__builtin_isfinite(s) || !__builtin_isfinite(o)) s = o = 0.0f;
-  }
-  uint32_t bin[kEPL];
+  // Bin map (see fbin); a degenerate or non-finite range puts every
+  // selectable score in bin 1.
+  const float s = (float)(kBins - 1) / (vmax - vmin);
+  const bool degen = !(vmax > vmin) || !(s > 0.0f) || !__builtin_isfinite(s);
+  // Bins of the lane's scores, four 8-bit bins per word (0: not selectable).
+  // Non-selectable blocks count in bin 0 (ignored) in a full wave, where
+  // they are rare, else in the lane's own discard word.
+  uint32_t pbin[kEPL / 4];
+  auto hist = [&](auto full_c, auto binf) {
 #pragma unroll
-  for (int e = 0; e < kEPL; ++e) {
-    bin[e] = sv[e] != ninf ? fbin(sv[e], s, o) : (uint32_t)(kBins + lane);
-    __hip_atomic_fetch_add(&lds.hist[bin[e]], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    for (int e = 0; e < kEPL; ++e) {
+      const uint32_t bn = binf(sv[e]);
+      pbin[e / 4] = e % 4 ? pbin[e / 4] | (bn << (8 * (e % 4))) : bn;
+      const uint32_t at = decltype(full_c)::value || bn ? bn : (uint32_t)(kBins + lane);
+      __hip_atomic_fetch_add(&lds.hist[at], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  };
+  auto bin_lin = [=](float v) { return fbin(v, vmin, s); };
+  auto bin_one = [=](float v) { return v != ninf ? 1u : 0u; };
+  if (!degen) {
+    if (full) hist(BoolC<true>(), bin_lin);
+    else hist(BoolC<false>(), bin_lin);
+  } else {
+    if (full) hist(BoolC<true>(), bin_one);
+    else hist(BoolC<false>(), bin_one);
   }
   __syncthreads();
 
@@ -318,35 +364,55 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
   const bool refine = nc > kCap;
 
   if (!refine) {
-    // Counting-sort scatter of the blocks in bins >= b*.
-    const uint32_t bstar = bd.bin, span = (uint32_t)kBins - bd.bin;
+    // Counting-sort scatter of the blocks in bins >= b* (b* >= 1, so bin 0,
+    // the non-selectable blocks, never qualifies); p < nc <= CAP.  The entry
+    // holds the raw score bits and 0xffffffff - id; the scores become ordered
+    // keys in one pass over the candidates below.
+    const uint32_t bstar = bd.bin > 1u ? bd.bin : 1u;
+    const uint32_t nid = 0xffffffffu - (uint32_t)(wbase + lbase);
 #pragma unroll
     for (int e = 0; e < kEPL; ++e) {
-      if (bin[e] - bstar < span) {
-        const uint32_t p = lds.above[bin[e]] +
-            __hip_atomic_fetch_add(&lds.fill[bin[e]], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if (p < kCap) lds.cand[p] = composite(sv[e], (uint32_t)(wbase + lbase + elem_off<BF16>(e)));
+      const uint32_t bn = (pbin[e / 4] >> (8 * (e % 4))) & 0xffu;
+      if (bn >= bstar) {
+        const uint32_t p = lds.above[bn] +
+            __hip_atomic_fetch_add(&lds.fill[bn], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        lds.cand[p & (kCap - 1)] = ((uint64_t)__float_as_uint(sv[e]) << 32) |
+                                   (uint64_t)(nid - (uint32_t)elem_off<BF16>(e));
       }
     }
   } else {
-    // Radix refinement on the composite key over [lo, hi]; found blocks lie
-    // above hi, need more are inside the range.
+    // Radix refinement on the composite key over [lo, hi]: found blocks lie
+    // above hi, need more inside the range.  The scores are read again from
+    // memory on each pass (this path is rare), so none stay live in VGPRs.
+    auto keys = [&](auto&& f) {
+#pragma unroll 1
+      for (int i = 0; i < kEPL / VEC; ++i) {
+        const u32x4 d = __builtin_amdgcn_raw_buffer_load_b128(
+            rs, (uint32_t)(wbase * esz) + (uint32_t)(i * 64 + lane) * 16u, 0, 0);
+#pragma unroll
+        for (int c = 0; c < VEC; ++c) {
+          const float v = vec_elem<BF16>(d, c);
+          const int off = i * (64 * VEC) + c;
+          if (lbase < nvalid - wbase - off && v != ninf)
+            f(composite(v, (uint32_t)(wbase + lbase + off)));
+        }
+      }
+    };
+    auto uni = [](uint64_t x) {
+      return (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)x) |
+             ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(x >> 32)) << 32);
+    };
     uint64_t lo = 1, hi = ~0ull, thr = 1;
     uint32_t need = (uint32_t)K, found = 0;
     int set = 0;
     for (;;) {
       uint64_t mn = ~0ull, mx = 0;
-#pragma unroll
-      for (int e = 0; e < kEPL; ++e) {
-        asm volatile("" : "+v"(sv[e]));     // keep the keys out of registers across passes
-        if (sv[e] != ninf) {
-          const uint64_t c = composite(sv[e], (uint32_t)(wbase + lbase + elem_off<BF16>(e)));
-          if (c >= lo && c <= hi) {
-            mn = c < mn ? c : mn;
-            mx = c > mx ? c : mx;
-          }
+      keys([&](uint64_t c) {
+        if (c >= lo && c <= hi) {
+          mn = c < mn ? c : mn;
+          mx = c > mx ? c : mx;
         }
-      }
+      });
       mn = wave_reduce64<false>(mn, lane);
       mx = wave_reduce64<true>(mx, lane);
       if (lane == 0) {
@@ -364,6 +430,8 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
         mn = a < mn ? a : mn;
         mx = c > mx ? c : mx;
       }
+      mn = uni(mn);
+      mx = uni(mx);
       set ^= 1;
       // 8-bit digit at the highest bit where mn and mx differ: they fall in
       // different bins, so every pass shrinks the range.
@@ -372,16 +440,11 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
       const uint64_t base = mn >> shift;
       if (w == 0) reinterpret_cast<u32x4*>(lds.hist)[lane] = u32x4{0u, 0u, 0u, 0u};
       __syncthreads();
-#pragma unroll
-      for (int e = 0; e < kEPL; ++e) {
-        asm volatile("" : "+v"(sv[e]));
-        if (sv[e] != ninf) {
-          const uint64_t c = composite(sv[e], (uint32_t)(wbase + lbase + elem_off<BF16>(e)));
-          if (c >= lo && c <= hi)
-            __hip_atomic_fetch_add(&lds.hist[(uint32_t)((c >> shift) - base)], 1u, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_WORKGROUP);
-        }
-      }
+      keys([&](uint64_t c) {
+        if (c >= lo && c <= hi)
+          __hip_atomic_fetch_add(&lds.hist[(uint32_t)((c >> shift) - base)], 1u, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_WORKGROUP);
+      });
       __syncthreads();
       const Boundary r = find_boundary<false>(lds, need, lane);
       thr = (base + r.bin) << shift;
@@ -398,36 +461,44 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
       need -= r.above;
       found += r.above;
     }
-#pragma unroll
-    for (int e = 0; e < kEPL; ++e) {
-      if (sv[e] != ninf) {
-        const uint64_t c = composite(sv[e], (uint32_t)(wbase + lbase + elem_off<BF16>(e)));
-        if (c >= thr) {
-          const uint32_t p = __hip_atomic_fetch_add(&lds.ncur, 1u, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_WORKGROUP);
-          if (p < kCap) lds.cand[p] = c;
-        }
+    keys([&](uint64_t c) {
+      if (c >= thr) {
+        const uint32_t p =
+            __hip_atomic_fetch_add(&lds.ncur, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (p < kCap) lds.cand[p] = c;
       }
-    }
+    });
   }
   __syncthreads();
 
-  // Ranks: each candidate counts the candidates of its segment ahead of it.
   const int stride = 64 * nwv;
   const int t = w * 64 + lane;
+  if (!refine) {
+    for (uint32_t i = (uint32_t)t; i < nc; i += (uint32_t)stride) {
+      const uint64_t c = lds.cand[i];
+      lds.cand[i] = ((uint64_t)score_key(__uint_as_float((uint32_t)(c >> 32))) << 32) | (uint32_t)c;
+    }
+    __syncthreads();
+  }
+
+  // Ranks: each candidate counts the candidates of its segment ahead of it.
   const int64_t ob = row * K;
   for (uint32_t i = (uint32_t)t; i < nc; i += (uint32_t)stride) {
     const uint64_t mine = lds.cand[i];
     uint32_t st = 0, len = nc;
     if (!refine) {
-      const uint32_t bb = fbin(key_score((uint32_t)(mine >> 32)), s, o);
+      const uint32_t bb = degen ? 1u : fbin(key_score((uint32_t)(mine >> 32)), vmin, s);
       st = lds.above[bb];
       len = lds.hist[bb];
     }
     st = st < nc ? st : nc;
     const uint32_t end = len < nc - st ? st + len : nc;
     uint32_t r = st;
-    for (uint32_t j = st; j < end; ++j) r += lds.cand[j] > mine ? 1u : 0u;
+    for (uint32_t j = st; j < end; j += 4) {     // reads stay inside cand[kCap + 4]
+      const uint64_t c0 = lds.cand[j], c1 = lds.cand[j + 1], c2 = lds.cand[j + 2], c3 = lds.cand[j + 3];
+      r += (c0 > mine ? 1u : 0u) + (j + 1 < end && c1 > mine ? 1u : 0u) +
+           (j + 2 < end && c2 > mine ? 1u : 0u) + (j + 3 < end && c3 > mine ? 1u : 0u);
+    }
     const uint32_t id = 0xffffffffu - (uint32_t)mine;
     if (r < (uint32_t)K && id < (uint32_t)g.NB) {
       g.out_blocks[ob + r] = (int32_t)id;
@@ -441,6 +512,18 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
 }
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// Multiplier and shifts of unsigned division by d (1 <= d < 2^31) for
+// dividends below 2^32: l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1
+// (Granlund and Montgomery, "Division by invariant integers using
+// multiplication", 1994, section 4).
+void set_divisor(DArgs& g, uint32_t d) {
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  g.bs_mul = (uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1);
+  g.bs_sh1 = l < 1 ? l : 1;
+  g.bs_sh2 = l > 1 ? l - 1 : 0;
+}
 
 }  // namespace
 }  // namespace dsa
@@ -465,7 +548,8 @@ FAGQ_API int fagq_dsa_topk_launch(const void* scores, int scores_dtype, const vo
   if (NB > FAGQ_DSA_MAX_NB || top_k > kMaxTopK || block_size > INT32_MAX) return FAGQ_E_TOO_LARGE;
   const int64_t rows = B * H * Q;
   const int64_t esz = scores_dtype == FAGQ_DSA_BF16 ? 2 : 4;
-  if (rows > (int64_t)INT32_MAX || NB * esz > (int64_t)UINT32_MAX)
+  if (rows > (int64_t)INT32_MAX || NB * esz > (int64_t)UINT32_MAX || H > kMaxGridYZ ||
+      B > kMaxGridYZ || Q > kMaxGridX)
     return FAGQ_E_TOO_LARGE;
   if (!aligned(scores, 16) || (NB * esz) % 16 != 0 || !aligned(page_table, 4) ||
       !aligned(out_blocks, 4) || !aligned(out_pages, 4) ||
@@ -491,12 +575,14 @@ FAGQ_API int fagq_dsa_topk_launch(const void* scores, int scores_dtype, const vo
   g.block_size = (int32_t)block_size;
   g.top_k = (int32_t)top_k;
   g.index64 = index_dtype == FAGQ_DSA_I64;
+  set_divisor(g, (uint32_t)block_size);
   const bool bf16 = scores_dtype == FAGQ_DSA_BF16;
   const int waves = (int)((NB + kChunk - 1) / kChunk);
   void* args[] = {&g};
   const void* k = bf16 ? (const void*)&dsa_topk_rows<true> : (const void*)&dsa_topk_rows<false>;
-  const hipError_t e = hipLaunchKernel(k, dim3((unsigned)rows), dim3((unsigned)(64 * waves)), args,
-                                       0, static_cast<hipStream_t>(stream));
+  const hipError_t e = hipLaunchKernel(k, dim3((unsigned)Q, (unsigned)H, (unsigned)B),
+                                       dim3((unsigned)(64 * waves)), args, 0,
+                                       static_cast<hipStream_t>(stream));
   return e == hipSuccess ? FAGQ_OK : -(int)e;
 }
 

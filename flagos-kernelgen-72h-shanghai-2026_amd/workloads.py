@@ -204,6 +204,7 @@ class DsaWorkload:
     block_size: int
     dtype: torch.dtype = torch.float32
     seed: int = 0
+    full_rows: bool = False        # every query sees all NB blocks (decode-like)
 
     @property
     def rows(self) -> int:
@@ -217,10 +218,10 @@ class DsaWorkload:
                 + 4 * self.B * self.Q + 4 * self.B)
 
 
-def _dsa(B, H, Q, NB, K, BS, dtype=torch.float32):
+def _dsa(B, H, Q, NB, K, BS, dtype=torch.float32, full_rows=False):
     tag = "bf16" if dtype == torch.bfloat16 else "f32"
-    name = f"dsa_{tag}_b{B}h{H}q{Q}_nb{NB}_k{K}_bs{BS}"
-    return name, DsaWorkload(name, B, H, Q, NB, K, BS, dtype)
+    name = f"dsa_{tag}_b{B}h{H}q{Q}_nb{NB}_k{K}_bs{BS}" + ("_full" if full_rows else "")
+    return name, DsaWorkload(name, B, H, Q, NB, K, BS, dtype, full_rows=full_rows)
 
 
 # The (B, H, Q, NB, top_k, block_size) shapes the reference routes
@@ -231,7 +232,10 @@ DSA_CONFIGS = dict(_dsa(*c) for c in [
     (1, 8, 128, 512, 32, 128), (2, 8, 128, 512, 32, 128), (1, 16, 256, 1024, 32, 128),
     (2, 16, 256, 1024, 64, 128),
 ])
-DSA_CONFIGS.update(dict([_dsa(2, 32, 512, 4096, 128, 64, torch.bfloat16)]))
+DSA_CONFIGS.update(dict([_dsa(2, 32, 512, 4096, 128, 64, torch.bfloat16),
+                         # all rows valid: the worst-case traffic R (4 NB + 12 K) bytes
+                         # (reports/task02_dsa_topk_page_table_transform.md:33-36)
+                         _dsa(2, 32, 512, 4096, 128, 64, full_rows=True)]))
 DSA_HEADLINE = "dsa_f32_b2h32q512_nb4096_k128_bs64"
 
 
@@ -240,13 +244,19 @@ def make_dsa_inputs(w: DsaWorkload):
     workload's dtype; kv_len[b] = NB * block_size - 3 b block_size (at least 1);
     query q of batch b at position (q + 1) kv_len / Q - 1, so the causal prefixes
     of a batch's rows spread evenly from ~kv_len/Q to kv_len tokens;
-    page_table[b] a random permutation of physical pages b * NB ...  int32."""
+    page_table[b] a random permutation of physical pages b * NB ...  int32.
+    With full_rows every kv_len is NB * block_size and every query sits at
+    the last position, so each row selects from all NB blocks."""
     g = torch.Generator(device="cpu").manual_seed(w.seed)
     scores = torch.randn(w.B, w.H, w.Q, w.NB, generator=g).to(w.dtype)
-    kv = torch.tensor([max(1, w.NB * w.block_size - 3 * b * w.block_size) for b in range(w.B)],
-                      dtype=torch.int32)
-    q = torch.arange(w.Q, dtype=torch.int64)
-    q_pos = torch.stack([((q + 1) * int(kv[b]) // w.Q - 1) for b in range(w.B)]).to(torch.int32)
+    if w.full_rows:
+        kv = torch.full((w.B,), w.NB * w.block_size, dtype=torch.int32)
+        q_pos = (kv[:, None] - 1).expand(w.B, w.Q).contiguous()
+    else:
+        kv = torch.tensor([max(1, w.NB * w.block_size - 3 * b * w.block_size)
+                           for b in range(w.B)], dtype=torch.int32)
+        q = torch.arange(w.Q, dtype=torch.int64)
+        q_pos = torch.stack([((q + 1) * int(kv[b]) // w.Q - 1) for b in range(w.B)]).to(torch.int32)
     page_table = torch.stack([b * w.NB + torch.randperm(w.NB, generator=g)
                               for b in range(w.B)]).to(torch.int32)
     return scores, page_table, q_pos, kv

@@ -41,7 +41,8 @@ enum fagq_dsa_index { FAGQ_DSA_I32 = 0, FAGQ_DSA_I64 = 1 };
  * page_table  int32 [B, NB]
  * q_pos       [B, Q], kv_lens [B]: int32 or int64 (index_dtype)
  * out_blocks, out_pages  int32 [B, H, Q, top_k]
- * 1 <= NB <= FAGQ_DSA_MAX_NB, 1 <= top_k <= FAGQ_DSA_MAX_TOP_K, block_size >= 1 */
+ * 1 <= NB <= FAGQ_DSA_MAX_NB, 1 <= top_k <= FAGQ_DSA_MAX_TOP_K, 1 <= block_size < 2^31,
+ * B and H <= 65535, Q < 2^24 (FAGQ_E_TOO_LARGE otherwise) */
 FAGQ_API int fagq_dsa_topk_launch(const void* scores, int scores_dtype, const void* page_table,
                                   const void* q_pos, const void* kv_lens, int index_dtype,
                                   void* out_blocks, void* out_pages, int64_t B, int64_t H,

@@ -247,3 +247,29 @@ def test_gemm_workloads():
     again = make_gemm_inputs(w)
     assert torch.equal(again[0].view(torch.uint8), a_q.view(torch.uint8))
     assert GEMM_CONFIGS["gemm_dsv3_16384x4096x7168"].flops() == 2 * 16384 * 4096 * 7168
+
+
+# --------------------------------------------------------- DSA top-k transform
+
+def dsa_call(lib, **kw):
+    a = dict(s=fake(0), sd=0, pt=fake(1), qp=fake(2), kv=fake(3), idx=0, ob=fake(4), op=fake(5),
+             B=2, H=4, Q=8, NB=1024, bs=64, k=128)
+    a.update(kw)
+    return lib.fagq_dsa_topk_launch(a["s"], a["sd"], a["pt"], a["qp"], a["kv"], a["idx"], a["ob"],
+                                    a["op"], a["B"], a["H"], a["Q"], a["NB"], a["bs"], a["k"], None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(s=None), 1), (dict(pt=None), 1), (dict(qp=None), 1), (dict(kv=None), 1),
+    (dict(ob=None), 1), (dict(op=None), 1),
+    (dict(sd=2), 5), (dict(idx=-1), 5),
+    (dict(B=-1), 2), (dict(NB=0), 2), (dict(bs=0), 2), (dict(k=0), 2),
+    (dict(NB=4097), 7), (dict(k=257), 7), (dict(bs=1 << 31), 7),
+    (dict(H=65536), 7), (dict(B=65536), 7), (dict(Q=1 << 24), 7),
+    (dict(s=ctypes.c_void_p(BASE + 8)), 4), (dict(NB=1022), 4), (dict(NB=1020, sd=1), 4),
+    (dict(qp=ctypes.c_void_p(BASE + 0x2_0000_0004), idx=1), 4),
+    (dict(op=fake(4)), 9), (dict(op=ctypes.c_void_p(BASE + 0x4_0000_0100)), 9),
+    (dict(Q=0), 0),
+])
+def test_dsa_validation(lib, kw, status):
+    assert dsa_call(lib, **kw) == status

@@ -88,6 +88,23 @@ def test_dsa_special_values(pkg, gpu):
     check(pkg, gpu, s, pt, pos, kv, 16, 64, "special values")
 
 
+@pytest.mark.parametrize("bs", [1, 3, 100])
+def test_dsa_odd_block_sizes(pkg, gpu, bs):
+    s, pt, pos, kv = case(21 + bs, NB=1000, bs=bs)
+    check(pkg, gpu, s, pt, pos, kv, bs, 64, f"block_size={bs}")
+
+
+def test_dsa_int64_positions_past_2_31(pkg, gpu):
+    s, pt, pos, kv = case(31, NB=1024, Q=16, idx=torch.int64)
+    g = torch.Generator().manual_seed(5)
+    bs = 1 << 22
+    kv[0], kv[1] = 1 << 33, (1 << 31) + 5 * bs
+    pos[0] = torch.randint(-2, 1 << 34, (16,), generator=g)
+    pos[1] = torch.randint(0, 1 << 32, (16,), generator=g)
+    pos[1, 0] = (1 << 31) + 5 * bs - 1
+    check(pkg, gpu, s, pt, pos, kv, bs, 128, "int64 positions past 2^31")
+
+
 def test_dsa_zero_kv_and_negative_pos(pkg, gpu):
     s, pt, pos, kv = case(12, NB=512, Q=8)
     kv[1] = 0
