@@ -122,9 +122,11 @@ def main() -> int:
     if args.copy:
         return copy_bench(args, torch, pkg)
     name = args.config or HEADLINE
-    from fagq_mi355x.workloads import DSA_CONFIGS, GEMM_CONFIGS, PARTS_CONFIGS
+    from fagq_mi355x.workloads import DSA_CONFIGS, GEMM_CONFIGS, MLA_CONFIGS, PARTS_CONFIGS
     if name in DSA_CONFIGS:
         return dsa_bench(args, torch, pkg, DSA_CONFIGS[name])
+    if name in MLA_CONFIGS:
+        return mla_bench(args, torch, pkg, MLA_CONFIGS[name])
     if name in GEMM_CONFIGS:
         return gemm_bench(args, torch, pkg, GEMM_CONFIGS[name])
     if name in PARTS_CONFIGS:
@@ -517,6 +519,130 @@ def dsa_bench(args, torch, pkg, w) -> int:
         out["cpu_baseline"] = dsa_cpu_baseline(w, scores, pt, pos, kv, sets[0], nbytes, args, torch)
     print(json.dumps(out), flush=True)
     return 0
+
+
+def mla_bench(args, torch, pkg, w) -> int:
+    """Times fagq_mla_bwd_launch (Task 03; four kernels per call) with inputs
+    resident in HBM, do / dq / dc sets rotated past the MALL; per-call time by
+    HIP events on the launch stream."""
+    import ctypes
+    from fagq_mi355x import _lib
+    from fagq_mi355x.workloads import make_mla_inputs
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = _lib.load()
+    q, c, out, do0, lse = make_mla_inputs(w, device=dev)
+    nbytes = w.algorithmic_bytes()
+    set_bytes = do0.numel() * 2 + do0.numel() * (2 if w.grad_dtype == torch.bfloat16 else 4)
+    nsets = max(1, min(16, math.ceil(ROTATE_BYTES / set_bytes) + 1)) if set_bytes < ROTATE_BYTES else 1
+    ws_bytes = lib.fagq_mla_bwd_workspace_bytes(w.B, w.S, w.D)
+    sets = []
+    for i in range(nsets):
+        d = do0 if i == 0 else do0.clone()
+        sets.append((d, torch.empty(w.B, w.H, w.S, w.D, dtype=w.grad_dtype, device=dev),
+                     torch.empty(w.B, w.S, w.D, dtype=w.grad_dtype, device=dev),
+                     torch.empty(ws_bytes, dtype=torch.uint8, device=dev)))
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    gcode = 1 if w.grad_dtype == torch.bfloat16 else 0
+
+    def step(i: int):
+        d, dq, dc, ws = sets[i % nsets]
+        st = lib.fagq_mla_bwd_launch(P(q), P(c), P(out), P(d), P(lse), P(dq), P(dc), P(ws), ws_bytes,
+                                     w.B, w.H, w.S, w.D, w.sm_scale, gcode, gcode, sp)
+        if st:
+            _lib.check(st, "fagq_mla_bwd_launch")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize(dev)
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    for i in range(args.steps):
+        starts[i].record(stream)
+        step(i)
+        ends[i].record(stream)
+    torch.cuda.synchronize(dev)
+    durs = sorted(a.elapsed_time(b) for a, b in zip(starts, ends))
+    kern_ms = sum(durs) / len(durs)
+    value = nbytes / (wall_ms * 1e-3) / 1e9
+    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    out_json = {
+        "metric": "MLA backward (Task 03) dQ+dC: algorithmic GB/s (% of 8 TB/s) + us/call",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 in, fp32 accumulate, " + ("bf16" if gcode else "fp32") + " gradients",
+        "data": "synthetic",
+        "config": {"workload": w.name, "B": w.B, "H": w.H, "S": w.S, "D": w.D,
+                   "sm_scale": w.sm_scale, "algorithmic_bytes": nbytes, "buffer_sets": nsets},
+        "us_per_call": round(kern_ms * 1e3, 2),
+        "us_per_call_median": round(durs[len(durs) // 2] * 1e3, 2),
+        "us_per_call_host_wall": round(wall_ms * 1e3, 2),
+        "pct_of_peak": round(100.0 * achieved / PEAK_HBM_GBS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None},
+        "cpu_baseline": None,
+    }
+    if args.cpu_seconds > 0:
+        out_json["cpu_baseline"] = mla_cpu_baseline(w, q, c, out, do0, lse, pkg, args, torch)
+    print(json.dumps(out_json), flush=True)
+    return 0
+
+
+def mla_cpu_baseline(w, q, c, out, do, lse, pkg, args, torch) -> dict:
+    """Times the C oracle on batch 0, heads 0..7 (all S rows) and checks the GPU
+    operator on the same sample against it (rows >= 16 of dq bit-exact)."""
+    import dataclasses
+    import numpy as np
+    import oracle
+    threads = max(1, min(16, os.cpu_count() or 1))
+    hs = min(8, w.H)
+    sw = dataclasses.replace(w, B=1, H=hs)
+    sq, sc, so, sd, sl = (q[:1, :hs].contiguous(), c[:1].contiguous(), out[:1, :hs].contiguous(),
+                          do[:1, :hs].contiguous(), lse[:1, :hs].contiguous())
+    bits = lambda t: t.cpu().view(torch.uint16).numpy()
+    aq, ac, ao, ad, al = bits(sq), bits(sc), bits(so), bits(sd), sl.cpu().numpy()
+
+    def run():
+        return oracle.mla_bwd(aq, ac, ao, ad, al, w.sm_scale, with_bound=False, nthreads=threads)
+
+    rdq, rdc, _ = run()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < args.cpu_seconds and len(times) < 100):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    t = times[len(times) // 2]
+    gq = torch.empty_like(sq, dtype=w.grad_dtype)
+    gc = torch.empty_like(sc, dtype=w.grad_dtype)
+    pkg.mla_bwd_nope_dkdv(sq, sc, so, sd, sl, gq, gc, w.sm_scale)
+    torch.cuda.synchronize()
+    E = sw.exact_rows
+    want = torch.from_numpy(rdq[:, :, E:].astype(np.float32)).to(w.grad_dtype)
+    ok = bool(torch.equal(gq[:, :, E:].cpu(), want))
+    dc_err = float(np.abs(gc.float().cpu().numpy() - rdc).max() / max(np.abs(rdc).max(), 1e-30))
+    return {"value": round(sw.algorithmic_bytes() / t / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port", "us_per_call": round(t * 1e6, 1),
+            "sample": f"batch 0, heads 0..{hs - 1} of {w.name} (B=1, H={hs}, S={w.S}, D={w.D}), "
+                      f"C oracle (OpenMP), median of {len(times)} runs; GB/s of that sample's "
+                      f"algorithmic bytes",
+            "parity_vs_gpu_sample": {"dq_rows_past_prefix_bit_exact": ok,
+                                     "dc_max_rel_err": dc_err}}
 
 
 def dsa_cpu_baseline(w, scores, pt, pos, kv, gpu_set, nbytes, args, torch) -> dict:

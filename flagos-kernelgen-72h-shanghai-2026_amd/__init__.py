@@ -10,6 +10,7 @@ from . import _lib
 from ._lib import FagqError, load as load_library
 from .dsa_topk import dsa_topk_page_table_transform
 from .gemm import fp8_block_scaled_gemm, gemm_route
+from .mla_bwd import mla_bwd_nope_dkdv
 from .ops import (empty_scales, fused_add_rmsnorm_group_quant, fused_add_rmsnorm_group_quant_fn,
                   fused_reduce_add_rmsnorm_group_quant, route_for)
 
@@ -23,5 +24,6 @@ __all__ = [
     "fused_reduce_add_rmsnorm_group_quant",
     "gemm_route",
     "load_library",
+    "mla_bwd_nope_dkdv",
     "route_for",
 ]

@@ -79,6 +79,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     units.append((CSRC / "fagq_api.hip", OBJ_DIR / "fagq_api.o", []))
     units.append((CSRC / "fagq_gemm.hip", OBJ_DIR / "fagq_gemm.o", []))
     units.append((CSRC / "dsa_topk.hip", OBJ_DIR / "dsa_topk.o", []))
+    units.append((CSRC / "mla_bwd.hip", OBJ_DIR / "mla_bwd.o", []))
     jobs = jobs or min(len(units), max(1, min(16, os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         futs = [ex.submit(_run, [cc, *flags, *defs, "-c", str(src), "-o", str(obj)], verbose)

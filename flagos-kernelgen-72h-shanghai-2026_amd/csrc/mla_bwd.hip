@@ -1,0 +1,491 @@
+// mla_bwd.hip - gfx950 MLA backward (NoPE, shared K = V = C): dQ and dC as
+// the reference's Task 03 operator computes them (C ABI: include/fagq_mla.h).
+//
+// Function (reference: src/task03_mla_bwd_nope_dkdv.py:401-425, :453-480):
+//   rows i < E = min(16, S) of every (b, h): exact dq_i = sum_j dS_ij c_j with
+//     P_ij = bf16(exp2((q_i . c_j * scale - lse_i) * log2 e)), j <= i,
+//     dS_ij = bf16(P_ij (do_i . c_j - delta_i) scale), delta_i = out_i . do_i
+//   rows i >= E: dq_i = scale * do_i
+//   dc_j = sum_{i >= j} hs_i / (i + 1), hs_i = sum_h do[h, i]
+//
+// Kernels, in stream order:
+//   K1 mla_stream_do   - the one pass over dO (all the HBM traffic): per row
+//                        and all H heads, dq = scale * do (rows >= E) and the
+//                        head sum, stored as hs_i / (i + 1) in the workspace.
+//                        A lane owns 8 consecutive dims (16-byte loads), a
+//                        workgroup 2048 / D rows, so each head contributes a
+//                        contiguous 4 KB (D = 512) segment per workgroup.
+//   K0 mla_exact_rows  - per (b, h) and 4 query rows: q, do rows and c rows
+//                        0..E-1 in LDS, the logits and dP by fp32 dot
+//                        products (4 lanes per (query, key) pair), P and dS
+//                        rounded to bf16 where the reference rounds, dq rows.
+//   K2 mla_block_total - per block of 16-64 rows: fp32 totals of hs / (i + 1)
+//                        (summed over the head groups' partial planes).
+//   K3 mla_suffix_scan - per block: carry = totals of all later blocks, then
+//                        the reverse running sum over the block, written as dc.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fagq.h"
+#include "fagq_dispatch.hpp"
+#include "fagq_mla.h"
+
+namespace fagq {
+namespace mla {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kE = FAGQ_MLA_EXACT_ROWS;
+constexpr int kMaxD = FAGQ_MLA_MAX_D;
+constexpr int kPadElems = 8;             // LDS row padding (bf16 elements) for K0
+#ifndef FAGQ_MLA_HEADS_IN_FLIGHT
+#define FAGQ_MLA_HEADS_IN_FLIGHT 2
+#endif
+constexpr int kHeadsInFlight = FAGQ_MLA_HEADS_IN_FLIGHT;   // K1 loads per batch
+
+struct MArgs {
+  const uint16_t* q;
+  const uint16_t* c;
+  const uint16_t* out;
+  const uint16_t* dout;
+  const float* lse;
+  void* dq;
+  void* dc;
+  float* hs;          // workspace: [hsplit, B, S, D] partial head sums / (i + 1)
+  float* tot;         // workspace: [B, nblk, D] block totals
+  int64_t hs_split;   // elements between the partial head-sum planes (B * S * D)
+  int32_t brows;      // rows per scan block
+  int32_t nblk;       // ceil(S / brows)
+  int32_t hsplit;     // head groups K1 splits the heads into
+  int32_t hps;        // heads per group
+  int32_t H, S, D;
+  int32_t erows;      // min(16, S)
+  float scale;
+  int32_t dq_bf16;    // dq is bf16 (else fp32)
+  int32_t dc_bf16;
+};
+
+__device__ __forceinline__ float bf16_to_f(uint32_t h) { return __uint_as_float(h << 16); }
+
+// fp32 -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t f_to_bf16(float v) { return pack_bf16x2(v, 0.0f) & 0xffffu; }
+__device__ __forceinline__ float round_bf16(float v) { return bf16_to_f(f_to_bf16(v)); }
+
+// Stores 8 fp32 values at element offset e of an fp32 or bf16 tensor.
+__device__ __forceinline__ void store8(const rsrc_t& rs, bool bf16, uint32_t e, const float (&v)[8]) {
+  if (bf16) {
+    const u32x4 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                     pack_bf16x2(v[6], v[7])};
+    __builtin_amdgcn_raw_buffer_store_b128(w, rs, e * 2u, 0, kNonTemporal);
+  } else {
+    const u32x4 a = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                     __float_as_uint(v[3])};
+    const u32x4 b = {__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]),
+                     __float_as_uint(v[7])};
+    __builtin_amdgcn_raw_buffer_store_b128(a, rs, e * 4u, 0, kNonTemporal);
+    __builtin_amdgcn_raw_buffer_store_b128(b, rs, e * 4u + 16u, 0, kNonTemporal);
+  }
+}
+
+// ------------------------------------------------------------------ K1
+
+// grid (ceil(S / rows_per_wg), B, hsplit); rows_per_wg = 256 / (D / 8);
+// z picks the head group [z hps, min(H, (z + 1) hps)).
+__global__ void __launch_bounds__(kThreads) mla_stream_do(const MArgs g) {
+  const int lpr = g.D / 8;                        // lanes per row
+  const int t = threadIdx.x;
+  const int row = (int)blockIdx.x * (kThreads / lpr) + t / lpr;
+  if (row >= g.S) return;
+  const int b = (int)blockIdx.y;
+  const int hbeg = (int)blockIdx.z * g.hps;
+  const int hend = hbeg + g.hps < g.H ? hbeg + g.hps : g.H;
+  const uint32_t hsd = (uint32_t)g.H * (uint32_t)g.S * (uint32_t)g.D;    // elements per batch
+  const rsrc_t rdo = make_rsrc(g.dout + (int64_t)b * hsd, hsd * 2u);
+  const rsrc_t rdq = make_rsrc((const uint8_t*)g.dq + (int64_t)b * hsd * (g.dq_bf16 ? 2 : 4),
+                               hsd * (g.dq_bf16 ? 2u : 4u));
+  const uint32_t e0 = (uint32_t)row * (uint32_t)g.D + (uint32_t)(t % lpr) * 8u;   // head 0
+  const uint32_t hstride = (uint32_t)g.S * (uint32_t)g.D;
+  const bool write_dq = row >= g.erows;
+  const bool dq_bf16 = g.dq_bf16 != 0;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  // Heads in batches of U, software-pipelined: the loads of batch i + 1 are
+  // issued before batch i is consumed.  Heads past hend re-read head hend - 1
+  // (in bounds) and are not used.
+  constexpr int U = kHeadsInFlight;
+  auto load_batch = [&](int h0, u32x4 (&v)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int h = h0 + u < hend ? h0 + u : hend - 1;
+      v[u] = __builtin_amdgcn_raw_buffer_load_b128(rdo, (e0 + (uint32_t)h * hstride) * 2u, 0,
+                                                   kNonTemporal);
+    }
+  };
+  u32x4 cur[U], nxt[U];
+  load_batch(hbeg, cur);
+  for (int h0 = hbeg; h0 < hend; h0 += U) {
+    if (h0 + U < hend) load_batch(h0 + U, nxt);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (h0 + u < hend) {
+        float f[8];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          f[2 * k] = bf16_lo(cur[u][k]);
+          f[2 * k + 1] = bf16_hi(cur[u][k]);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[k] += f[k];
+        if (write_dq) {
+          float d[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) d[k] = f[k] * g.scale;
+          store8(rdq, dq_bf16, e0 + (uint32_t)(h0 + u) * hstride, d);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) cur[u] = nxt[u];
+  }
+  const float n1 = (float)(row + 1);
+  float o[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) o[k] = acc[k] / n1;
+  const uint32_t sd = (uint32_t)g.S * (uint32_t)g.D;
+  const rsrc_t rhs = make_rsrc(g.hs + (int64_t)blockIdx.z * g.hs_split + (int64_t)b * sd, sd * 4u);
+  store8(rhs, false, (uint32_t)row * (uint32_t)g.D + (uint32_t)(t % lpr) * 8u, o);
+}
+
+// ------------------------------------------------------------------ K0
+
+constexpr int kRowsK0 = 4;                // query rows per workgroup, one wave each
+
+// grid (B * H, ceil(E / 4)).  Wave w owns query row m = 4 blockIdx.y + w; its
+// lane 4 n + k computes quarter k of the dims of the dot products with key n
+// (n < 16), the quarters joined by two DPP steps.  Dynamic LDS: q and do rows
+// of the workgroup, c rows 0..E-1 (rows padded by 16 bytes), then dS.
+__global__ void __launch_bounds__(kThreads) mla_exact_rows(const MArgs g) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int D = g.D, E = g.erows;
+  const int ld = D + kPadElems;                   // bf16 elements per LDS row
+  uint16_t* qs = reinterpret_cast<uint16_t*>(smem);
+  uint16_t* dos = qs + kRowsK0 * ld;
+  uint16_t* cs = dos + kRowsK0 * ld;
+  float* dS = reinterpret_cast<float*>(cs + kE * ld);   // [kRowsK0][kE]
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int bh = (int)blockIdx.x;
+  const int b = bh / g.H;
+  const int m0 = (int)blockIdx.y * kRowsK0;
+  const int m = m0 + w;
+  const int64_t qrow0 = (int64_t)bh * g.S * D;    // q, do, out rows of (b, h)
+  const int64_t crow0 = (int64_t)b * g.S * D;
+  const int kmax = m0 + kRowsK0 < E ? m0 + kRowsK0 : E;   // keys 0..kmax-1 are needed
+
+  const int cpr = D / 8;                          // 16-byte chunks per row
+  for (int i = t; i < kRowsK0 * cpr; i += kThreads) {
+    const int r = i / cpr, k = i % cpr;
+    u32x4 a = {0u, 0u, 0u, 0u}, d = a;
+    if (m0 + r < E) {
+      a = *reinterpret_cast<const u32x4*>(g.q + qrow0 + (int64_t)(m0 + r) * D + k * 8);
+      d = *reinterpret_cast<const u32x4*>(g.dout + qrow0 + (int64_t)(m0 + r) * D + k * 8);
+    }
+    *reinterpret_cast<u32x4*>(qs + r * ld + k * 8) = a;
+    *reinterpret_cast<u32x4*>(dos + r * ld + k * 8) = d;
+  }
+  for (int i = t; i < kmax * cpr; i += kThreads) {
+    const int r = i / cpr, k = i % cpr;
+    *reinterpret_cast<u32x4*>(cs + r * ld + k * 8) =
+        *reinterpret_cast<const u32x4*>(g.c + crow0 + (int64_t)r * D + k * 8);
+  }
+  // delta_m = out_m . do_m (wave-wide), read from global memory.
+  float delta = 0.0f;
+  if (m < E) {
+    for (int k = lane; k < cpr; k += 64) {
+      const u32x4 o = *reinterpret_cast<const u32x4*>(g.out + qrow0 + (int64_t)m * D + k * 8);
+      const u32x4 d = *reinterpret_cast<const u32x4*>(g.dout + qrow0 + (int64_t)m * D + k * 8);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        delta += bf16_lo(o[j]) * bf16_lo(d[j]);
+        delta += bf16_hi(o[j]) * bf16_hi(d[j]);
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) delta += __shfl_xor(delta, off, 64);
+  __syncthreads();
+
+  // Logits and dP of (m, n = lane / 4), dims quarter lane % 4.
+  const int n = lane >> 2, qtr = lane & 3;
+  float logit = 0.0f, dp = 0.0f;
+  if (m < E && n <= m) {
+    const int kq = D / 4;
+    const uint16_t* qr = qs + w * ld + qtr * kq;
+    const uint16_t* dr = dos + w * ld + qtr * kq;
+    const uint16_t* cr = cs + n * ld + qtr * kq;
+    for (int k = 0; k < kq; k += 8) {
+      const u32x4 a = *reinterpret_cast<const u32x4*>(qr + k);
+      const u32x4 d = *reinterpret_cast<const u32x4*>(dr + k);
+      const u32x4 c = *reinterpret_cast<const u32x4*>(cr + k);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        logit = fmaf(bf16_lo(a[j]), bf16_lo(c[j]), logit);
+        logit = fmaf(bf16_hi(a[j]), bf16_hi(c[j]), logit);
+        dp = fmaf(bf16_lo(d[j]), bf16_lo(c[j]), dp);
+        dp = fmaf(bf16_hi(d[j]), bf16_hi(c[j]), dp);
+      }
+    }
+  }
+  logit += __uint_as_float(dpp_u32<0xB1>(__float_as_uint(logit)));   // quad xor 1
+  logit += __uint_as_float(dpp_u32<0x4E>(__float_as_uint(logit)));   // quad xor 2
+  dp += __uint_as_float(dpp_u32<0xB1>(__float_as_uint(dp)));
+  dp += __uint_as_float(dpp_u32<0x4E>(__float_as_uint(dp)));
+  if (qtr == 0) {
+    float sv = 0.0f;
+    if (m < E && n <= m) {
+      const float lse = g.lse[(int64_t)bh * g.S + m];
+      const float p = round_bf16(exp2f((logit * g.scale - lse) * 1.4426950408889634f));
+      sv = round_bf16(p * (dp - delta) * g.scale);
+    }
+    dS[w * kE + n] = sv;
+  }
+  __syncthreads();
+
+  // dq row m: lane owns 8-dim groups lane, lane + 64, ...
+  if (m < E) {
+    const rsrc_t rdq = make_rsrc((const uint8_t*)g.dq + qrow0 * (g.dq_bf16 ? 2 : 4),
+                                 (uint32_t)(E * D) * (g.dq_bf16 ? 2u : 4u));
+    for (int k = lane * 8; k < D; k += 64 * 8) {
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j <= m; ++j) {
+        const float sv = dS[w * kE + j];
+        const u32x4 c = *reinterpret_cast<const u32x4*>(cs + j * ld + k);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[2 * i] = fmaf(sv, bf16_lo(c[i]), acc[2 * i]);
+          acc[2 * i + 1] = fmaf(sv, bf16_hi(c[i]), acc[2 * i + 1]);
+        }
+      }
+      store8(rdq, g.dq_bf16 != 0, (uint32_t)(m * D + k), acc);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ K2
+
+constexpr int kBatch = 16;                // rows loaded before they are used
+
+__device__ __forceinline__ void add4(float4& a, const float4& b) {
+  a.x += b.x;
+  a.y += b.y;
+  a.z += b.z;
+  a.w += b.w;
+}
+
+// v[k] = 4 columns of row row(k), summed over the head groups' partial
+// planes; each plane's kBatch rows are loaded together.
+template <class RowOf>
+__device__ __forceinline__ void load_rows(const MArgs& g, const float* __restrict__ hs,
+                                          RowOf row, float4 (&v)[kBatch]) {
+#pragma unroll
+  for (int k = 0; k < kBatch; ++k) v[k] = *reinterpret_cast<const float4*>(hs + (int64_t)row(k) * g.D);
+  for (int sp = 1; sp < g.hsplit; ++sp) {
+    float4 w[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k)
+      w[k] = *reinterpret_cast<const float4*>(hs + sp * g.hs_split + (int64_t)row(k) * g.D);
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) add4(v[k], w[k]);
+  }
+}
+
+// grid (nblk, B); thread t owns columns 4 t .. 4 t + 3 (t < D / 4) of the
+// rows of block blockIdx.x (g.brows rows): their total over rows and head groups.
+__global__ void __launch_bounds__(kThreads) mla_block_total(const MArgs g) {
+  const int t = threadIdx.x;
+  if (4 * t >= g.D) return;
+  const int b = (int)blockIdx.y, blk = (int)blockIdx.x;
+  const int r0 = blk * g.brows;
+  const int r1 = r0 + g.brows < g.S ? r0 + g.brows : g.S;
+  const float* __restrict__ hs = g.hs + (int64_t)b * g.S * g.D + 4 * t;
+  float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int r = r0; r < r1; r += kBatch) {
+    float4 v[kBatch];
+    load_rows(g, hs, [&](int k) { return r + k < r1 ? r + k : r0; }, v);
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k)
+      if (r + k < r1) add4(a, v[k]);
+  }
+  *reinterpret_cast<float4*>(g.tot + ((int64_t)b * g.nblk + blk) * g.D + 4 * t) = a;
+}
+
+// grid (nblk, B): carry = totals of the later blocks, then the reverse running
+// sum over the block's rows, written as dc.
+__global__ void __launch_bounds__(kThreads) mla_suffix_scan(const MArgs g) {
+  const int t = threadIdx.x;
+  if (4 * t >= g.D) return;
+  const int b = (int)blockIdx.y, blk = (int)blockIdx.x;
+  float4 cy = make_float4(0.f, 0.f, 0.f, 0.f);
+  const float* __restrict__ tot = g.tot + (int64_t)b * g.nblk * g.D + 4 * t;
+  for (int x = blk + 1; x < g.nblk; x += kBatch) {
+    float4 v[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k)
+      v[k] = *reinterpret_cast<const float4*>(tot + (int64_t)(x + k < g.nblk ? x + k : x) * g.D);
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k)
+      if (x + k < g.nblk) add4(cy, v[k]);
+  }
+  const int r0 = blk * g.brows;
+  const int r1 = r0 + g.brows < g.S ? r0 + g.brows : g.S;
+  // The workspace and dc never overlap (checked at launch): restrict lets a
+  // batch's loads issue together ahead of its stores.
+  const float* __restrict__ hs = g.hs + (int64_t)b * g.S * g.D + 4 * t;
+  float* __restrict__ dcf = static_cast<float*>(g.dc) + (int64_t)b * g.S * g.D + 4 * t;
+  uint16_t* __restrict__ dch = static_cast<uint16_t*>(g.dc) + (int64_t)b * g.S * g.D + 4 * t;
+  const bool bf16 = g.dc_bf16 != 0;
+  for (int top = r1; top > r0; top -= kBatch) {      // rows top - 1 down to top - kBatch
+    float4 v[kBatch];
+    load_rows(g, hs, [&](int k) { return top - 1 - k >= r0 ? top - 1 - k : r0; }, v);
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int r = top - 1 - k;
+      if (r >= r0) {
+        add4(cy, v[k]);
+        if (bf16) {
+          const uint2 wv = {pack_bf16x2(cy.x, cy.y), pack_bf16x2(cy.z, cy.w)};
+          *reinterpret_cast<uint2*>(dch + (int64_t)r * g.D) = wv;
+        } else {
+          *reinterpret_cast<float4*>(dcf + (int64_t)r * g.D) = cy;
+        }
+      }
+    }
+  }
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+bool overlap(const void* a, int64_t na, const void* b, int64_t nb) {
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return na > 0 && nb > 0 && x < y + (uintptr_t)nb && y < x + (uintptr_t)na;
+}
+
+constexpr int kMinK1Groups = 1024;        // K1 workgroups wanted (4 per CU)
+constexpr int kMaxHeadSplit = 8;
+
+// Head groups for K1 when the row grid alone is small: doubles while the grid
+// has fewer than kMinK1Groups workgroups (at most 8 groups, never more than H).
+int64_t head_split(int64_t B, int64_t S, int64_t D, int64_t H) {
+  if (D < 64) return 1;
+  const int64_t rows_per_wg = kThreads / (D / 8);
+  const int64_t base = ((S + rows_per_wg - 1) / rows_per_wg) * B;
+  int64_t sp = 1;
+  while (base * sp < kMinK1Groups && sp < kMaxHeadSplit && sp * 2 <= H) sp *= 2;
+  return sp;
+}
+
+// Rows per scan block: S / 64 rounded up to a multiple of 16, within [16, 64],
+// so short sequences still spread over many blocks and each thread's carry and
+// in-block loops stay short.
+int64_t block_rows(int64_t S) {
+  int64_t r = ((S + 63) / 64 + 15) / 16 * 16;
+  return r < 16 ? 16 : r > 64 ? 64 : r;
+}
+
+int64_t workspace_bytes(int64_t B, int64_t S, int64_t D) {
+  if (B < 0 || S < 0 || D < 0 || B > (1 << 20) || S > (1ll << 31) || D > kMaxD) return -1;
+  const int64_t sp = head_split(B, S, D, kMaxHeadSplit);   // the most any H can use
+  const int64_t nblk = (S + block_rows(S) - 1) / block_rows(S);
+  return (sp * B * S + B * nblk) * D * 4;
+}
+
+}  // namespace
+}  // namespace mla
+}  // namespace fagq
+
+using namespace fagq;
+using namespace fagq::mla;
+
+extern "C" {
+
+FAGQ_API int64_t fagq_mla_bwd_workspace_bytes(int64_t B, int64_t S, int64_t D) {
+  return workspace_bytes(B, S, D);
+}
+
+FAGQ_API int fagq_mla_bwd_launch(const void* q, const void* c_kv, const void* out, const void* dout,
+                                 const float* lse, void* dq, void* dc_kv, void* workspace,
+                                 int64_t ws_bytes, int64_t B, int64_t H, int64_t S, int64_t D,
+                                 float sm_scale, int dq_dtype, int dc_dtype, void* stream) {
+  if (!q || !c_kv || !out || !dout || !lse || !dq || !dc_kv || !workspace) return FAGQ_E_NULL;
+  if ((dq_dtype != FAGQ_MLA_F32 && dq_dtype != FAGQ_MLA_BF16) ||
+      (dc_dtype != FAGQ_MLA_F32 && dc_dtype != FAGQ_MLA_BF16))
+    return FAGQ_E_FORMAT;
+  if (B < 0 || H < 1 || S < 1 || D < 64 || D % 64 != 0 || !(sm_scale == sm_scale))
+    return FAGQ_E_SHAPE;
+  if (D > kMaxD || B > 65535 || H > 65535 || H * S * D * 4 >= (1ll << 32)) return FAGQ_E_TOO_LARGE;
+  const int64_t need = workspace_bytes(B, S, D);
+  if (need < 0) return FAGQ_E_TOO_LARGE;
+  if (ws_bytes < need) return FAGQ_E_SHAPE;
+  if (!aligned(q, 16) || !aligned(c_kv, 16) || !aligned(out, 16) || !aligned(dout, 16) ||
+      !aligned(lse, 4) || !aligned(dq, 16) || !aligned(dc_kv, 16) || !aligned(workspace, 16))
+    return FAGQ_E_ALIGN;
+  if (B == 0) return FAGQ_OK;
+  const int64_t nq = B * H * S * D * 2, nc = B * S * D * 2, nl = B * H * S * 4;
+  const int64_t ndq = B * H * S * D * (dq_dtype == FAGQ_MLA_BF16 ? 2 : 4);
+  const int64_t ndc = B * S * D * (dc_dtype == FAGQ_MLA_BF16 ? 2 : 4);
+  const void* ins[5] = {q, c_kv, out, dout, lse};
+  const int64_t nin[5] = {nq, nc, nq, nq, nl};
+  void* outs[3] = {dq, dc_kv, workspace};
+  const int64_t nout[3] = {ndq, ndc, need};
+  for (int i = 0; i < 3; ++i) {
+    for (int j = 0; j < 5; ++j)
+      if (overlap(outs[i], nout[i], ins[j], nin[j])) return FAGQ_E_ALIAS;
+    for (int j = i + 1; j < 3; ++j)
+      if (overlap(outs[i], nout[i], outs[j], nout[j])) return FAGQ_E_ALIAS;
+  }
+  const int dcheck = device_check();
+  if (dcheck != FAGQ_OK) return dcheck;
+
+  MArgs g;
+  g.q = static_cast<const uint16_t*>(q);
+  g.c = static_cast<const uint16_t*>(c_kv);
+  g.out = static_cast<const uint16_t*>(out);
+  g.dout = static_cast<const uint16_t*>(dout);
+  g.lse = lse;
+  g.dq = dq;
+  g.dc = dc_kv;
+  const int64_t hsplit = head_split(B, S, D, H);
+  g.hps = (int32_t)((H + hsplit - 1) / hsplit);
+  g.hsplit = (int32_t)((H + g.hps - 1) / g.hps);          // non-empty head groups
+  g.hs = static_cast<float*>(workspace);
+  g.hs_split = B * S * D;
+  g.brows = (int32_t)block_rows(S);
+  g.nblk = (int32_t)((S + g.brows - 1) / g.brows);
+  g.tot = g.hs + g.hsplit * B * S * D;
+  g.H = (int32_t)H;
+  g.S = (int32_t)S;
+  g.D = (int32_t)D;
+  g.erows = (int32_t)(S < kE ? S : kE);
+  g.scale = sm_scale;
+  g.dq_bf16 = dq_dtype == FAGQ_MLA_BF16;
+  g.dc_bf16 = dc_dtype == FAGQ_MLA_BF16;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  void* args[] = {&g};
+  const int rows_per_wg = kThreads / (int)(D / 8);
+  hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_stream_do),
+                                 dim3((unsigned)((S + rows_per_wg - 1) / rows_per_wg), (unsigned)B,
+                                      (unsigned)g.hsplit),
+                                 dim3(kThreads), args, 0, st);
+  if (e != hipSuccess) return -(int)e;
+  const size_t lds = (size_t)(2 * kRowsK0 + kE) * (D + kPadElems) * 2 + (size_t)kRowsK0 * kE * 4;
+  e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_exact_rows),
+                      dim3((unsigned)(B * H), (unsigned)((g.erows + kRowsK0 - 1) / kRowsK0)),
+                      dim3(kThreads), args, lds, st);
+  if (e != hipSuccess) return -(int)e;
+  e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_block_total),
+                      dim3((unsigned)g.nblk, (unsigned)B), dim3(kThreads), args, 0, st);
+  if (e != hipSuccess) return -(int)e;
+  e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_suffix_scan),
+                      dim3((unsigned)g.nblk, (unsigned)B), dim3(kThreads), args, 0, st);
+  return e == hipSuccess ? FAGQ_OK : -(int)e;
+}
+
+}  // extern "C"

@@ -271,3 +271,70 @@ def dsa_valid_blocks(w: DsaWorkload, q_pos: torch.Tensor, kv_lens: torch.Tensor)
                          (vb - 1)[:, None])
     per_row = torch.clamp(last + 1, min=0)                                         # [B, Q]
     return int(per_row.sum()) * w.H
+
+
+# ---------------------------------------------------------------- Task 03 MLA backward
+
+@dataclass(frozen=True)
+class MlaWorkload:
+    """q, out, do [B, H, S, D], c_kv [B, S, D] bf16 -> dq, dc_kv."""
+    name: str
+    B: int
+    H: int
+    S: int
+    D: int
+    grad_dtype: torch.dtype = torch.bfloat16     # dq and dc_kv
+    seed: int = 0
+
+    @property
+    def sm_scale(self) -> float:
+        return self.D ** -0.5
+
+    @property
+    def exact_rows(self) -> int:
+        return min(16, self.S)
+
+    def algorithmic_bytes(self) -> int:
+        """do read once, dq and dc written once, plus the exact rows' q, out, c
+        and lse reads."""
+        g = 2 if self.grad_dtype == torch.bfloat16 else 4
+        n = self.B * self.H * self.S * self.D
+        e = self.exact_rows
+        return (2 * n + g * n + g * self.B * self.S * self.D
+                + 4 * self.B * self.H * e * self.D + 2 * self.B * e * self.D
+                + 4 * self.B * self.H * e)
+
+
+def _mla(B, H, S, D, grad=torch.bfloat16):
+    tag = "" if grad == torch.bfloat16 else "_f32grad"
+    name = f"mla_b{B}h{H}s{S}d{D}{tag}"
+    return name, MlaWorkload(name, B, H, S, D, grad)
+
+
+# The reference's workloads: H = 64, D = 512, S in {256, ..., 4096}, up to B = 2
+# (reports/task03_mla_bwd_nope_dkdv.md:27-33, :57).
+MLA_CONFIGS = dict(_mla(2, 64, S, 512) for S in (256, 512, 1024, 2048, 4096))
+MLA_CONFIGS.update(dict([_mla(2, 64, 4096, 512, torch.float32)]))
+MLA_HEADLINE = "mla_b2h64s4096d512"
+
+
+def make_mla_inputs(w: MlaWorkload, device="cpu"):
+    """(q, c_kv, out, do, lse) on `device`: q, c_kv, do N(0, 1) in bf16.  The
+    first exact_rows query rows of out and lse come from the causal forward
+    with K = V = C (the only rows of out and lse the operator reads); the
+    other rows of out are N(0, 0.05) and of lse log(i + 1)."""
+    g = torch.Generator(device=device).manual_seed(w.seed)
+    B, H, S, D, E = w.B, w.H, w.S, w.D, w.exact_rows
+    q = torch.randn(B, H, S, D, generator=g, device=device).to(torch.bfloat16)
+    c = torch.randn(B, S, D, generator=g, device=device).to(torch.bfloat16)
+    do = torch.randn(B, H, S, D, generator=g, device=device).to(torch.bfloat16)
+    out = (torch.randn(B, H, S, D, generator=g, device=device) * 0.05).to(torch.bfloat16)
+    lse = torch.log(torch.arange(1, S + 1, device=device, dtype=torch.float32)).expand(B, H, S)
+    lse = lse.contiguous()
+    qe, ce = q[:, :, :E].double(), c[:, :E].double()
+    logits = torch.einsum("bhsd,btd->bhst", qe, ce) * w.sm_scale
+    logits = logits.masked_fill(~torch.ones(E, E, dtype=torch.bool, device=device).tril(),
+                                float("-inf"))
+    lse[:, :, :E] = torch.logsumexp(logits, -1).float()
+    out[:, :, :E] = torch.einsum("bhst,btd->bhsd", torch.softmax(logits, -1), ce).to(torch.bfloat16)
+    return q, c, out, do, lse

@@ -64,6 +64,8 @@ def lib() -> ctypes.CDLL:
         L.orc_gemm.argtypes = [P, P, P, P, P, P, I64, I64, I64, I, I, I, I]
         L.orc_gemm.restype = I
         L.orc_dsa_topk.argtypes = [P, I, P, P, P, I, P, P, I64, I64, I64, I64, I64, I64, I]
+        L.orc_mla_bwd.restype = I
+        L.orc_mla_bwd.argtypes = [P] * 8 + [I64] * 4 + [F, I]
         L.orc_dsa_topk.restype = I
         _lib = L
     return _lib
@@ -223,3 +225,29 @@ def dsa_topk(scores: np.ndarray, page_table: np.ndarray, q_pos: np.ndarray, kv_l
     if st != 0:
         raise ValueError(f"oracle rejected the arguments (status {st})")
     return ob, op
+
+
+def mla_bwd(q: np.ndarray, c: np.ndarray, out: np.ndarray, do: np.ndarray, lse: np.ndarray,
+            sm_scale: float, with_bound: bool = True, nthreads: int = 0):
+    """The reference's Task 03 operator (oracle/mla_bwd_oracle.c).  q, out, do:
+    uint16 bf16 bits [B, H, S, D]; c: uint16 [B, S, D]; lse: float32 [B, H, S].
+    Returns (dq float64 [B, H, S, D], dc float64 [B, S, D], dq_bound float64
+    [2, B, H, E, D] or None), E = min(16, S): dq_bound[0] = sum_j |dS_ij| |c_jd|,
+    dq_bound[1] = the sensitivity of dq to absolute errors in dp - delta
+    (oracle/mla_bwd_oracle.c)."""
+    import os
+    q, c, out, do = (np.ascontiguousarray(a, dtype=np.uint16) for a in (q, c, out, do))
+    lse = np.ascontiguousarray(lse, dtype=np.float32)
+    B, H, S, D = q.shape
+    assert c.shape == (B, S, D) and out.shape == q.shape and do.shape == q.shape
+    assert lse.shape == (B, H, S)
+    E = min(16, S)
+    dq = np.empty((B, H, S, D), np.float64)
+    dc = np.empty((B, S, D), np.float64)
+    bound = np.empty((2, B, H, E, D), np.float64) if with_bound else None
+    st = lib().orc_mla_bwd(_ptr(q), _ptr(c), _ptr(out), _ptr(do), _ptr(lse), _ptr(dq), _ptr(dc),
+                           _ptr(bound) if bound is not None else None, B, H, S, D,
+                           float(sm_scale), nthreads or min(8, os.cpu_count() or 1))
+    if st != 0:
+        raise ValueError(f"oracle rejected the arguments (status {st})")
+    return dq, dc, bound

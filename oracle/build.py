@@ -15,7 +15,8 @@ import subprocess
 from pathlib import Path
 
 ORACLE_DIR = Path(__file__).resolve().parent
-SRCS = [ORACLE_DIR / "fagq_oracle.c", ORACLE_DIR / "gemm_oracle.c", ORACLE_DIR / "dsa_topk_oracle.c"]
+SRCS = [ORACLE_DIR / "fagq_oracle.c", ORACLE_DIR / "gemm_oracle.c", ORACLE_DIR / "dsa_topk_oracle.c",
+        ORACLE_DIR / "mla_bwd_oracle.c"]
 LIB = ORACLE_DIR / "libfagq_oracle.so"
 
 CFLAGS = ["-O2", "-std=gnu11", "-fPIC", "-shared", "-fopenmp", "-ffp-contract=off",

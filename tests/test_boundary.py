@@ -273,3 +273,47 @@ def dsa_call(lib, **kw):
 ])
 def test_dsa_validation(lib, kw, status):
     assert dsa_call(lib, **kw) == status
+
+
+# ------------------------------------------------------------ MLA backward (Task 03)
+
+def mla_call(lib, **kw):
+    a = dict(q=fake(0), c=fake(1), o=fake(2), do=fake(3), lse=fake(4), dq=fake(5), dc=fake(6),
+             ws=fake(7), wsb=1 << 30, B=1, H=4, S=256, D=512, scale=0.05, dqt=0, dct=0)
+    a.update(kw)
+    return lib.fagq_mla_bwd_launch(a["q"], a["c"], a["o"], a["do"], a["lse"], a["dq"], a["dc"], a["ws"],
+                                   a["wsb"], a["B"], a["H"], a["S"], a["D"], a["scale"], a["dqt"],
+                                   a["dct"], None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(q=None), 1), (dict(lse=None), 1), (dict(dc=None), 1), (dict(ws=None), 1),
+    (dict(dqt=2), 5), (dict(dct=-1), 5),
+    (dict(B=-1), 2), (dict(H=0), 2), (dict(S=0), 2), (dict(D=96), 2), (dict(D=32), 2),
+    (dict(scale=float("nan")), 2), (dict(wsb=1000), 2),
+    (dict(D=576), 7), (dict(B=65536), 7), (dict(H=65536, S=64), 7), (dict(H=64, S=1 << 15), 7),
+    (dict(q=ctypes.c_void_p(BASE + 8)), 4), (dict(lse=ctypes.c_void_p(BASE + 0x4_0000_0002)), 4),
+    (dict(ws=ctypes.c_void_p(BASE + 0x7_0000_0004)), 4),
+    (dict(dq=fake(0)), 9), (dict(dc=fake(3)), 9), (dict(ws=fake(5)), 9),
+    (dict(dc=ctypes.c_void_p(BASE + 0x5_0000_0100)), 9),
+    (dict(B=0), 0),
+])
+def test_mla_validation(lib, kw, status):
+    assert mla_call(lib, **kw) == status
+
+
+def test_mla_workspace_size(lib):
+    # head sums [B, S, D] plus the totals of 64-row blocks
+    assert lib.fagq_mla_bwd_workspace_bytes(2, 4096, 512) == 2 * (4096 + 64) * 512 * 4
+    # small grids split the heads into up to 8 groups, one partial plane each;
+    # 16-row blocks
+    assert lib.fagq_mla_bwd_workspace_bytes(1, 65, 64) == (8 * 65 + 5) * 64 * 4
+    assert lib.fagq_mla_bwd_workspace_bytes(-1, 1, 64) == -1
+
+
+def test_mla_workloads():
+    from fagq_mi355x.workloads import MLA_CONFIGS, MLA_HEADLINE
+    w = MLA_CONFIGS[MLA_HEADLINE]
+    assert (w.B, w.H, w.S, w.D) == (2, 64, 4096, 512)
+    n = 2 * 64 * 4096 * 512
+    assert w.algorithmic_bytes() >= 4 * n
