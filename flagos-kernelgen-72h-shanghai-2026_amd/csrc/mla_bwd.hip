@@ -15,14 +15,26 @@
 //                        A lane owns 8 consecutive dims (16-byte loads), a
 //                        workgroup 2048 / D rows, so each head contributes a
 //                        contiguous 4 KB (D = 512) segment per workgroup.
-//   K0 mla_exact_rows  - per (b, h) and 4 query rows: q, do rows and c rows
-//                        0..E-1 in LDS, the logits and dP by fp32 dot
-//                        products (4 lanes per (query, key) pair), P and dS
-//                        rounded to bf16 where the reference rounds, dq rows.
-//   K2 mla_block_total - per block of 16-64 rows: fp32 totals of hs / (i + 1)
-//                        (summed over the head groups' partial planes).
+//                        Short sequences split the heads into up to 8 groups,
+//                        each writing a partial head-sum plane.
+//   K2 mla_exact_rows_block_total - one launch of 1024-thread workgroups, two
+//                        kinds:
+//                        * exact rows, one per (b, h): q, do and c rows 0..E-1
+//                          in LDS, the logits and dP by fp32 dot products (4
+//                          lanes per (query, key) pair), P and dS rounded to
+//                          bf16 where the reference rounds, dq rows 0..E-1
+//                          (which K1 does not write);
+//                        * block totals, per block of 16-64 rows: fp32 totals
+//                          of hs / (i + 1) over rows and head-group planes;
+//                          each row's plane sum is written back over plane 0.
+//                        The exact rows depend on nothing K1 writes; sharing
+//                        the launch with the few block-total workgroups runs
+//                        them in the part of the chip those leave idle.
 //   K3 mla_suffix_scan - per block: carry = totals of all later blocks, then
-//                        the reverse running sum over the block, written as dc.
+//                        the reverse running sum over the block's rows (plane
+//                        0), written as dc.
+// K2 and K3 issue each thread's loads as one batch: at these sizes they are
+// latency-bound: every dependent round trip to memory adds its full latency.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -37,11 +49,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kE = FAGQ_MLA_EXACT_ROWS;
 constexpr int kMaxD = FAGQ_MLA_MAX_D;
-constexpr int kPadElems = 8;             // LDS row padding (bf16 elements) for K0
-#ifndef FAGQ_MLA_HEADS_IN_FLIGHT
-#define FAGQ_MLA_HEADS_IN_FLIGHT 2
-#endif
-constexpr int kHeadsInFlight = FAGQ_MLA_HEADS_IN_FLIGHT;   // K1 loads per batch
+constexpr int kPadElems = 8;             // LDS row padding (bf16 elements), exact rows
 
 struct MArgs {
   const uint16_t* q;
@@ -90,7 +98,11 @@ __device__ __forceinline__ void store8(const rsrc_t& rs, bool bf16, uint32_t e, 
 // ------------------------------------------------------------------ K1
 
 // grid (ceil(S / rows_per_wg), B, hsplit); rows_per_wg = 256 / (D / 8);
-// z picks the head group [z hps, min(H, (z + 1) hps)).
+// z picks the head group [z hps, min(H, (z + 1) hps)).  U heads' loads are in
+// flight per lane: U = 2 keeps the kernel at 50 VGPRs, 8 workgroups per CU,
+// for grids of 2048 and more; U = 8 (110 VGPRs, 4 per CU) for grids that fit
+// 4 per CU, where each workgroup's few heads are then loaded at once.
+template <int U>
 __global__ void __launch_bounds__(kThreads) mla_stream_do(const MArgs g) {
   const int lpr = g.D / 8;                        // lanes per row
   const int t = threadIdx.x;
@@ -111,7 +123,6 @@ __global__ void __launch_bounds__(kThreads) mla_stream_do(const MArgs g) {
   // Heads in batches of U, software-pipelined: the loads of batch i + 1 are
   // issued before batch i is consumed.  Heads past hend re-read head hend - 1
   // (in bounds) and are not used.
-  constexpr int U = kHeadsInFlight;
   auto load_batch = [&](int h0, u32x4 (&v)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -155,62 +166,53 @@ __global__ void __launch_bounds__(kThreads) mla_stream_do(const MArgs g) {
   store8(rhs, false, (uint32_t)row * (uint32_t)g.D + (uint32_t)(t % lpr) * 8u, o);
 }
 
-// ------------------------------------------------------------------ K0
+// ------------------------------------------------------------------ K2: exact rows
 
-constexpr int kRowsK0 = 4;                // query rows per workgroup, one wave each
+constexpr int kWide = 1024;               // threads of K2 and K3 (16 waves)
 
-// grid (B * H, ceil(E / 4)).  Wave w owns query row m = 4 blockIdx.y + w; its
-// lane 4 n + k computes quarter k of the dims of the dot products with key n
-// (n < 16), the quarters joined by two DPP steps.  Dynamic LDS: q and do rows
-// of the workgroup, c rows 0..E-1 (rows padded by 16 bytes), then dS.
-__global__ void __launch_bounds__(kThreads) mla_exact_rows(const MArgs g) {
+// Exact rows 0..E-1 of (b, h), wave m owning query row m.  Lane 4 n + k
+// computes quarter k of the dims of the dot products with key n (n <= m), the
+// quarters joined by two DPP steps.  Every global load is issued before the
+// first LDS store: wave m loads chunk `lane` (16 bytes) of its q, do and out
+// rows, and thread t chunk t of c rows 0..E-1 (16 D / 8 <= 1024 chunks).
+// Buffer descriptors over rows 0..E-1 return zeros for the rest.  Dynamic
+// LDS: q, do and c rows 0..15 (padded by 16 bytes), then dS [16][16].
+__device__ __forceinline__ void exact_rows(const MArgs& g, int b, int h) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int D = g.D, E = g.erows;
   const int ld = D + kPadElems;                   // bf16 elements per LDS row
   uint16_t* qs = reinterpret_cast<uint16_t*>(smem);
-  uint16_t* dos = qs + kRowsK0 * ld;
-  uint16_t* cs = dos + kRowsK0 * ld;
-  float* dS = reinterpret_cast<float*>(cs + kE * ld);   // [kRowsK0][kE]
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int bh = (int)blockIdx.x;
-  const int b = bh / g.H;
-  const int m0 = (int)blockIdx.y * kRowsK0;
-  const int m = m0 + w;
+  uint16_t* dos = qs + kE * ld;
+  uint16_t* cs = dos + kE * ld;
+  float* dS = reinterpret_cast<float*>(cs + kE * ld);
+  const int t = threadIdx.x, lane = t & 63, m = t >> 6;
+  const int bh = b * g.H + h;
+  const int cpr = D / 8;                          // 16-byte chunks per row (8..64)
   const int64_t qrow0 = (int64_t)bh * g.S * D;    // q, do, out rows of (b, h)
-  const int64_t crow0 = (int64_t)b * g.S * D;
-  const int kmax = m0 + kRowsK0 < E ? m0 + kRowsK0 : E;   // keys 0..kmax-1 are needed
-
-  const int cpr = D / 8;                          // 16-byte chunks per row
-  for (int i = t; i < kRowsK0 * cpr; i += kThreads) {
-    const int r = i / cpr, k = i % cpr;
-    u32x4 a = {0u, 0u, 0u, 0u}, d = a;
-    if (m0 + r < E) {
-      a = *reinterpret_cast<const u32x4*>(g.q + qrow0 + (int64_t)(m0 + r) * D + k * 8);
-      d = *reinterpret_cast<const u32x4*>(g.dout + qrow0 + (int64_t)(m0 + r) * D + k * 8);
-    }
-    *reinterpret_cast<u32x4*>(qs + r * ld + k * 8) = a;
-    *reinterpret_cast<u32x4*>(dos + r * ld + k * 8) = d;
+  const uint32_t rbytes = (uint32_t)(E * D * 2);
+  const rsrc_t rq = make_rsrc(g.q + qrow0, rbytes);
+  const rsrc_t rdo = make_rsrc(g.dout + qrow0, rbytes);
+  const rsrc_t rout = make_rsrc(g.out + qrow0, rbytes);
+  const rsrc_t rc = make_rsrc(g.c + (int64_t)b * g.S * D, rbytes);
+  const uint32_t off = m < E && lane < cpr ? (uint32_t)(m * D + lane * 8) * 2u : rbytes;
+  const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0);
+  const u32x4 d = __builtin_amdgcn_raw_buffer_load_b128(rdo, off, 0, 0);
+  const u32x4 o = __builtin_amdgcn_raw_buffer_load_b128(rout, off, 0, 0);
+  const u32x4 cv = __builtin_amdgcn_raw_buffer_load_b128(rc, (uint32_t)t * 16u, 0, 0);
+  if (lane < cpr) {
+    *reinterpret_cast<u32x4*>(qs + m * ld + lane * 8) = a;
+    *reinterpret_cast<u32x4*>(dos + m * ld + lane * 8) = d;
   }
-  for (int i = t; i < kmax * cpr; i += kThreads) {
-    const int r = i / cpr, k = i % cpr;
-    *reinterpret_cast<u32x4*>(cs + r * ld + k * 8) =
-        *reinterpret_cast<const u32x4*>(g.c + crow0 + (int64_t)r * D + k * 8);
-  }
-  // delta_m = out_m . do_m (wave-wide), read from global memory.
+  if (t < kE * cpr) *reinterpret_cast<u32x4*>(cs + (t / cpr) * ld + (t % cpr) * 8) = cv;
+  // delta_m = out_m . do_m (wave-wide).
   float delta = 0.0f;
-  if (m < E) {
-    for (int k = lane; k < cpr; k += 64) {
-      const u32x4 o = *reinterpret_cast<const u32x4*>(g.out + qrow0 + (int64_t)m * D + k * 8);
-      const u32x4 d = *reinterpret_cast<const u32x4*>(g.dout + qrow0 + (int64_t)m * D + k * 8);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        delta += bf16_lo(o[j]) * bf16_lo(d[j]);
-        delta += bf16_hi(o[j]) * bf16_hi(d[j]);
-      }
-    }
+  for (int j = 0; j < 4; ++j) {
+    delta += bf16_lo(o[j]) * bf16_lo(d[j]);
+    delta += bf16_hi(o[j]) * bf16_hi(d[j]);
   }
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) delta += __shfl_xor(delta, off, 64);
+  for (int s = 32; s > 0; s >>= 1) delta += __shfl_xor(delta, s, 64);
   __syncthreads();
 
   // Logits and dP of (m, n = lane / 4), dims quarter lane % 4.
@@ -218,19 +220,20 @@ __global__ void __launch_bounds__(kThreads) mla_exact_rows(const MArgs g) {
   float logit = 0.0f, dp = 0.0f;
   if (m < E && n <= m) {
     const int kq = D / 4;
-    const uint16_t* qr = qs + w * ld + qtr * kq;
-    const uint16_t* dr = dos + w * ld + qtr * kq;
+    const uint16_t* qr = qs + m * ld + qtr * kq;
+    const uint16_t* dr = dos + m * ld + qtr * kq;
     const uint16_t* cr = cs + n * ld + qtr * kq;
+#pragma unroll 4
     for (int k = 0; k < kq; k += 8) {
-      const u32x4 a = *reinterpret_cast<const u32x4*>(qr + k);
-      const u32x4 d = *reinterpret_cast<const u32x4*>(dr + k);
+      const u32x4 x = *reinterpret_cast<const u32x4*>(qr + k);
+      const u32x4 y = *reinterpret_cast<const u32x4*>(dr + k);
       const u32x4 c = *reinterpret_cast<const u32x4*>(cr + k);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        logit = fmaf(bf16_lo(a[j]), bf16_lo(c[j]), logit);
-        logit = fmaf(bf16_hi(a[j]), bf16_hi(c[j]), logit);
-        dp = fmaf(bf16_lo(d[j]), bf16_lo(c[j]), dp);
-        dp = fmaf(bf16_hi(d[j]), bf16_hi(c[j]), dp);
+        logit = fmaf(bf16_lo(x[j]), bf16_lo(c[j]), logit);
+        logit = fmaf(bf16_hi(x[j]), bf16_hi(c[j]), logit);
+        dp = fmaf(bf16_lo(y[j]), bf16_lo(c[j]), dp);
+        dp = fmaf(bf16_hi(y[j]), bf16_hi(c[j]), dp);
       }
     }
   }
@@ -245,7 +248,7 @@ __global__ void __launch_bounds__(kThreads) mla_exact_rows(const MArgs g) {
       const float p = round_bf16(exp2f((logit * g.scale - lse) * 1.4426950408889634f));
       sv = round_bf16(p * (dp - delta) * g.scale);
     }
-    dS[w * kE + n] = sv;
+    dS[m * kE + n] = sv;
   }
   __syncthreads();
 
@@ -256,7 +259,7 @@ __global__ void __launch_bounds__(kThreads) mla_exact_rows(const MArgs g) {
     for (int k = lane * 8; k < D; k += 64 * 8) {
       float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
       for (int j = 0; j <= m; ++j) {
-        const float sv = dS[w * kE + j];
+        const float sv = dS[m * kE + j];
         const u32x4 c = *reinterpret_cast<const u32x4*>(cs + j * ld + k);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -269,9 +272,17 @@ __global__ void __launch_bounds__(kThreads) mla_exact_rows(const MArgs g) {
   }
 }
 
-// ------------------------------------------------------------------ K2
+// Dynamic LDS of K2: the exact rows' rows and dS, at least kWide float4 for
+// the block totals' join.
+size_t k2_lds_bytes(int64_t D) {
+  const size_t ex = (size_t)3 * kE * (D + kPadElems) * 2 + (size_t)kE * kE * 4;
+  const size_t bt = (size_t)kWide * 16;
+  return ex > bt ? ex : bt;
+}
 
-constexpr int kBatch = 16;                // rows loaded before they are used
+// ------------------------------------------------------------------ K2: block totals
+
+constexpr int kBatch = 16;                // loads issued before they are used
 
 __device__ __forceinline__ void add4(float4& a, const float4& b) {
   a.x += b.x;
@@ -280,82 +291,149 @@ __device__ __forceinline__ void add4(float4& a, const float4& b) {
   a.w += b.w;
 }
 
-// v[k] = 4 columns of row row(k), summed over the head groups' partial
-// planes; each plane's kBatch rows are loaded together.
-template <class RowOf>
-__device__ __forceinline__ void load_rows(const MArgs& g, const float* __restrict__ hs,
-                                          RowOf row, float4 (&v)[kBatch]) {
-#pragma unroll
-  for (int k = 0; k < kBatch; ++k) v[k] = *reinterpret_cast<const float4*>(hs + (int64_t)row(k) * g.D);
-  for (int sp = 1; sp < g.hsplit; ++sp) {
-    float4 w[kBatch];
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k)
-      w[k] = *reinterpret_cast<const float4*>(hs + sp * g.hs_split + (int64_t)row(k) * g.D);
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k) add4(v[k], w[k]);
-  }
-}
+// Thread layout of K2's block totals and K3: cpt = D / 4 column threads (16..128)
+// per part, np = kWide / cpt parts (8..64); thread t owns columns
+// 4 (t % cpt) .. + 3 of part t / cpt (threads of parts >= np idle).
+struct Parts {
+  int cpt, np, p, col;
+  __device__ explicit Parts(int D) : cpt(D >> 2), np(kWide / (D >> 2)), p((int)threadIdx.x / (D >> 2)),
+                                     col((int)threadIdx.x - p * (D >> 2)) {}
+};
 
-// grid (nblk, B); thread t owns columns 4 t .. 4 t + 3 (t < D / 4) of the
-// rows of block blockIdx.x (g.brows rows): their total over rows and head groups.
-__global__ void __launch_bounds__(kThreads) mla_block_total(const MArgs g) {
-  const int t = threadIdx.x;
-  if (4 * t >= g.D) return;
-  const int b = (int)blockIdx.y, blk = (int)blockIdx.x;
+// Part p of the block's threads sums rows r0 + p, r0 + p + np, ... of the
+// block over the HS head-group planes; a batch loads all planes of
+// kBatch / HS such rows together.  With HS > 1 each row's plane sum
+// (planes in order) is written back over plane 0, so K3 reads one plane.
+// The parts' totals are joined in LDS, in part order.
+template <int HS>
+__device__ __forceinline__ void block_total_hs(const MArgs& g, int b, int blk, float4* part) {
+  constexpr int R = kBatch / HS;
+  const Parts P(g.D);
   const int r0 = blk * g.brows;
   const int r1 = r0 + g.brows < g.S ? r0 + g.brows : g.S;
-  const float* __restrict__ hs = g.hs + (int64_t)b * g.S * g.D + 4 * t;
+  float* __restrict__ hs = g.hs + (int64_t)b * g.S * g.D + 4 * P.col;
   float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int r = r0; r < r1; r += kBatch) {
-    float4 v[kBatch];
-    load_rows(g, hs, [&](int k) { return r + k < r1 ? r + k : r0; }, v);
+  if (P.p < P.np) {
+    for (int r = r0 + P.p; r < r1; r += R * P.np) {
+      float4 v[R][HS];
 #pragma unroll
-    for (int k = 0; k < kBatch; ++k)
-      if (r + k < r1) add4(a, v[k]);
+      for (int i = 0; i < R; ++i) {
+        const int rr = r + i * P.np < r1 ? r + i * P.np : r0;
+#pragma unroll
+        for (int s = 0; s < HS; ++s)
+          v[i][s] = *reinterpret_cast<const float4*>(hs + s * g.hs_split + (int64_t)rr * g.D);
+      }
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        const int rr = r + i * P.np;
+        if (rr < r1) {
+          float4 sum = v[i][0];
+#pragma unroll
+          for (int s = 1; s < HS; ++s) add4(sum, v[i][s]);
+          if (HS > 1) *reinterpret_cast<float4*>(hs + (int64_t)rr * g.D) = sum;
+          add4(a, sum);
+        }
+      }
+    }
   }
-  *reinterpret_cast<float4*>(g.tot + ((int64_t)b * g.nblk + blk) * g.D + 4 * t) = a;
+  part[threadIdx.x] = a;
+  __syncthreads();
+  if (P.p == 0) {
+    for (int q = 1; q < P.np; ++q) add4(a, part[q * P.cpt + P.col]);
+    *reinterpret_cast<float4*>(g.tot + ((int64_t)b * g.nblk + blk) * g.D + 4 * P.col) = a;
+  }
 }
 
-// grid (nblk, B): carry = totals of the later blocks, then the reverse running
-// sum over the block's rows, written as dc.
-__global__ void __launch_bounds__(kThreads) mla_suffix_scan(const MArgs g) {
-  const int t = threadIdx.x;
-  if (4 * t >= g.D) return;
-  const int b = (int)blockIdx.y, blk = (int)blockIdx.x;
-  float4 cy = make_float4(0.f, 0.f, 0.f, 0.f);
-  const float* __restrict__ tot = g.tot + (int64_t)b * g.nblk * g.D + 4 * t;
-  for (int x = blk + 1; x < g.nblk; x += kBatch) {
-    float4 v[kBatch];
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k)
-      v[k] = *reinterpret_cast<const float4*>(tot + (int64_t)(x + k < g.nblk ? x + k : x) * g.D);
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k)
-      if (x + k < g.nblk) add4(cy, v[k]);
+// Totals of block blk (g.brows rows) of batch b over rows and head groups.
+__device__ __forceinline__ void block_total(const MArgs& g, int b, int blk) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  float4* part = reinterpret_cast<float4*>(smem);
+  switch (g.hsplit) {                     // 1..8 (kMaxHeadSplit)
+    case 1: block_total_hs<1>(g, b, blk, part); break;
+    case 2: block_total_hs<2>(g, b, blk, part); break;
+    case 3: block_total_hs<3>(g, b, blk, part); break;
+    case 4: block_total_hs<4>(g, b, blk, part); break;
+    case 5: block_total_hs<5>(g, b, blk, part); break;
+    case 6: block_total_hs<6>(g, b, blk, part); break;
+    case 7: block_total_hs<7>(g, b, blk, part); break;
+    default: block_total_hs<8>(g, b, blk, part); break;
   }
+}
+
+// grid (H + nblk, B): x < H are the exact rows of head x, the rest block
+// totals.  Uniform per workgroup, so every barrier sees all its waves.
+__global__ void __launch_bounds__(kWide) mla_exact_rows_block_total(const MArgs g) {
+  const int x = (int)blockIdx.x, b = (int)blockIdx.y;
+  if (x < g.H)
+    exact_rows(g, b, x);
+  else
+    block_total(g, b, x - g.H);
+}
+
+// ------------------------------------------------------------------ K3
+
+constexpr int kChunkRows = 8;             // >= ceil(64 / 8): rows per part of a block
+
+// grid (nblk, B).  The block's rows are np chunks of cr = ceil(brows / np)
+// rows (cr <= 8 since brows <= 64 and np >= 8); part p scans chunk p.  Part p
+// first sums (1) the totals of later blocks blk + 1 + p, blk + 1 + p + np, ...
+// and (2) the rows of its chunk (kept in registers); after one barrier its
+// carry is all parts' (1), in part order, plus the (2) of the chunks above
+// it, then the reverse running sum over the chunk is written as dc.
+__global__ void __launch_bounds__(kWide) mla_suffix_scan(const MArgs g) {
+  __shared__ float4 later[kWide], chunk[kWide];
+  const Parts P(g.D);
+  const int b = (int)blockIdx.y, blk = (int)blockIdx.x;
   const int r0 = blk * g.brows;
   const int r1 = r0 + g.brows < g.S ? r0 + g.brows : g.S;
-  // The workspace and dc never overlap (checked at launch): restrict lets a
-  // batch's loads issue together ahead of its stores.
-  const float* __restrict__ hs = g.hs + (int64_t)b * g.S * g.D + 4 * t;
-  float* __restrict__ dcf = static_cast<float*>(g.dc) + (int64_t)b * g.S * g.D + 4 * t;
-  uint16_t* __restrict__ dch = static_cast<uint16_t*>(g.dc) + (int64_t)b * g.S * g.D + 4 * t;
-  const bool bf16 = g.dc_bf16 != 0;
-  for (int top = r1; top > r0; top -= kBatch) {      // rows top - 1 down to top - kBatch
-    float4 v[kBatch];
-    load_rows(g, hs, [&](int k) { return top - 1 - k >= r0 ? top - 1 - k : r0; }, v);
+  const int cr = (g.brows + P.np - 1) / P.np;
+  const int c0 = r0 + P.p * cr < r1 ? r0 + P.p * cr : r1;
+  const int c1 = c0 + cr < r1 ? c0 + cr : r1;
+  // The workspace and dc never overlap (checked at launch): restrict lets the
+  // loads issue together ahead of the stores.
+  const float* __restrict__ hs = g.hs + (int64_t)b * g.S * g.D + 4 * P.col;
+  const float* __restrict__ tot = g.tot + (int64_t)b * g.nblk * g.D + 4 * P.col;
+  float4 rows[kChunkRows];
+  float4 lat = make_float4(0.f, 0.f, 0.f, 0.f), own = lat;
+  if (P.p < P.np) {
 #pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const int r = top - 1 - k;
-      if (r >= r0) {
-        add4(cy, v[k]);
-        if (bf16) {
-          const uint2 wv = {pack_bf16x2(cy.x, cy.y), pack_bf16x2(cy.z, cy.w)};
-          *reinterpret_cast<uint2*>(dch + (int64_t)r * g.D) = wv;
-        } else {
-          *reinterpret_cast<float4*>(dcf + (int64_t)r * g.D) = cy;
-        }
+    for (int k = 0; k < kChunkRows; ++k)        // rows c1 - 1 - k (clamped)
+      rows[k] = *reinterpret_cast<const float4*>(hs + (int64_t)(c1 - 1 - k >= c0 ? c1 - 1 - k : r0) * g.D);
+    for (int x = blk + 1 + P.p; x < g.nblk; x += kBatch * P.np) {
+      float4 v[kBatch];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const int xx = x + k * P.np;
+        v[k] = *reinterpret_cast<const float4*>(tot + (int64_t)(xx < g.nblk ? xx : x) * g.D);
+      }
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k)
+        if (x + k * P.np < g.nblk) add4(lat, v[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < kChunkRows; ++k)
+      if (c1 - 1 - k >= c0) add4(own, rows[k]);
+  }
+  later[threadIdx.x] = lat;
+  chunk[threadIdx.x] = own;
+  __syncthreads();
+  if (P.p >= P.np || c0 >= c1) return;
+  float4 cy = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int q = 0; q < P.np; ++q) add4(cy, later[q * P.cpt + P.col]);
+  for (int q = P.np - 1; q > P.p; --q) add4(cy, chunk[q * P.cpt + P.col]);
+  float* __restrict__ dcf = static_cast<float*>(g.dc) + (int64_t)b * g.S * g.D + 4 * P.col;
+  uint16_t* __restrict__ dch = static_cast<uint16_t*>(g.dc) + (int64_t)b * g.S * g.D + 4 * P.col;
+  const bool bf16 = g.dc_bf16 != 0;
+#pragma unroll
+  for (int k = 0; k < kChunkRows; ++k) {
+    const int r = c1 - 1 - k;
+    if (r >= c0) {
+      add4(cy, rows[k]);
+      if (bf16) {
+        const uint2 wv = {pack_bf16x2(cy.x, cy.y), pack_bf16x2(cy.z, cy.w)};
+        *reinterpret_cast<uint2*>(dch + (int64_t)r * g.D) = wv;
+      } else {
+        *reinterpret_cast<float4*>(dcf + (int64_t)r * g.D) = cy;
       }
     }
   }
@@ -470,21 +548,19 @@ FAGQ_API int fagq_mla_bwd_launch(const void* q, const void* c_kv, const void* ou
   hipStream_t st = static_cast<hipStream_t>(stream);
   void* args[] = {&g};
   const int rows_per_wg = kThreads / (int)(D / 8);
-  hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_stream_do),
-                                 dim3((unsigned)((S + rows_per_wg - 1) / rows_per_wg), (unsigned)B,
-                                      (unsigned)g.hsplit),
-                                 dim3(kThreads), args, 0, st);
+  const dim3 k1_grid((unsigned)((S + rows_per_wg - 1) / rows_per_wg), (unsigned)B, (unsigned)g.hsplit);
+  const bool k1_wide = (int64_t)k1_grid.x * k1_grid.y * k1_grid.z <= kMinK1Groups;
+  hipError_t e = hipLaunchKernel(k1_wide ? reinterpret_cast<const void*>(&mla_stream_do<8>)
+                                         : reinterpret_cast<const void*>(&mla_stream_do<2>),
+                                 k1_grid, dim3(kThreads), args, 0, st);
   if (e != hipSuccess) return -(int)e;
-  const size_t lds = (size_t)(2 * kRowsK0 + kE) * (D + kPadElems) * 2 + (size_t)kRowsK0 * kE * 4;
-  e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_exact_rows),
-                      dim3((unsigned)(B * H), (unsigned)((g.erows + kRowsK0 - 1) / kRowsK0)),
-                      dim3(kThreads), args, lds, st);
-  if (e != hipSuccess) return -(int)e;
-  e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_block_total),
-                      dim3((unsigned)g.nblk, (unsigned)B), dim3(kThreads), args, 0, st);
+  // H + nblk < 2^17 + 2^20: nblk <= S / 16 + 1 and H S D 4 < 2^32 with D >= 64.
+  e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_exact_rows_block_total),
+                      dim3((unsigned)(H + g.nblk), (unsigned)B), dim3(kWide), args, k2_lds_bytes(D),
+                      st);
   if (e != hipSuccess) return -(int)e;
   e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_suffix_scan),
-                      dim3((unsigned)g.nblk, (unsigned)B), dim3(kThreads), args, 0, st);
+                      dim3((unsigned)g.nblk, (unsigned)B), dim3(kWide), args, 0, st);
   return e == hipSuccess ? FAGQ_OK : -(int)e;
 }
 

@@ -50,7 +50,7 @@ FAGQ_API int64_t fagq_mla_bwd_workspace_bytes(int64_t B, int64_t S, int64_t D);
  * (dq_dtype, dc_dtype), 16-byte aligned.  workspace: at least
  * fagq_mla_bwd_workspace_bytes(B, S, D) bytes, 16-byte aligned, overwritten.
  * 64 <= D <= FAGQ_MLA_MAX_D, D % 64 == 0; B, H <= 65535; S >= 1;
- * H * S * D * 4 < 2^32.  Four kernels on `stream`. */
+ * H * S * D * 4 < 2^32.  Three kernels on `stream`. */
 FAGQ_API int fagq_mla_bwd_launch(const void* q, const void* c_kv, const void* out, const void* dout,
                                  const float* lse, void* dq, void* dc_kv, void* workspace,
                                  int64_t workspace_bytes, int64_t B, int64_t H, int64_t S,
