@@ -18,16 +18,17 @@
 //
 // Selection is exact and never runs a sorting network:
 //   1. The fp32 range [vmin, vmax] of the selectable scores (non-selectable
-//      blocks hold -inf) defines 255 bins, bin(v) = clamp((v - vmin) * s +
-//      1.5, 0, 255) with s = 255 / (vmax - vmin): a monotone function of the
-//      score, 0 only for -inf.
+//      blocks hold -inf) defines 255 bins, bin(v) = round(clamp(v s + c, 0,
+//      255)) with s = 255 / (vmax - vmin), c = 1.5 - vmin s: a monotone
+//      function of the score, 0 only for -inf (one fma and one
+//      v_cvt_pk_u8_f32, which also packs four bins per word).
 //   2. An LDS histogram of the bins; its suffix sums above(b) (blocks in
 //      higher bins) give the boundary bin b* holding the top_k-th block.
 //      The candidates are the blocks of bins >= b*: found = above(b*) of them
 //      are certainly selected, and all of them fit in CAP = 512.
-//   3. Counting sort: a candidate is stored at above(bin) plus a per-bin
-//      cursor, so each bin owns one segment of the candidate array, bins in
-//      descending order.  A candidate's rank is above(bin) plus the number of
+//   3. Counting sort: a candidate is stored at its bin's cursor, which starts
+//      at above(bin), so each bin owns one segment of the candidate array,
+//      bins in descending order.  A candidate's rank is above(bin) plus the number of
 //      candidates in its own segment that precede it (64-bit composite key:
 //      (ordered score bits << 32) | (0xffffffff - id)); for Gaussian-like
 //      scores a segment holds a few blocks.  Ranks below top_k are written
@@ -80,14 +81,13 @@ __device__ __forceinline__ uint32_t div_bs(const DArgs& g, uint32_t n) {
 
 struct Lds {
   uint32_t hist[kBins + 64];        // bin counts, then one discard word per lane
-  uint32_t fill[kBins];             // per-bin scatter cursors
-  uint32_t above[kBins];            // candidates in higher bins (segment starts)
+  uint32_t above[kBins];            // candidates in higher bins; the scatter's per-bin cursors
   uint64_t cand[kCap + 4];           // 4 spare entries: the rank loop reads in fours
-  float fslot[kMaxWaves][2];        // per-wave max / min
+  uint32_t kslot[kMaxWaves][2];     // per-wave max / min (ord_key)
   uint32_t uslot[2][kMaxWaves][4];  // per-wave partials of the refinement
   uint32_t ncur;                    // refinement scatter cursor
 };
-constexpr int kZeroWords = kBins + 64 + kBins;   // hist and fill, cleared per row
+constexpr int kZeroWords = kBins + 64;   // hist, cleared per row
 static_assert(kZeroWords % 4 == 0, "cleared with 16-byte stores");
 
 // --------------------------------------------------------- wave primitives
@@ -116,10 +116,24 @@ __device__ __forceinline__ uint32_t wave_reduce(uint32_t v, Op op) {
   }
   return v;
 }
-struct FMax { __device__ uint32_t operator()(uint32_t a, uint32_t b) const {
-  return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b))); } };
-struct FMin { __device__ uint32_t operator()(uint32_t a, uint32_t b) const {
-  return __float_as_uint(fminf(__uint_as_float(a), __uint_as_float(b))); } };
+struct UMax {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; }
+};
+struct UMin {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a < b ? a : b; }
+};
+
+// Order-preserving uint32 image of a non-NaN fp32 value (a < b implies
+// ord_key(a) < ord_key(b); -0 sorts just below +0) and its inverse.  Wave and
+// workgroup min / max run on these keys: one integer op per step, where fp32
+// fmaxf / fminf would also quiet their operands.
+__device__ __forceinline__ uint32_t ord_key(float v) {
+  const uint32_t u = __float_as_uint(v);
+  return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
+}
+__device__ __forceinline__ float ord_val(uint32_t k) {
+  return __uint_as_float(k ^ (~(uint32_t)((int32_t)k >> 31) | 0x80000000u));
+}
 
 // Value of lane (lane ^ m), m a power of two below 64.
 __device__ __forceinline__ uint32_t xor_lane(uint32_t v, int m, int lane) {
@@ -178,13 +192,21 @@ __device__ __forceinline__ uint64_t composite(float v, uint32_t id) {
   return ((uint64_t)score_key(v) << 32) | (uint64_t)(0xffffffffu - id);
 }
 
-// Histogram bin of a score under the linear map of [vmin, vmax] (s = 255 /
-// (vmax - vmin), finite and positive): clamp(fma(v - vmin, s, 1.5), 0, 255)
-// truncated.  It is non-decreasing in v; a selectable score (v >= vmin) gets
-// a bin in [1, 255] and -inf gets bin 0.
-__device__ __forceinline__ uint32_t fbin(float v, float vmin, float s) {
-  return (uint32_t)fminf(fmaxf(fmaf(v - vmin, s, 1.5f), 0.0f), (float)(kBins - 1));
+// Histogram bin of a score under the linear map of [vmin, vmax]: s = 255 /
+// (vmax - vmin), finite and positive, and c = fma(-vmin, s, 1.5) with
+// |vmin s| < 2^21.  x = fma(v, s, c) is then within 0.125 of
+// (v - vmin) s + 1.5, and v_cvt_pk_u8_f32 rounds it to the nearest integer
+// clamped to [0, 255] (-inf -> 0), written into byte `byte` of `word`.  The
+// bin is non-decreasing in v; a selectable score (v >= vmin) gets a bin in
+// [1, 255] (x >= 1.375) and -inf gets bin 0.
+__device__ __forceinline__ uint32_t fbin_pack(float v, float s, float c, uint32_t byte,
+                                              uint32_t word) {
+  return __builtin_amdgcn_cvt_pk_u8_f32(fmaf(v, s, c), byte, word);
 }
+__device__ __forceinline__ uint32_t fbin(float v, float s, float c) {
+  return fbin_pack(v, s, c, 0u, 0u);
+}
+constexpr float kMaxBinOffset = 2097152.0f;   // 2^21: bound on |vmin s| for the map above
 
 template <bool B>
 struct BoolC {
@@ -203,13 +225,13 @@ __device__ __forceinline__ int elem_off(int e) {
 // above(b) < need <= above(b) + hist[b], above(b) = count in bins > b.
 // Every lane receives bin, above(bin), hist[bin] and the histogram total.
 // STORE marks the fp32-bin histogram: its bin 0 (non-selectable blocks) is
-// left out, and above(b) is written to lds.above (identical values from
-// every wave).
+// left out, and, where `store`, above(b) is written to lds.above.
 struct Boundary {
   uint32_t bin, above, cnt, total;
 };
 template <bool STORE>
-__device__ __forceinline__ Boundary find_boundary(Lds& lds, uint32_t k, int lane) {
+__device__ __forceinline__ Boundary find_boundary(Lds& lds, uint32_t k, int lane,
+                                                  bool store = false) {
   u32x4 h = reinterpret_cast<const u32x4*>(lds.hist)[lane];   // bins 4 lane .. 4 lane + 3
   if (STORE && lane == 0) h[0] = 0u;     // fp32 bins: bin 0 counts non-selectable blocks
   const uint32_t sum = h[0] + h[1] + h[2] + h[3];
@@ -222,7 +244,8 @@ __device__ __forceinline__ Boundary find_boundary(Lds& lds, uint32_t k, int lane
   a[2] = a[3] + h[3];
   a[1] = a[2] + h[2];
   a[0] = a[1] + h[1];
-  if constexpr (STORE) reinterpret_cast<u32x4*>(lds.above)[lane] = a;
+  if constexpr (STORE)
+    if (store) reinterpret_cast<u32x4*>(lds.above)[lane] = a;
   uint32_t bin = 0, ab = 0, cb = 0;
   bool hit = false;
 #pragma unroll
@@ -313,28 +336,42 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
         const float v = vec_elem<BF16>(d, c);
         sv[e] = decltype(full_c)::value || lbase < nvalid - wbase - elem_off<BF16>(e) ? v : ninf;
         vmax = fmaxf(vmax, sv[e]);
-        vmin = fminf(vmin, sv[e] != ninf ? sv[e] : __builtin_inff());
+        // A full wave takes the plain minimum and redoes it below in the rare
+        // case that an explicit -inf score made it -inf.
+        if constexpr (decltype(full_c)::value) vmin = fminf(vmin, sv[e]);
+        else vmin = fminf(vmin, sv[e] != ninf ? sv[e] : __builtin_inff());
       }
+    }
+    if (decltype(full_c)::value && vmin == ninf) {
+      vmin = __builtin_inff();
+#pragma unroll
+      for (int e = 0; e < kEPL; ++e) vmin = fminf(vmin, sv[e] != ninf ? sv[e] : __builtin_inff());
     }
   };
   if (full) load(BoolC<true>());
   else load(BoolC<false>());
-  vmax = __uint_as_float(wave_reduce(__float_as_uint(vmax), FMax()));
-  vmin = __uint_as_float(wave_reduce(__float_as_uint(vmin), FMin()));
+  uint32_t kmax = wave_reduce(ord_key(vmax), UMax());
+  uint32_t kmin = wave_reduce(ord_key(vmin), UMin());
   if (lane == 0) {
-    lds.fslot[w][0] = vmax;
-    lds.fslot[w][1] = vmin;
+    lds.kslot[w][0] = kmax;
+    lds.kslot[w][1] = kmin;
   }
   __syncthreads();
   for (int x = 0; x < nwv; ++x) {
-    vmax = fmaxf(vmax, lds.fslot[x][0]);
-    vmin = fminf(vmin, lds.fslot[x][1]);
+    kmax = kmax > lds.kslot[x][0] ? kmax : lds.kslot[x][0];
+    kmin = kmin < lds.kslot[x][1] ? kmin : lds.kslot[x][1];
   }
+  vmax = ord_val(kmax);
+  vmin = ord_val(kmin);
 
-  // Bin map (see fbin); a degenerate or non-finite range puts every
-  // selectable score in bin 1.
-  const float s = (float)(kBins - 1) / (vmax - vmin);
-  const bool degen = !(vmax > vmin) || !(s > 0.0f) || !__builtin_isfinite(s);
+  // Bin map (see fbin); a degenerate or non-finite range, or one too narrow
+  // for its offset (|vmin s| >= 2^21), puts every selectable score in bin 1.
+  // s needs no correct rounding: the histogram and the ranks use the same s
+  // and c, and x(vmax) stays within rounding of 256.5, which clamps to 255.
+  const float s = (float)(kBins - 1) * __builtin_amdgcn_rcpf(vmax - vmin);
+  const float c = fmaf(-vmin, s, 1.5f);
+  const bool degen = !(vmax > vmin) || !(s > 0.0f) || !__builtin_isfinite(s) ||
+                     !(fabsf(vmin * s) < kMaxBinOffset);
   // Bins of the lane's scores, four 8-bit bins per word (0: not selectable).
   // Non-selectable blocks count in bin 0 (ignored) in a full wave, where
   // they are rare, else in the lane's own discard word.
@@ -342,14 +379,18 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
   auto hist = [&](auto full_c, auto binf) {
 #pragma unroll
     for (int e = 0; e < kEPL; ++e) {
-      const uint32_t bn = binf(sv[e]);
-      pbin[e / 4] = e % 4 ? pbin[e / 4] | (bn << (8 * (e % 4))) : bn;
+      pbin[e / 4] = binf(sv[e], (uint32_t)(e % 4), e % 4 ? pbin[e / 4] : 0u);
+      const uint32_t bn = (pbin[e / 4] >> (8 * (e % 4))) & 0xffu;
       const uint32_t at = decltype(full_c)::value || bn ? bn : (uint32_t)(kBins + lane);
       __hip_atomic_fetch_add(&lds.hist[at], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   };
-  auto bin_lin = [=](float v) { return fbin(v, vmin, s); };
-  auto bin_one = [=](float v) { return v != ninf ? 1u : 0u; };
+  auto bin_lin = [=](float v, uint32_t byte, uint32_t word) {
+    return fbin_pack(v, s, c, byte, word);
+  };
+  auto bin_one = [=](float v, uint32_t byte, uint32_t word) {
+    return word | ((v != ninf ? 1u : 0u) << (8 * byte));
+  };
   if (!degen) {
     if (full) hist(BoolC<true>(), bin_lin);
     else hist(BoolC<false>(), bin_lin);
@@ -359,7 +400,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
   }
   __syncthreads();
 
-  const Boundary bd = find_boundary<true>(lds, (uint32_t)K, lane);
+  const Boundary bd = find_boundary<true>(lds, (uint32_t)K, lane, w == 0);
   uint32_t nc = bd.total ? bd.above + bd.cnt : 0u;
   const bool refine = nc > kCap;
 
@@ -370,12 +411,13 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
     // keys in one pass over the candidates below.
     const uint32_t bstar = bd.bin > 1u ? bd.bin : 1u;
     const uint32_t nid = 0xffffffffu - (uint32_t)(wbase + lbase);
+    __syncthreads();                      // above(b) stored by wave 0
 #pragma unroll
     for (int e = 0; e < kEPL; ++e) {
       const uint32_t bn = (pbin[e / 4] >> (8 * (e % 4))) & 0xffu;
       if (bn >= bstar) {
-        const uint32_t p = lds.above[bn] +
-            __hip_atomic_fetch_add(&lds.fill[bn], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const uint32_t p = __hip_atomic_fetch_add(&lds.above[bn], 1u, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_WORKGROUP);
         lds.cand[p & (kCap - 1)] = ((uint64_t)__float_as_uint(sv[e]) << 32) |
                                    (uint64_t)(nid - (uint32_t)elem_off<BF16>(e));
       }
@@ -487,9 +529,9 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
     const uint64_t mine = lds.cand[i];
     uint32_t st = 0, len = nc;
     if (!refine) {
-      const uint32_t bb = degen ? 1u : fbin(key_score((uint32_t)(mine >> 32)), vmin, s);
-      st = lds.above[bb];
+      const uint32_t bb = degen ? 1u : fbin(key_score((uint32_t)(mine >> 32)), s, c);
       len = lds.hist[bb];
+      st = lds.above[bb] - len;          // the scatter advanced above(bb) by its count
     }
     st = st < nc ? st : nc;
     const uint32_t end = len < nc - st ? st + len : nc;

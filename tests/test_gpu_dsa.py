@@ -45,6 +45,10 @@ def case(seed, B=2, H=2, Q=24, NB=512, bs=16, dtype=torch.float32, ties=None, id
         s[..., 3] = 1e30
     elif ties == "cluster":                  # half the row in a narrow band above the rest
         s = torch.where(torch.rand(s.shape, generator=g) < 0.5, 5 + 1e-4 * s, s)
+    elif ties == "offset":                   # range tiny next to the magnitude: degenerate bin map
+        s = 1000 + 1e-3 * s
+    elif ties == "offset_lin":               # large bin offset (|vmin s| ~ 4e4), still linear
+        s = 10 + 1e-2 * s
     s[torch.rand(s.shape, generator=g) < 0.01] = float("-inf")
     s = s.to(dtype)
     kv = torch.randint(0, NB * bs + 2 * bs, (B,), generator=g).to(idx)
@@ -61,7 +65,8 @@ def test_dsa_random(pkg, gpu, NB, k):
     check(pkg, gpu, s, pt, pos, kv, 16, k, f"random NB={NB}")
 
 
-@pytest.mark.parametrize("ties", ["round", "heavy", "equal", "outlier", "cluster"])
+@pytest.mark.parametrize("ties", ["round", "heavy", "equal", "outlier", "cluster", "offset",
+                                  "offset_lin"])
 @pytest.mark.parametrize("NB,k", [(4096, 128), (2048, 64), (1024, 256)])
 def test_dsa_ties(pkg, gpu, ties, NB, k):
     s, pt, pos, kv = case(7, NB=NB, ties=ties)
