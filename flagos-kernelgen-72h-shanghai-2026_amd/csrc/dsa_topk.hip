@@ -81,7 +81,8 @@ __device__ __forceinline__ uint32_t div_bs(const DArgs& g, uint32_t n) {
 
 struct Lds {
   uint32_t hist[kBins + 64];        // bin counts, then one discard word per lane
-  uint32_t above[kBins];            // candidates in higher bins; the scatter's per-bin cursors
+  uint32_t above[kBins];            // 8 x candidates in higher bins: cand byte offsets, then
+                                    // the scatter's per-bin cursors
   uint64_t cand[kCap + 4];           // 4 spare entries: the rank loop reads in fours
   uint32_t kslot[kMaxWaves][2];     // per-wave max / min (ord_key)
   uint32_t uslot[2][kMaxWaves][4];  // per-wave partials of the refinement
@@ -225,7 +226,8 @@ __device__ __forceinline__ int elem_off(int e) {
 // above(b) < need <= above(b) + hist[b], above(b) = count in bins > b.
 // Every lane receives bin, above(bin), hist[bin] and the histogram total.
 // STORE marks the fp32-bin histogram: its bin 0 (non-selectable blocks) is
-// left out, and, where `store`, above(b) is written to lds.above.
+// left out, and, where `store`, 8 above(b) (the byte offset of bin b's
+// segment of lds.cand) is written to lds.above.
 struct Boundary {
   uint32_t bin, above, cnt, total;
 };
@@ -245,7 +247,8 @@ __device__ __forceinline__ Boundary find_boundary(Lds& lds, uint32_t k, int lane
   a[1] = a[2] + h[2];
   a[0] = a[1] + h[1];
   if constexpr (STORE)
-    if (store) reinterpret_cast<u32x4*>(lds.above)[lane] = a;
+    if (store)
+      reinterpret_cast<u32x4*>(lds.above)[lane] = u32x4{8u * a[0], 8u * a[1], 8u * a[2], 8u * a[3]};
   uint32_t bin = 0, ab = 0, cb = 0;
   bool hit = false;
 #pragma unroll
@@ -325,15 +328,19 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
   const float ninf = -__builtin_inff();
   float sv[kEPL];
   float vmax = ninf, vmin = __builtin_inff();
+  // Every vector load is issued before the full / partial split.
+  u32x4 raw[kEPL / VEC];
+#pragma unroll
+  for (int i = 0; i < kEPL / VEC; ++i)
+    raw[i] = __builtin_amdgcn_raw_buffer_load_b128(
+        rs, (uint32_t)(wbase * esz) + (uint32_t)(i * 64 + lane) * 16u, 0, 0);
   auto load = [&](auto full_c) {
 #pragma unroll
     for (int i = 0; i < kEPL / VEC; ++i) {
-      const u32x4 d = __builtin_amdgcn_raw_buffer_load_b128(
-          rs, (uint32_t)(wbase * esz) + (uint32_t)(i * 64 + lane) * 16u, 0, 0);
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
         const int e = i * VEC + c;
-        const float v = vec_elem<BF16>(d, c);
+        const float v = vec_elem<BF16>(raw[i], c);
         sv[e] = decltype(full_c)::value || lbase < nvalid - wbase - elem_off<BF16>(e) ? v : ninf;
         vmax = fmaxf(vmax, sv[e]);
         // A full wave takes the plain minimum and redoes it below in the rare
@@ -416,10 +423,13 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
     for (int e = 0; e < kEPL; ++e) {
       const uint32_t bn = (pbin[e / 4] >> (8 * (e % 4))) & 0xffu;
       if (bn >= bstar) {
-        const uint32_t p = __hip_atomic_fetch_add(&lds.above[bn], 1u, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_WORKGROUP);
-        lds.cand[p & (kCap - 1)] = ((uint64_t)__float_as_uint(sv[e]) << 32) |
-                                   (uint64_t)(nid - (uint32_t)elem_off<BF16>(e));
+        // The cursor returns the entry's byte offset; a bin's slots end at
+        // 8 (above(b*) + hist[b*]) = 8 nc <= 8 CAP, so no mask is needed.
+        const uint32_t off = __hip_atomic_fetch_add(&lds.above[bn], 8u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_WORKGROUP);
+        const uint32_t lo = nid - (uint32_t)elem_off<BF16>(e);
+        *reinterpret_cast<uint64_t*>(reinterpret_cast<uint8_t*>(lds.cand) + off) =
+            ((uint64_t)__float_as_uint(sv[e]) << 32) | (uint64_t)lo;
       }
     }
   } else {
@@ -531,7 +541,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
     if (!refine) {
       const uint32_t bb = degen ? 1u : fbin(key_score((uint32_t)(mine >> 32)), s, c);
       len = lds.hist[bb];
-      st = lds.above[bb] - len;          // the scatter advanced above(bb) by its count
+      st = (lds.above[bb] >> 3) - len;   // the scatter advanced the cursor by 8 per entry
     }
     st = st < nc ? st : nc;
     const uint32_t end = len < nc - st ? st + len : nc;
