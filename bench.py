@@ -522,7 +522,7 @@ def dsa_bench(args, torch, pkg, w) -> int:
 
 
 def mla_bench(args, torch, pkg, w) -> int:
-    """Times fagq_mla_bwd_launch (Task 03; four kernels per call) with inputs
+    """Times fagq_mla_bwd_launch (Task 03; three kernels per call) with inputs
     resident in HBM, do / dq / dc sets rotated past the MALL; per-call time by
     HIP events on the launch stream."""
     import ctypes
