@@ -102,7 +102,7 @@ __device__ __forceinline__ void store8(const rsrc_t& rs, bool bf16, uint32_t e, 
 // flight per lane: U = 2 keeps the kernel at 50 VGPRs, 8 workgroups per CU,
 // for grids of 2048 and more; U = 8 (110 VGPRs, 4 per CU) for grids that fit
 // 4 per CU, where each workgroup's few heads are then loaded at once.
-template <int U>
+template <int U, bool HALVES>
 __global__ void __launch_bounds__(kThreads) mla_stream_do(const MArgs g) {
   const int lpr = g.D / 8;                        // lanes per row
   const int t = threadIdx.x;
@@ -115,7 +115,12 @@ __global__ void __launch_bounds__(kThreads) mla_stream_do(const MArgs g) {
   const rsrc_t rdo = make_rsrc(g.dout + (int64_t)b * hsd, hsd * 2u);
   const rsrc_t rdq = make_rsrc((const uint8_t*)g.dq + (int64_t)b * hsd * (g.dq_bf16 ? 2 : 4),
                                hsd * (g.dq_bf16 ? 2u : 4u));
-  const uint32_t e0 = (uint32_t)row * (uint32_t)g.D + (uint32_t)(t % lpr) * 8u;   // head 0
+  // Elements of the lane (head 0): 8 consecutive from ea, or with HALVES 4
+  // from ea and 4 from eb = ea + D / 2, so that each of its two 16-byte fp32
+  // stores lies in a contiguous half-row span of the row's lanes.
+  const uint32_t li = (uint32_t)(t % lpr);
+  const uint32_t ea = (uint32_t)row * (uint32_t)g.D + li * (HALVES ? 4u : 8u);
+  const uint32_t eb = ea + (uint32_t)g.D / 2u;
   const uint32_t hstride = (uint32_t)g.S * (uint32_t)g.D;
   const bool write_dq = row >= g.erows;
   const bool dq_bf16 = g.dq_bf16 != 0;
@@ -127,8 +132,28 @@ __global__ void __launch_bounds__(kThreads) mla_stream_do(const MArgs g) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int h = h0 + u < hend ? h0 + u : hend - 1;
-      v[u] = __builtin_amdgcn_raw_buffer_load_b128(rdo, (e0 + (uint32_t)h * hstride) * 2u, 0,
-                                                   kNonTemporal);
+      const uint32_t ho = (uint32_t)h * hstride;
+      if constexpr (HALVES) {
+        const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rdo, (ea + ho) * 2u, 0, kNonTemporal);
+        const u32x2 y = __builtin_amdgcn_raw_buffer_load_b64(rdo, (eb + ho) * 2u, 0, kNonTemporal);
+        v[u] = u32x4{x[0], x[1], y[0], y[1]};
+      } else {
+        v[u] = __builtin_amdgcn_raw_buffer_load_b128(rdo, (ea + ho) * 2u, 0, kNonTemporal);
+      }
+    }
+  };
+  // 8 fp32 values of the lane at head offset ho: one 16-byte bf16 or two
+  // 16-byte fp32 stores at ea (HALVES: the second at eb).
+  auto store_lane = [&](const rsrc_t& rs, bool bf16, uint32_t ho, const float (&v)[8]) {
+    if constexpr (HALVES) {
+      const u32x4 x = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                       __float_as_uint(v[3])};
+      const u32x4 y = {__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]),
+                       __float_as_uint(v[7])};
+      __builtin_amdgcn_raw_buffer_store_b128(x, rs, (ea + ho) * 4u, 0, kNonTemporal);
+      __builtin_amdgcn_raw_buffer_store_b128(y, rs, (eb + ho) * 4u, 0, kNonTemporal);
+    } else {
+      store8(rs, bf16, ea + ho, v);
     }
   };
   u32x4 cur[U], nxt[U];
@@ -150,7 +175,7 @@ __global__ void __launch_bounds__(kThreads) mla_stream_do(const MArgs g) {
           float d[8];
 #pragma unroll
           for (int k = 0; k < 8; ++k) d[k] = f[k] * g.scale;
-          store8(rdq, dq_bf16, e0 + (uint32_t)(h0 + u) * hstride, d);
+          store_lane(rdq, dq_bf16, (uint32_t)(h0 + u) * hstride, d);
         }
       }
     }
@@ -163,7 +188,7 @@ __global__ void __launch_bounds__(kThreads) mla_stream_do(const MArgs g) {
   for (int k = 0; k < 8; ++k) o[k] = acc[k] / n1;
   const uint32_t sd = (uint32_t)g.S * (uint32_t)g.D;
   const rsrc_t rhs = make_rsrc(g.hs + (int64_t)blockIdx.z * g.hs_split + (int64_t)b * sd, sd * 4u);
-  store8(rhs, false, (uint32_t)row * (uint32_t)g.D + (uint32_t)(t % lpr) * 8u, o);
+  store_lane(rhs, false, 0u, o);
 }
 
 // ------------------------------------------------------------------ K2: exact rows
@@ -550,9 +575,12 @@ FAGQ_API int fagq_mla_bwd_launch(const void* q, const void* c_kv, const void* ou
   const int rows_per_wg = kThreads / (int)(D / 8);
   const dim3 k1_grid((unsigned)((S + rows_per_wg - 1) / rows_per_wg), (unsigned)B, (unsigned)g.hsplit);
   const bool k1_wide = (int64_t)k1_grid.x * k1_grid.y * k1_grid.z <= kMinK1Groups;
-  hipError_t e = hipLaunchKernel(k1_wide ? reinterpret_cast<const void*>(&mla_stream_do<8>)
-                                         : reinterpret_cast<const void*>(&mla_stream_do<2>),
-                                 k1_grid, dim3(kThreads), args, 0, st);
+  const bool halves = dq_dtype == FAGQ_MLA_F32;
+  const void* k1 = halves ? (k1_wide ? reinterpret_cast<const void*>(&mla_stream_do<8, true>)
+                                     : reinterpret_cast<const void*>(&mla_stream_do<2, true>))
+                          : (k1_wide ? reinterpret_cast<const void*>(&mla_stream_do<8, false>)
+                                     : reinterpret_cast<const void*>(&mla_stream_do<2, false>));
+  hipError_t e = hipLaunchKernel(k1, k1_grid, dim3(kThreads), args, 0, st);
   if (e != hipSuccess) return -(int)e;
   // H + nblk < 2^17 + 2^20: nblk <= S / 16 + 1 and H S D 4 < 2^32 with D >= 64.
   e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_exact_rows_block_total),
