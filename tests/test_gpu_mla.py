@@ -92,10 +92,12 @@ def test_mla_matches_oracle(pkg, gpu, B, H, S, D, grad):
 
 @pytest.mark.parametrize("B,H,S,D", [(1, 5, 33, 192), (3, 9, 70, 320), (1, 13, 17, 448),
                                      (1, 7, 129, 384)])
-def test_mla_uneven_head_groups(pkg, gpu, B, H, S, D):
+@pytest.mark.parametrize("dq_dtype", [torch.bfloat16, torch.float32])
+def test_mla_uneven_head_groups(pkg, gpu, B, H, S, D, dq_dtype):
     # short sequences split the heads into 3, 5, 7 and 4 groups of partial
-    # head sums; D not a power of two leaves some scan threads idle
-    case(pkg, gpu, B, H, S, D, torch.bfloat16, torch.float32, seed=B + H + S)
+    # head sums; D not a power of two leaves some scan threads idle, and with
+    # fp32 dq the dO pass splits each row into two halves of D / 2
+    case(pkg, gpu, B, H, S, D, dq_dtype, torch.float32, seed=B + H + S)
 
 
 def test_mla_mixed_output_dtypes(pkg, gpu):
