@@ -53,6 +53,19 @@ METRIC = "achieved HBM GB/s (% of 8 TB/s peak) + µs/call, 16384×7168 bf16→fp
 ROTATE_BYTES = 1 << 30     # rotate buffer sets until > 1 GiB (4x the 256 MB MALL)
 
 
+def measured_traffic(name: str):
+    """HBM bytes per launch (per call for multi-kernel operators) from the committed
+    profiles/traffic_<name>.json, measured with rocprofv3 FETCH_SIZE / WRITE_SIZE runs and
+    calibrated against a copy kernel; None when no such file exists."""
+    tfile = REPO_DIR / "profiles" / f"traffic_{name}.json"
+    if not tfile.exists():
+        return None
+    try:
+        return json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+    except (ValueError, OSError):
+        return None
+
+
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
@@ -214,13 +227,7 @@ def main() -> int:
     value = set_bytes / (wall_ms * 1e-3) / 1e9
     achieved = set_bytes / (kern_ms * 1e-3) / 1e9
 
-    traffic = None
-    tfile = REPO_DIR / "profiles" / f"traffic_{name}.json"
-    if tfile.exists():
-        try:
-            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
-        except (ValueError, OSError):
-            traffic = None
+    traffic = measured_traffic(name)
 
     route = pkg.route_for(w.M, w.D, w.group_size)
     out = {
@@ -388,7 +395,8 @@ def parts_bench(args, torch, pkg, w) -> int:
         "us_per_call_host_wall": round(wall_ms * 1e3, 2),
         "pct_of_peak": round(100.0 * achieved / PEAK_HBM_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": measured_traffic(w.name)},
         "cpu_baseline": None,
     }
     if args.cpu_seconds > 0:
@@ -512,7 +520,8 @@ def dsa_bench(args, torch, pkg, w) -> int:
         "rows_per_s": round(w.rows / (kern_ms * 1e-3), 1),
         "pct_of_peak": round(100.0 * achieved / PEAK_HBM_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": measured_traffic(w.name)},
         "cpu_baseline": None,
     }
     if args.cpu_seconds > 0:
@@ -593,7 +602,8 @@ def mla_bench(args, torch, pkg, w) -> int:
         "us_per_call_host_wall": round(wall_ms * 1e3, 2),
         "pct_of_peak": round(100.0 * achieved / PEAK_HBM_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": measured_traffic(w.name)},
         "cpu_baseline": None,
     }
     if args.cpu_seconds > 0:
@@ -724,13 +734,7 @@ def gemm_bench(args, torch, pkg, w) -> int:
     flops = w.flops()
     value = flops / (wall_ms * 1e-3) / 1e12
     achieved = flops / (kern_ms * 1e-3) / 1e12
-    traffic = None
-    tfile = REPO_DIR / "profiles" / f"traffic_{w.name}.json"
-    if tfile.exists():
-        try:
-            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
-        except (ValueError, OSError):
-            traffic = None
+    traffic = measured_traffic(w.name)
     out = {
         "metric": "fp8 block-scaled GEMM TFLOP/s (% of 5.0 PFLOP/s dense fp8), consumer of "
                   "the quantizer's codes and scales",
