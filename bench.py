@@ -119,7 +119,7 @@ def main() -> int:
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(rows shard with no exchange; see DESIGN.md for the multi-GPU design)",
+              "(rows shard with no exchange: one process per GPU runs its own row block)",
               file=sys.stderr)
         return 2
     sys.path.insert(0, str(REPO_DIR))
