@@ -28,8 +28,8 @@
 //      are certainly selected, and all of them fit in CAP = 512.
 //   3. Counting sort: a candidate is stored at its bin's cursor, which starts
 //      at above(bin), so each bin owns one segment of the candidate array,
-//      bins in descending order.  A candidate's rank is above(bin) plus the number of
-//      candidates in its own segment that precede it (64-bit composite key:
+//      bins in descending order.  A candidate's rank is above(bin) plus the
+//      number of candidates in its own segment that precede it (64-bit composite key:
 //      (ordered score bits << 32) | (0xffffffff - id)); for Gaussian-like
 //      scores a segment holds a few blocks.  Ranks below top_k are written
 //      with their page-table entries.
