@@ -14,7 +14,7 @@
 // it are never fetched, and waves wholly past the prefix exit at once (a
 // workgroup barrier waits only for the waves still running).  Cross-lane
 // steps use DPP and v_permlane32_swap; the waves of a row combine through LDS
-// and three workgroup barriers.
+// and five workgroup barriers.
 //
 // Selection is exact and never runs a sorting network:
 //   1. The fp32 range [vmin, vmax] of the selectable scores (non-selectable
@@ -537,6 +537,10 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
   const int64_t ob = row * K;
   for (uint32_t i = (uint32_t)t; i < nc; i += (uint32_t)stride) {
     const uint64_t mine = lds.cand[i];
+    const uint32_t id = 0xffffffffu - (uint32_t)mine;
+    // Loaded ahead of the count, which then covers its latency; every
+    // candidate's id lies in the valid prefix, so below NB.
+    const int32_t page = g.page_table[(int64_t)b * g.NB + (id < (uint32_t)g.NB ? id : 0u)];
     uint32_t st = 0, len = nc;
     if (!refine) {
       const uint32_t bb = degen ? 1u : fbin(key_score((uint32_t)(mine >> 32)), s, c);
@@ -551,10 +555,9 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
       r += (c0 > mine ? 1u : 0u) + (j + 1 < end && c1 > mine ? 1u : 0u) +
            (j + 2 < end && c2 > mine ? 1u : 0u) + (j + 3 < end && c3 > mine ? 1u : 0u);
     }
-    const uint32_t id = 0xffffffffu - (uint32_t)mine;
     if (r < (uint32_t)K && id < (uint32_t)g.NB) {
       g.out_blocks[ob + r] = (int32_t)id;
-      g.out_pages[ob + r] = g.page_table[(int64_t)b * g.NB + id];
+      g.out_pages[ob + r] = page;
     }
   }
   for (int i = (int)nc + t; i < K; i += stride) {
