@@ -34,6 +34,10 @@ output (fagq_gemm_launch); value and roofline in TFLOP/s against MI355X's
 5.0 PFLOP/s dense fp8 peak, cpu_baseline = the C oracle (oracle/gemm_oracle.c)
 on a row sample.
 
+--copy BYTES and --mfma-peak time the library's two ceiling probes instead: a
+plain 16-byte copy kernel (achievable HBM bandwidth, counter calibration) and
+the GEMM's matrix instruction issued from registers (achievable MFMA rate).
+
 Usage: python bench.py [--steps K] [--warmup W] [--config NAME] [--gpus 1]
 """
 from __future__ import annotations
@@ -78,6 +82,9 @@ def parse_args():
     p.add_argument("--copy", type=int, default=0, metavar="BYTES",
                    help="instead: time the library's plain 16-byte copy kernel over BYTES "
                         "(reference for achievable bandwidth and HBM counter calibration)")
+    p.add_argument("--mfma-peak", action="store_true",
+                   help="instead: time the library's register-only issue-rate probe of the fp8 "
+                        "GEMM's matrix instruction (the compute ceiling its rate is compared with)")
     return p.parse_args()
 
 
@@ -115,6 +122,40 @@ def copy_bench(args, torch, pkg) -> int:
     return 0
 
 
+def mfma_peak_bench(args, torch, pkg) -> int:
+    """Times fagq_diag_mfma_peak: 2048 workgroups of 4 waves, each wave issuing
+    1000 x 8 v_mfma_scale_f32_16x16x128_f8f6f4 on register operands."""
+    import ctypes
+    dev = torch.device("cuda:0")
+    lib = pkg.load_library()
+    blocks, iters = 2048, 1000
+    flops = blocks * 4 * iters * 8 * 65536
+    out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+
+    def step():
+        pkg._lib.check(lib.fagq_diag_mfma_peak(ctypes.c_void_p(out.data_ptr()), blocks, iters, sp),
+                       "fagq_diag_mfma_peak")
+
+    for _ in range(args.warmup):
+        step()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(dev)
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize(dev)
+    ms = e0.elapsed_time(e1) / args.steps
+    tflops = flops / (ms * 1e-3) / 1e12
+    print(json.dumps({"instruction": "v_mfma_scale_f32_16x16x128_f8f6f4", "flops_per_call": flops,
+                      "us_per_call": round(ms * 1e3, 2), "TFLOPs": round(tflops, 1),
+                      "frac_of_5000_TFLOPs": round(tflops / 5000.0, 4),
+                      "steps": args.steps, "warmup": args.warmup}), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -134,6 +175,8 @@ def main() -> int:
         return 2
     if args.copy:
         return copy_bench(args, torch, pkg)
+    if args.mfma_peak:
+        return mfma_peak_bench(args, torch, pkg)
     name = args.config or HEADLINE
     from fagq_mi355x.workloads import DSA_CONFIGS, GEMM_CONFIGS, MLA_CONFIGS, PARTS_CONFIGS
     if name in DSA_CONFIGS:

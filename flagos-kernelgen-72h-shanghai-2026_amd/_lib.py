@@ -57,6 +57,7 @@ SIGNATURES = {
     "fagq_version": ([], _I),
     "fagq_diag_encode": ([_P, _P, _I64, _I, _I, _P], _I),
     "fagq_diag_copy": ([_P, _P, _I64, _P], _I),
+    "fagq_diag_mfma_peak": ([_P, _I64, _I, _P], _I),
     "fagq_dsa_topk_launch": ([_P, _I, _P, _P, _P, _I, _P, _P] + [_I64] * 6 + [_P], _I),
     "fagq_gemm_launch": ([_P] * 5 + [_I64, _I64, _I64, _I, _I, _I, _P], _I),
     "fagq_gemm_query_route": ([_I64, _I64, _I64, ctypes.POINTER(GemmRoute)], _I),

@@ -8,9 +8,9 @@
 // quantized tensor and scales); this is the layer those formats feed.
 //
 // Work mapping.  A workgroup computes a 256 x 256 tile of C: 8 waves of
-// 64 x 128 (fp32 scales) or 4 waves of 128 x 128 (UE8M0 scales), each wave a
-// grid of 16 x 16 tiles, each one v_mfma_scale_f32_16x16x128_f8f6f4 per
-// 128-deep k-block.  The weight tile is the MFMA's first operand and the activation
+// 64 x 128 for every scale format, each wave a grid of 16 x 16 tiles, each
+// one v_mfma_scale_f32_16x16x128_f8f6f4 per 128-deep k-block.  The weight
+// tile is the MFMA's first operand and the activation
 // tile its second, so each lane's four results are four consecutive columns
 // of one row of C (lane l: row l % 16, columns 4 (l / 16) .. +4) and the
 // activation scale a lane needs is that of its own row.
@@ -42,6 +42,7 @@
 #include <stdint.h>
 
 #include "fagq.h"
+#include "fagq_diag.h"
 #include "fagq_dispatch.hpp"
 #include "fagq_gemm.h"
 
@@ -329,6 +330,32 @@ const void* kernel_for(int asf, int bsf, int* threads) {
   return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_F32, SF_F32, LayoutF32>);
 }
 
+// Issue-rate probe of the GEMM's instruction: every wave keeps 8 independent
+// 16 x 16 accumulators and issues iters x 8 v_mfma_scale_f32_16x16x128_f8f6f4
+// (E8M0 scales 2^-7 and 2^3) on register operands, with no memory access in
+// the loop; each thread then writes the sum of its accumulators.
+constexpr int kPeakThreads = 256;
+constexpr int kPeakChain = 8;
+__global__ void __launch_bounds__(kPeakThreads) mfma_peak_kernel(float* out, int iters) {
+  const int t = threadIdx.x;
+  i32x8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {   // fp8 e4m3 values near 1.0 (0x38) and 0.5 (0x30)
+    a[i] = 0x38383838 ^ (t * 7 + i);
+    b[i] = 0x30303030 ^ (t * 3 + i);
+  }
+  f32x4 c[kPeakChain] = {};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int j = 0; j < kPeakChain; ++j)
+      c[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c[j], 0, 0, 0, 120, 0, 130);
+  }
+  float r = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kPeakChain; ++j) r += c[j][0] + c[j][1] + c[j][2] + c[j][3];
+  out[(int64_t)blockIdx.x * kPeakThreads + t] = r;
+}
+
 }  // namespace
 }  // namespace gemm
 }  // namespace fagq
@@ -382,6 +409,21 @@ FAGQ_API int fagq_gemm_query_route(int64_t M, int64_t N, int64_t K, fagq_gemm_ro
   route->group_m = kGroupM;
   route->grid_blocks = ceil_div(M, kBM) * ceil_div(N, kBN);
   return FAGQ_OK;
+}
+
+FAGQ_API int fagq_diag_mfma_peak(float* out, int64_t blocks, int32_t iters, void* stream) {
+  if (!out) return FAGQ_E_NULL;
+  if (blocks < 1 || iters < 1) return FAGQ_E_SHAPE;
+  if (blocks > (1 << 20) || iters > (1 << 20)) return FAGQ_E_TOO_LARGE;
+  if (!aligned(out, 4)) return FAGQ_E_ALIGN;
+  const int dc = device_check();
+  if (dc != FAGQ_OK) return dc;
+  int it = iters;
+  void* args[] = {&out, &it};
+  const hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&mfma_peak_kernel),
+                                       dim3((unsigned)blocks), dim3(kPeakThreads), args, 0,
+                                       static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? FAGQ_OK : -(int)e;
 }
 
 }  // extern "C"

@@ -45,6 +45,15 @@ FAGQ_API int fagq_diag_encode(const float* in, void* out, int64_t n, int q_forma
  * plain 16-byte-vector streaming kernel. */
 FAGQ_API int fagq_diag_copy(const void* src, void* dst, int64_t bytes, void* stream);
 
+/* Issue-rate probe of the fp8 GEMM's matrix instruction: `blocks`
+ * workgroups of 4 waves (1 <= blocks <= 2^20), each wave issuing iters x 8
+ * v_mfma_scale_f32_16x16x128_f8f6f4 (1 <= iters <= 2^20) on register
+ * operands with no memory traffic, then writing one float per thread:
+ * `out` holds blocks x 256 floats.  One launch performs
+ * blocks x 4 x iters x 8 x 65536 flops, the ceiling the GEMM's measured
+ * rate is compared with. */
+FAGQ_API int fagq_diag_mfma_peak(float* out, int64_t blocks, int32_t iters, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

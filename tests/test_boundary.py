@@ -143,6 +143,11 @@ def test_diag_validation(lib):
     assert lib.fagq_diag_copy(fake(0), fake(1), 15, None) == 2
     assert lib.fagq_diag_copy(None, fake(1), 16, None) == 1
     assert lib.fagq_diag_copy(fake(0), fake(1), 0, None) == 0
+    assert lib.fagq_diag_mfma_peak(None, 1, 1, None) == 1
+    assert lib.fagq_diag_mfma_peak(fake(0), 0, 1, None) == 2
+    assert lib.fagq_diag_mfma_peak(fake(0), 1, 0, None) == 2
+    assert lib.fagq_diag_mfma_peak(fake(0), (1 << 20) + 1, 1, None) == 7
+    assert lib.fagq_diag_mfma_peak(ctypes.c_void_p(BASE + 2), 1, 1, None) == 4
 
 
 # ----------------------------------------------------------------- Python layer
