@@ -60,6 +60,7 @@ SIGNATURES = {
     "fagq_diag_mfma_peak": ([_P, _I64, _I, _P], _I),
     "fagq_dsa_topk_launch": ([_P, _I, _P, _P, _P, _I, _P, _P] + [_I64] * 6 + [_P], _I),
     "fagq_gemm_launch": ([_P] * 5 + [_I64, _I64, _I64, _I, _I, _I, _P], _I),
+    "fagq_gemm_launch_mapped": ([_P] * 5 + [_I64, _I64, _I64, _I, _I, _I, _I, _P], _I),
     "fagq_gemm_query_route": ([_I64, _I64, _I64, ctypes.POINTER(GemmRoute)], _I),
     "fagq_mla_bwd_workspace_bytes": ([_I64, _I64, _I64], _I64),
     "fagq_mla_bwd_launch": ([_P] * 8 + [_I64] * 5 + [_F, _I, _I, _P], _I),

@@ -7,15 +7,15 @@
 // src/task01_fused_add_rmsnorm_group_quant.py:1731-1851, stops at the
 // quantized tensor and scales); this is the layer those formats feed.
 //
-// Work mapping.  A workgroup computes a 256 x 256 tile of C: 8 waves of
-// 64 x 128 for every scale format, each wave a grid of 16 x 16 tiles, each
-// one v_mfma_scale_f32_16x16x128_f8f6f4 per 128-deep k-block.  The weight
-// tile is the MFMA's first operand and the activation
+// Work mapping.  A workgroup computes a 256 x BN tile of C (BN = 256, or 192
+// where that suits N): 8 waves of 64 x BN / 2 for every scale format, each
+// wave a grid of 16 x 16 tiles, each one v_mfma_scale_f32_16x16x128_f8f6f4
+// per 128-deep k-block.  The weight tile is the MFMA's first operand and the activation
 // tile its second, so each lane's four results are four consecutive columns
 // of one row of C (lane l: row l % 16, columns 4 (l / 16) .. +4) and the
 // activation scale a lane needs is that of its own row.
 //
-// Operand staging.  Per k-block, the 256 x 128-byte tiles of A and B go from
+// Operand staging.  Per k-block, the 256 x 128- and BN x 128-byte tiles of A and B go from
 // global memory straight into LDS (buffer_load_dwordx4 ... lds: each
 // instruction writes 1 KB, 16 bytes per lane, in lane order).  LDS holds
 // each 128-byte row with its eight 16-byte chunks XOR-swizzled: logical chunk
@@ -25,8 +25,9 @@
 // consecutive rows at one logical chunk: rows of equal parity then land in
 // distinct 16-byte slots of the 256-byte bank window (a swizzle by r % 8
 // maps rows r and r + 8 to the same banks, which measured as a 2-way
-// conflict on every read).  Two LDS stages (2 x 64 KB): the next k-block's
-// copies are issued before the current one is consumed.
+// conflict on every read).  Two LDS stages (2 x 64 KB, or 2 x 56 KB at
+// BN = 192): the next k-block's copies are issued before the current one is
+// consumed.
 //
 // Scales.  fp32 (or mixed) scales: each k-block's 16 x 16 x 128 product goes
 // to a temporary and is added to the accumulator as t * (sa * sb) with fmaf.
@@ -56,32 +57,42 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 constexpr int kBM = 256;                 // rows of C per workgroup
-constexpr int kBN = 256;                 // columns of C per workgroup
+constexpr int kMaxBN = 256;              // columns of C per workgroup, at most
 constexpr int kBK = 128;                 // k per block (one MFMA deep, one scale block)
-constexpr int kTileBytes = 256 * kBK;    // one operand tile in LDS
-constexpr int kStageBytes = 2 * kTileBytes;
-constexpr int kCopyInsts = kTileBytes / 1024;   // 1 KB copy instructions per operand tile
+constexpr int kATileBytes = kBM * kBK;   // the activation tile of one stage in LDS
 constexpr int kGroupM = 4;               // row tiles per group of the tile order
+constexpr int kCUs = 256;                // compute units of a gfx950 MI355X / MI350X
 
-// Wave layouts of the 256 x 256 tile.  WAVES_M x WAVES_N waves, each owning
-// TM x TN tiles of 16 x 16.  8 waves of 64 x 128 for every format: with two
-// waves per SIMD one wave's MFMAs cover the other's LDS reads.  (4 waves of
-// 128 x 128, accumulators in AGPRs, read a third less from LDS per MFMA but
-// measured 15 % slower with UE8M0 scales: one wave per SIMD leaves the
-// operand reads after each barrier exposed.)
-template <int WAVES_M_, int WAVES_N_>
+// Wave layouts of the 256 x BN tile.  WAVES_M x WAVES_N waves, each owning
+// TM x TN tiles of 16 x 16.  8 waves of 64 x (BN / 2) for every format: with
+// two waves per SIMD one wave's MFMAs cover the other's LDS reads.  (4 waves
+// of 128 x 128, accumulators in AGPRs, read a third less from LDS per MFMA
+// but measured 15 % slower with UE8M0 scales: one wave per SIMD leaves the
+// operand reads after each barrier exposed.)  BN is 256, or 192 where that
+// tiles N into fewer column-weighted rounds of the CUs (N = 2112: 11 tiles
+// of 192 against 9 of 256, the last a quarter full).  A wave's columns then
+// start at a multiple of 96 and may span two 128-column weight blocks.
+template <int BN_, int WAVES_M_, int WAVES_N_>
 struct Layout {
+  static constexpr int BN = BN_;
   static constexpr int WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
   static constexpr int WAVES = WAVES_M * WAVES_N;
   static constexpr int THREADS = 64 * WAVES;
   static constexpr int TM = kBM / 16 / WAVES_M;
-  static constexpr int TN = kBN / 16 / WAVES_N;
-  static constexpr int COPY_PER_WAVE = kCopyInsts / WAVES;
-  static_assert(16 * TN == 128, "a wave's columns must be one 128-column weight block");
-  static_assert(COPY_PER_WAVE % 2 == 0, "copy instructions alternate swizzle parity");
+  static constexpr int TN = BN / 16 / WAVES_N;
+  static constexpr int B_TILE_BYTES = BN * kBK;
+  static constexpr int STAGE_BYTES = kATileBytes + B_TILE_BYTES;
+  static constexpr int COPY_A = kATileBytes / 1024 / WAVES;    // 1 KB copy instructions per wave
+  static constexpr int COPY_B = B_TILE_BYTES / 1024 / WAVES;
+  // A wave's columns lie in one weight block unless they can straddle two.
+  static constexpr bool SPLIT = BN % 128 != 0 || (16 * TN) % 128 != 0;
+  static_assert(16 * TN <= 128, "a wave's columns touch at most two 128-column weight blocks");
+  static_assert(kATileBytes == COPY_A * 1024 * WAVES && B_TILE_BYTES == COPY_B * 1024 * WAVES,
+                "copy instructions cover each operand tile");
+  static_assert(BN <= kMaxBN, "tile width");
 };
-using LayoutF32 = Layout<4, 2>;
-using LayoutE8 = Layout<4, 2>;
+using Layout256 = Layout<256, 4, 2>;
+using Layout192 = Layout<192, 4, 2>;
 constexpr int kVmcnt0 = 0x0F70;          // s_waitcnt vmcnt(0) (other counters not waited)
 
 struct GArgs {
@@ -137,27 +148,27 @@ template <int ASF, int BSF, class L>
 __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g) {
   constexpr bool kHwScale = ASF == SF_UE8M0 && BSF == SF_UE8M0;
   constexpr int kTM = L::TM, kTN = L::TN;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStageBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * L::STAGE_BYTES];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave % L::WAVES_M, wn = wave / L::WAVES_M;
   int mt, nt;
   tile_coords((int)blockIdx.x, g.m_tiles, g.n_tiles, mt, nt);
-  const int m0 = mt * kBM, n0 = nt * kBN;
+  const int m0 = mt * kBM, n0 = nt * L::BN;
   const int mrows = g.M - m0 < kBM ? g.M - m0 : kBM;
-  const int nrows = g.N - n0 < kBN ? g.N - n0 : kBN;
+  const int nrows = g.N - n0 < L::BN ? g.N - n0 : L::BN;
   const rsrc_t ra = make_rsrc(g.a + (int64_t)m0 * g.K, (uint32_t)mrows * (uint32_t)g.K);
   const rsrc_t rb = make_rsrc(g.b + (int64_t)n0 * g.K, (uint32_t)nrows * (uint32_t)g.K);
   const rsrc_t ras = make_rsrc(g.as, g.as_bytes);
   const rsrc_t rbs = make_rsrc(g.bs, g.bs_bytes);
 
   // Copy geometry: instruction u of this wave is copy instruction i = wave *
-  // COPY_PER_WAVE + u of each operand tile and fills LDS rows 8 i .. +8; the
-  // lane's row within them is lane / 8, its position lane % 8, and it fetches
-  // the logical chunk stored there.  For row 8 i + lane / 8, (row / 2) % 8 =
-  // 4 (i % 2) + lane / 16, so even and odd instructions (i has the parity of
-  // u) need one lane offset each.
+  // COPY + u of an operand tile (COPY_A for the activation tile, COPY_B for
+  // the weight tile) and fills LDS rows 8 i .. +8; the lane's row within them
+  // is lane / 8, its position lane % 8, and it fetches the logical chunk
+  // stored there.  For row 8 i + lane / 8, (row / 2) % 8 = 4 (i % 2) +
+  // lane / 16, so even and odd instructions need one lane offset each.
   // The whole offset goes in the VGPR offset and the scalar offset is zero:
   // the hardware range-checks only the VGPR offset (plus the immediate), so
   // this is what turns rows past M or N into zero reads.  The lane part is
@@ -168,40 +179,55 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g)
       (uint32_t)crow * (uint32_t)g.K + (uint32_t)swz(lane & 7, crow + 8) * 16u};
 
   auto issue = [&](int kb, int stage) {
-    uint8_t* sa_tile = lds + stage * kStageBytes;
-    uint8_t* sb_tile = sa_tile + kTileBytes;
+    uint8_t* sa_tile = lds + stage * L::STAGE_BYTES;
+    uint8_t* sb_tile = sa_tile + kATileBytes;
+    constexpr int kCopies = L::COPY_A > L::COPY_B ? L::COPY_A : L::COPY_B;
 #pragma unroll
-    for (int u = 0; u < L::COPY_PER_WAVE; ++u) {
-      const int inst = wave * L::COPY_PER_WAVE + u;
-      const uint32_t off = cvoff[u & 1] +
-                           (uint32_t)__builtin_amdgcn_readfirstlane(inst * 8 * g.K + kb * kBK);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(sa_tile + inst * 1024), 16, off,
-                                               0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(sb_tile + inst * 1024), 16, off,
-                                               0, 0, 0);
+    for (int u = 0; u < kCopies; ++u) {   // the two tiles' copies interleaved
+      if (u < L::COPY_A) {
+        const int inst = wave * L::COPY_A + u;
+        const uint32_t off = cvoff[inst & 1] +
+                             (uint32_t)__builtin_amdgcn_readfirstlane(inst * 8 * g.K + kb * kBK);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(sa_tile + inst * 1024), 16, off,
+                                                 0, 0, 0);
+      }
+      if (u < L::COPY_B) {
+        const int inst = wave * L::COPY_B + u;
+        const uint32_t off = cvoff[inst & 1] +
+                             (uint32_t)__builtin_amdgcn_readfirstlane(inst * 8 * g.K + kb * kBK);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(sb_tile + inst * 1024), 16, off,
+                                                 0, 0, 0);
+      }
     }
   };
 
   // Scales of this lane's rows (m0 + 16 (TM wm + i) + lane % 16) and of the
-  // wave's 128-column weight block (n0 / 128 + wn) for k-block kb, as loaded
-  // bits: they are converted only after the barrier that ends the k-block,
-  // so no wait for them (and, the counter being in order, for the LDS copies
-  // issued before them) lands inside the MFMA loop.
+  // 128-column weight blocks of the wave's columns (block wblk for tiles
+  // j < jsplit, wblk + 1 for the rest) for k-block kb, as loaded bits: they
+  // are converted only after the barrier that ends the k-block, so no wait
+  // for them (and, the counter being in order, for the LDS copies issued
+  // before them) lands inside the MFMA loop.
   const int arow = m0 + wm * 16 * kTM + (lane & 15);
-  const int wblk = (n0 >> 7) + wn;
+  const int wcol = n0 + wn * 16 * kTN;             // the wave's first column
+  const int wblk = wcol >> 7;
+  const int jsplit = L::SPLIT ? (((wblk + 1) << 7) - wcol) >> 4 : kTN;
   struct Scales {
-    uint32_t a[kTM], b;
+    uint32_t a[kTM], b[L::SPLIT ? 2 : 1];
   };
   // Offsets as for the copies: all in the range-checked VGPR offset, so scale
   // reads for rows past M or weight blocks past N fall outside the arrays'
-  // descriptors and read zeros.
+  // descriptors and read zeros (those rows and columns are never stored).
   constexpr uint32_t asb = ASF == SF_F32 ? 4u : 1u, bsb = BSF == SF_F32 ? 4u : 1u;
   const uint32_t a_voff = (uint32_t)arow * (uint32_t)g.as_mstride * asb;   // lane part
   auto load_scales = [&](int kb) {
     Scales sc;
-    const uint32_t boff = (uint32_t)__builtin_amdgcn_readfirstlane((wblk * g.kblocks + kb) * (int)bsb);
-    sc.b = BSF == SF_F32 ? __builtin_amdgcn_raw_buffer_load_b32(rbs, boff, 0, 0)
-                         : (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rbs, boff, 0, 0);
+#pragma unroll
+    for (int h = 0; h < (L::SPLIT ? 2 : 1); ++h) {
+      const uint32_t boff =
+          (uint32_t)__builtin_amdgcn_readfirstlane(((wblk + h) * g.kblocks + kb) * (int)bsb);
+      sc.b[h] = BSF == SF_F32 ? __builtin_amdgcn_raw_buffer_load_b32(rbs, boff, 0, 0)
+                              : (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rbs, boff, 0, 0);
+    }
 #pragma unroll
     for (int i = 0; i < kTM; ++i) {
       const uint32_t off = a_voff + (uint32_t)__builtin_amdgcn_readfirstlane(
@@ -211,7 +237,9 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g)
     }
     return sc;
   };
-  auto to_f32 = [](uint32_t bits, bool e8m0) { return e8m0 ? e8m0_to_f32(bits) : __uint_as_float(bits); };
+  auto to_f32 = [](uint32_t bits, bool e8m0) {
+    return e8m0 ? e8m0_to_f32(bits) : __uint_as_float(bits);
+  };
 
   f32x4 acc[kTN][kTM];
 #pragma unroll
@@ -231,30 +259,37 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g)
       issue(kb + 1, stage ^ 1);
       nxt = load_scales(kb + 1);
     }
-    float smul[kTM];
+    constexpr int kNB = L::SPLIT ? 2 : 1;
+    float smul[kNB][kTM];
     if constexpr (!kHwScale) {
-      const float sb = to_f32(cur.b, BSF == SF_UE8M0);
 #pragma unroll
-      for (int i = 0; i < kTM; ++i) smul[i] = to_f32(cur.a[i], ASF == SF_UE8M0) * sb;
+      for (int h = 0; h < kNB; ++h) {
+        const float sb = to_f32(cur.b[h], BSF == SF_UE8M0);
+#pragma unroll
+        for (int i = 0; i < kTM; ++i) smul[h][i] = to_f32(cur.a[i], ASF == SF_UE8M0) * sb;
+      }
     }
-    const uint8_t* ta = lds + stage * kStageBytes;
-    const uint8_t* tb = ta + kTileBytes;
+    const uint8_t* ta = lds + stage * L::STAGE_BYTES;
+    const uint8_t* tb = ta + kATileBytes;
     i32x8 af[kTM];
 #pragma unroll
     for (int i = 0; i < kTM; ++i) af[i] = lds_frag(ta, wm * 16 * kTM + 16 * i + (lane & 15), lane);
 #pragma unroll
     for (int j = 0; j < kTN; ++j) {
-      const i32x8 bf = lds_frag(tb, wn * 128 + 16 * j + (lane & 15), lane);
+      const bool hi = L::SPLIT && j >= jsplit;   // weight block wblk + 1; uniform over the wave
+      const i32x8 bf = lds_frag(tb, wn * 16 * kTN + 16 * j + (lane & 15), lane);
 #pragma unroll
       for (int i = 0; i < kTM; ++i) {
         if constexpr (kHwScale) {
+          const int sbj = (int)(hi ? cur.b[kNB - 1] : cur.b[0]);
           acc[j][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-              bf, af[i], acc[j][i], 0, 0, 0, (int)cur.b, 0, (int)cur.a[i]);
+              bf, af[i], acc[j][i], 0, 0, 0, sbj, 0, (int)cur.a[i]);
         } else {
+          const float sm = hi ? smul[kNB - 1][i] : smul[0][i];
           const f32x4 t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
               bf, af[i], f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 127, 0, 127);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[j][i][r] = __builtin_fmaf(t[r], smul[i], acc[j][i][r]);
+          for (int r = 0; r < 4; ++r) acc[j][i][r] = __builtin_fmaf(t[r], sm, acc[j][i][r]);
         }
       }
     }
@@ -268,7 +303,7 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g)
   const rsrc_t rc = make_rsrc(g.c + (int64_t)m0 * g.N, (uint32_t)mrows * (uint32_t)g.N * 2u);
 #pragma unroll
   for (int j = 0; j < kTN; ++j) {
-    const int ncol = n0 + wn * 128 + 16 * j;
+    const int ncol = wcol + 16 * j;
     if (ncol >= g.N) continue;   // uniform over the wave
 #pragma unroll
     for (int i = 0; i < kTM; ++i) {
@@ -303,9 +338,9 @@ int validate(const void* a_q, const void* a_scale, const void* b_q, const void* 
   const int64_t asb = asf == FAGQ_SCALE_F32 ? 4 : 1, bsb = bsf == FAGQ_SCALE_F32 ? 4 : 1;
   // 32-bit buffer offsets: one workgroup's rows of A, B and C, and each scale array.
   if (M > INT32_MAX || (int64_t)kBM * K > (int64_t)UINT32_MAX ||
-      (int64_t)kBN * K > (int64_t)UINT32_MAX || (int64_t)kBM * N * 2 > (int64_t)UINT32_MAX ||
+      (int64_t)kMaxBN * K > (int64_t)UINT32_MAX || (int64_t)kBM * N * 2 > (int64_t)UINT32_MAX ||
       M * kb * asb > (int64_t)UINT32_MAX || ceil_div(N, 128) * kb * bsb > (int64_t)UINT32_MAX ||
-      ceil_div(M, kBM) * ceil_div(N, kBN) > INT32_MAX)
+      ceil_div(M, kBM) * ceil_div(N, Layout192::BN) > INT32_MAX)
     return FAGQ_E_TOO_LARGE;
   if (!aligned(a_q, 16) || !aligned(b_q, 16) || !aligned(c, 16) ||
       (asf == FAGQ_SCALE_F32 && !aligned(a_scale, 4)) ||
@@ -319,15 +354,56 @@ int validate(const void* a_q, const void* a_scale, const void* b_q, const void* 
   return FAGQ_OK;
 }
 
-// Kernel and workgroup size for a pair of scale formats.
-const void* kernel_for(int asf, int bsf, int* threads) {
+// Kernel for a pair of scale formats and a tile width.
+template <class L>
+const void* kernel_for_layout(int asf, int bsf) {
   const bool au = asf == FAGQ_SCALE_UE8M0, bu = bsf == FAGQ_SCALE_UE8M0;
-  *threads = au && bu ? LayoutE8::THREADS : LayoutF32::THREADS;
-  if (au && bu)
-    return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_UE8M0, SF_UE8M0, LayoutE8>);
-  if (au) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_UE8M0, SF_F32, LayoutF32>);
-  if (bu) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_F32, SF_UE8M0, LayoutF32>);
-  return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_F32, SF_F32, LayoutF32>);
+  if (au && bu) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_UE8M0, SF_UE8M0, L>);
+  if (au) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_UE8M0, SF_F32, L>);
+  if (bu) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_F32, SF_UE8M0, L>);
+  return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_F32, SF_F32, L>);
+}
+static_assert(Layout256::THREADS == Layout192::THREADS, "one workgroup size");
+
+// Tile width: 256 unless 192 takes fewer column-weighted rounds of the CUs
+// (one workgroup per CU at a time), cost(BN) = ceil(tiles(BN) / CUs) * BN;
+// ties keep 256.
+int pick_bn(int64_t M, int64_t N) {
+  auto cost = [&](int64_t bn) { return ceil_div(ceil_div(M, kBM) * ceil_div(N, bn), kCUs) * bn; };
+  return cost(Layout192::BN) < cost(Layout256::BN) ? Layout192::BN : Layout256::BN;
+}
+
+int launch(const void* a_q, const void* a_scale, const void* b_q, const void* b_scale, void* c,
+           int64_t M, int64_t N, int64_t K, int asf, int asl, int bsf, int bn, void* stream) {
+  const int v = validate(a_q, a_scale, b_q, b_scale, c, M, N, K, asf, asl, bsf);
+  if (v != FAGQ_OK || M == 0) return v;
+  const int dc = device_check();
+  if (dc != FAGQ_OK) return dc;
+  if (bn == 0) bn = pick_bn(M, N);
+  GArgs g;
+  g.a = static_cast<const uint8_t*>(a_q);
+  g.as = static_cast<const uint8_t*>(a_scale);
+  g.b = static_cast<const uint8_t*>(b_q);
+  g.bs = static_cast<const uint8_t*>(b_scale);
+  g.c = static_cast<uint16_t*>(c);
+  g.M = (int32_t)M;
+  g.N = (int32_t)N;
+  g.K = (int32_t)K;
+  g.kblocks = (int32_t)(K / kBK);
+  const bool col = asl == FAGQ_LAYOUT_COL_MAJOR;
+  g.as_kstride = col ? (int32_t)M : 1;
+  g.as_mstride = col ? 1 : g.kblocks;
+  g.m_tiles = (int32_t)ceil_div(M, kBM);
+  g.n_tiles = (int32_t)ceil_div(N, bn);
+  g.as_bytes = (uint32_t)(M * g.kblocks * (asf == FAGQ_SCALE_F32 ? 4 : 1));
+  g.bs_bytes = (uint32_t)(ceil_div(N, 128) * g.kblocks * (bsf == FAGQ_SCALE_F32 ? 4 : 1));
+  void* args[] = {&g};
+  const void* kernel = bn == Layout192::BN ? kernel_for_layout<Layout192>(asf, bsf)
+                                           : kernel_for_layout<Layout256>(asf, bsf);
+  const hipError_t e = hipLaunchKernel(kernel, dim3((unsigned)(g.m_tiles * g.n_tiles)),
+                                       dim3((unsigned)Layout256::THREADS), args, 0,
+                                       static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? FAGQ_OK : -(int)e;
 }
 
 // Issue-rate probe of the GEMM's instruction: every wave keeps 8 independent
@@ -369,45 +445,28 @@ FAGQ_API int fagq_gemm_launch(const void* a_q, const void* a_scale, const void* 
                               const void* b_scale, void* c, int64_t M, int64_t N, int64_t K,
                               int a_scale_format, int a_scale_layout, int b_scale_format,
                               void* stream) {
-  const int v = validate(a_q, a_scale, b_q, b_scale, c, M, N, K, a_scale_format, a_scale_layout,
-                         b_scale_format);
-  if (v != FAGQ_OK || M == 0) return v;
-  const int dc = device_check();
-  if (dc != FAGQ_OK) return dc;
-  GArgs g;
-  g.a = static_cast<const uint8_t*>(a_q);
-  g.as = static_cast<const uint8_t*>(a_scale);
-  g.b = static_cast<const uint8_t*>(b_q);
-  g.bs = static_cast<const uint8_t*>(b_scale);
-  g.c = static_cast<uint16_t*>(c);
-  g.M = (int32_t)M;
-  g.N = (int32_t)N;
-  g.K = (int32_t)K;
-  g.kblocks = (int32_t)(K / kBK);
-  const bool col = a_scale_layout == FAGQ_LAYOUT_COL_MAJOR;
-  g.as_kstride = col ? (int32_t)M : 1;
-  g.as_mstride = col ? 1 : g.kblocks;
-  g.m_tiles = (int32_t)ceil_div(M, kBM);
-  g.n_tiles = (int32_t)ceil_div(N, kBN);
-  g.as_bytes = (uint32_t)(M * g.kblocks * (a_scale_format == FAGQ_SCALE_F32 ? 4 : 1));
-  g.bs_bytes = (uint32_t)(ceil_div(N, 128) * g.kblocks * (b_scale_format == FAGQ_SCALE_F32 ? 4 : 1));
-  void* args[] = {&g};
-  int threads = 0;
-  const void* kernel = kernel_for(a_scale_format, b_scale_format, &threads);
-  const hipError_t e = hipLaunchKernel(kernel, dim3((unsigned)(g.m_tiles * g.n_tiles)),
-                                       dim3((unsigned)threads), args, 0,
-                                       static_cast<hipStream_t>(stream));
-  return e == hipSuccess ? FAGQ_OK : -(int)e;
+  return launch(a_q, a_scale, b_q, b_scale, c, M, N, K, a_scale_format, a_scale_layout,
+                b_scale_format, 0, stream);
+}
+
+FAGQ_API int fagq_gemm_launch_mapped(const void* a_q, const void* a_scale, const void* b_q,
+                                     const void* b_scale, void* c, int64_t M, int64_t N,
+                                     int64_t K, int a_scale_format, int a_scale_layout,
+                                     int b_scale_format, int block_n, void* stream) {
+  if (block_n != 0 && block_n != Layout192::BN && block_n != Layout256::BN) return FAGQ_E_FORMAT;
+  return launch(a_q, a_scale, b_q, b_scale, c, M, N, K, a_scale_format, a_scale_layout,
+                b_scale_format, block_n, stream);
 }
 
 FAGQ_API int fagq_gemm_query_route(int64_t M, int64_t N, int64_t K, fagq_gemm_route* route) {
   if (!route) return FAGQ_E_NULL;
   if (M < 0 || N <= 0 || K <= 0 || N % 16 != 0 || K % kBK != 0) return FAGQ_E_SHAPE;
+  const int bn = pick_bn(M, N);
   route->block_m = kBM;
-  route->block_n = kBN;
-  route->block_threads = LayoutF32::THREADS;   // LayoutE8::THREADS when both scales are UE8M0
+  route->block_n = bn;
+  route->block_threads = Layout256::THREADS;
   route->group_m = kGroupM;
-  route->grid_blocks = ceil_div(M, kBM) * ceil_div(N, kBN);
+  route->grid_blocks = ceil_div(M, kBM) * ceil_div(N, bn);
   return FAGQ_OK;
 }
 

@@ -35,6 +35,16 @@ FAGQ_API int fagq_launch_mapped(const void* x, const void* residual, const void*
                                 int rounding, int waves_per_row, int rows_per_block,
                                 int rows_in_sequence, int xcd_remap, void* stream);
 
+/* fagq_gemm_launch with the tile width forced: block_n 192 or 256 columns
+ * of C per workgroup (0: the shape's own choice, as fagq_gemm_launch).  Any
+ * width gives the same bits: each output takes the same MFMA and scale
+ * sequence.  Other arguments and rules as fagq_gemm_launch (fagq_gemm.h);
+ * FAGQ_E_FORMAT for another block_n. */
+FAGQ_API int fagq_gemm_launch_mapped(const void* a_q, const void* a_scale, const void* b_q,
+                                     const void* b_scale, void* c, int64_t M, int64_t N,
+                                     int64_t K, int a_scale_format, int a_scale_layout,
+                                     int b_scale_format, int block_n, void* stream);
+
 /* Encodes n fp32 values (n % 8 == 0, 16-byte aligned) with the operator's
  * device encoder, after a clamp to [-QMAX, QMAX] (which the operator itself
  * never needs: its values are within that range): one byte per value. */

@@ -237,9 +237,29 @@ def test_gemm_route(pkg):
     r = pkg.gemm_route(16384, 4096, 7168)
     assert (r["block_m"], r["block_n"], r["block_threads"]) == (256, 256, 512)
     assert r["grid_blocks"] == 64 * 16
-    assert pkg.gemm_route(1, 16, 128)["grid_blocks"] == 1
+    # N = 2112: 11 tiles of 192 columns (704 workgroups, 3 rounds of 256 CUs
+    # at 3/4 of the width) against 9 of 256 (576, 3 rounds at full width)
+    r = pkg.gemm_route(16384, 2112, 7168)
+    assert (r["block_n"], r["grid_blocks"]) == (192, 64 * 11)
+    # one round either way: the narrower tile
+    assert (pkg.gemm_route(1, 16, 128)["block_n"], pkg.gemm_route(1, 16, 128)["grid_blocks"]) == (192, 1)
+    # 6 rounds of 192 (22 tiles per row panel) against 4 of 256
+    assert pkg.gemm_route(16384, 4096, 128)["block_n"] == 256
     with pytest.raises(pkg.FagqError):
         pkg.gemm_route(16, 16, 100)
+
+
+def test_gemm_mapped_validation(lib):
+    def mapped(bn, **kw):
+        a = dict(a=fake(0), sa=fake(1), b=fake(2), sb=fake(3), c=fake(4), M=0, N=256, K=1024)
+        a.update(kw)
+        return lib.fagq_gemm_launch_mapped(a["a"], a["sa"], a["b"], a["sb"], a["c"], a["M"], a["N"],
+                                           a["K"], 0, 1, 0, bn, None)
+    for bn in (0, 192, 256):
+        assert mapped(bn) == 0                      # M = 0: validated, nothing launched
+    for bn in (-1, 128, 320):
+        assert mapped(bn) == 5
+    assert mapped(192, K=1000) == 2
 
 
 def test_gemm_workloads():

@@ -76,6 +76,36 @@ def test_gemm_formats(pkg, gpu, M, N, K, afmt, bfmt, col):
     assert_close(got, ref, bound, K, f"{M}x{N}x{K} {afmt}/{bfmt} col={col}")
 
 
+@pytest.mark.parametrize("afmt,bfmt,col", FORMATS)
+@pytest.mark.parametrize("M,N,K", [(300, 2112, 1024), (257, 400, 512), (513, 1536, 256),
+                                   (17, 16, 128)])
+def test_gemm_tile_widths_agree_bitwise(pkg, gpu, M, N, K, afmt, bfmt, col):
+    # 192- and 256-column tiles give the same bits (each output takes the same
+    # MFMA and scale sequence); with 192 a wave's 96 columns start at a
+    # multiple of 32 mod 128 and may straddle two weight blocks (N = 400,
+    # 1536, 2112 all have such waves).  The 192 result is also checked
+    # against the oracle.
+    import ctypes
+    note(f"gemm widths M={M} N={N} K={K} a={afmt} b={bfmt} col={col}")
+    a_q, a_s, b_q, b_s = make(M, N, K, afmt, bfmt, col, seed=M + N)
+    lib = pkg._lib.load()
+    d = [t.to(gpu).contiguous() for t in (a_q, a_s, b_q, b_s)]
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    outs = {}
+    for bn in (192, 256):
+        c = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu)
+        st = lib.fagq_gemm_launch_mapped(P(d[0]), P(d[1]), P(d[2]), P(d[3]), P(c), M, N, K,
+                                         0 if afmt == "f32" else 1, 1 if col else 0,
+                                         0 if bfmt == "f32" else 1, bn,
+                                         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert st == 0, st
+        torch.cuda.synchronize()
+        outs[bn] = c.cpu()
+    assert torch.equal(outs[192].view(torch.int16), outs[256].view(torch.int16))
+    ref, bound = run_ref(a_q, a_s, b_q, b_s, col)
+    assert_close(outs[192].float().numpy(), ref, bound, K, f"BN 192 M={M} N={N}")
+
+
 @pytest.mark.parametrize("M", [1, 3, 255, 257, 513])
 @pytest.mark.parametrize("N", [16, 144, 400])
 def test_gemm_ragged_shapes(pkg, gpu, M, N):
