@@ -20,10 +20,10 @@
 //   K2 mla_exact_rows_block_total - one launch of 1024-thread workgroups, two
 //                        kinds:
 //                        * exact rows, one per (b, h): q, do and c rows 0..E-1
-//                          in LDS, the logits and dP by fp32 dot products (4
-//                          lanes per (query, key) pair), P and dS rounded to
-//                          bf16 where the reference rounds, dq rows 0..E-1
-//                          (which K1 does not write);
+//                          in LDS, the logits and dP by bf16 MFMAs with fp32
+//                          accumulation (one wave), P and dS rounded to bf16
+//                          where the reference rounds, dq rows 0..E-1 (which
+//                          K1 does not write);
 //                        * block totals, per block of 16-64 rows: fp32 totals
 //                          of hs / (i + 1) over rows and head-group planes;
 //                          each row's plane sum is written back over plane 0.
@@ -50,6 +50,8 @@ constexpr int kThreads = 256;
 constexpr int kE = FAGQ_MLA_EXACT_ROWS;
 constexpr int kMaxD = FAGQ_MLA_MAX_D;
 constexpr int kPadElems = 8;             // LDS row padding (bf16 elements), exact rows
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 struct MArgs {
   const uint16_t* q;
@@ -195,13 +197,13 @@ __global__ void __launch_bounds__(kThreads) mla_stream_do(const MArgs g) {
 
 constexpr int kWide = 1024;               // threads of K2 and K3 (16 waves)
 
-// Exact rows 0..E-1 of (b, h), wave m owning query row m.  Lane 4 n + k
-// computes quarter k of the dims of the dot products with key n (n <= m), the
-// quarters joined by two DPP steps.  Every global load is issued before the
-// first LDS store: wave m loads chunk `lane` (16 bytes) of its q, do and out
-// rows, and thread t chunk t of c rows 0..E-1 (16 D / 8 <= 1024 chunks).
-// Buffer descriptors over rows 0..E-1 return zeros for the rest.  Dynamic
-// LDS: q, do and c rows 0..15 (padded by 16 bytes), then dS [16][16].
+// Exact rows 0..E-1 of (b, h), wave m owning query row m for delta and dq;
+// wave 0 computes all 16 x 16 logits and dP with MFMAs.  Every global load
+// is issued before the first LDS store: wave m loads chunk `lane` (16 bytes)
+// of its q, do and out rows, and thread t chunk t of c rows 0..E-1
+// (16 D / 8 <= 1024 chunks).  Buffer descriptors over rows 0..E-1 return
+// zeros for the rest.  Dynamic LDS: q, do and c rows 0..15 (padded by 16
+// bytes), then dS [16][16] and delta [16].
 __device__ __forceinline__ void exact_rows(const MArgs& g, int b, int h) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int D = g.D, E = g.erows;
@@ -238,42 +240,44 @@ __device__ __forceinline__ void exact_rows(const MArgs& g, int b, int h) {
   }
 #pragma unroll
   for (int s = 32; s > 0; s >>= 1) delta += __shfl_xor(delta, s, 64);
+  float* deltas = dS + kE * kE;                   // [kE], after dS
+  if (lane == 0) deltas[m] = delta;
   __syncthreads();
 
-  // Logits and dP of (m, n = lane / 4), dims quarter lane % 4.
-  const int n = lane >> 2, qtr = lane & 3;
-  float logit = 0.0f, dp = 0.0f;
-  if (m < E && n <= m) {
-    const int kq = D / 4;
-    const uint16_t* qr = qs + m * ld + qtr * kq;
-    const uint16_t* dr = dos + m * ld + qtr * kq;
-    const uint16_t* cr = cs + n * ld + qtr * kq;
-#pragma unroll 4
-    for (int k = 0; k < kq; k += 8) {
-      const u32x4 x = *reinterpret_cast<const u32x4*>(qr + k);
-      const u32x4 y = *reinterpret_cast<const u32x4*>(dr + k);
-      const u32x4 c = *reinterpret_cast<const u32x4*>(cr + k);
+  // Logits and dP of query row qm = lane % 16 with keys n = 4 (lane / 16) +
+  // r (r < 4), by wave 0 alone: v_mfma_f32_16x16x32_bf16 with A = c rows
+  // (key), B = q or dO rows (query), K = D in steps of 32.  Lane l supplies
+  // row l % 16 of both operands, 8 consecutive dims (the same ones for both)
+  // per step, and receives D[4 (l / 16) + r][l % 16] (checked on the GPU).
+  // Rows past E were staged as zeros.
+  if (m == 0) {
+    const int qm = lane & 15, k0 = (lane >> 4) * 8;
+    const uint16_t* cr = cs + qm * ld + k0;
+    const uint16_t* qr = qs + qm * ld + k0;
+    const uint16_t* dr = dos + qm * ld + k0;
+    f32x4 lg = {0.0f, 0.0f, 0.0f, 0.0f}, dpv = lg;
+    auto ld8 = [](const uint16_t* p) { return *reinterpret_cast<const bf16x8*>(p); };
+#pragma unroll 2
+    for (int k = 0; k < D; k += 64) {             // D % 64 == 0: two steps per pass
+      const bf16x8 c0 = ld8(cr + k), q0 = ld8(qr + k), d0 = ld8(dr + k);
+      const bf16x8 c1 = ld8(cr + k + 32), q1 = ld8(qr + k + 32), d1 = ld8(dr + k + 32);
+      lg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c0, q0, lg, 0, 0, 0);
+      dpv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c0, d0, dpv, 0, 0, 0);
+      lg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c1, q1, lg, 0, 0, 0);
+      dpv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c1, d1, dpv, 0, 0, 0);
+    }
+    const float lse = qm < E ? g.lse[(int64_t)bh * g.S + qm] : 0.0f;
+    const float dlt = deltas[qm];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        logit = fmaf(bf16_lo(x[j]), bf16_lo(c[j]), logit);
-        logit = fmaf(bf16_hi(x[j]), bf16_hi(c[j]), logit);
-        dp = fmaf(bf16_lo(y[j]), bf16_lo(c[j]), dp);
-        dp = fmaf(bf16_hi(y[j]), bf16_hi(c[j]), dp);
+    for (int r = 0; r < 4; ++r) {
+      const int kn = 4 * (lane >> 4) + r;
+      float sv = 0.0f;
+      if (qm < E && kn <= qm) {
+        const float p = round_bf16(exp2f((lg[r] * g.scale - lse) * 1.4426950408889634f));
+        sv = round_bf16(p * (dpv[r] - dlt) * g.scale);
       }
+      dS[qm * kE + kn] = sv;
     }
-  }
-  logit += __uint_as_float(dpp_u32<0xB1>(__float_as_uint(logit)));   // quad xor 1
-  logit += __uint_as_float(dpp_u32<0x4E>(__float_as_uint(logit)));   // quad xor 2
-  dp += __uint_as_float(dpp_u32<0xB1>(__float_as_uint(dp)));
-  dp += __uint_as_float(dpp_u32<0x4E>(__float_as_uint(dp)));
-  if (qtr == 0) {
-    float sv = 0.0f;
-    if (m < E && n <= m) {
-      const float lse = g.lse[(int64_t)bh * g.S + m];
-      const float p = round_bf16(exp2f((logit * g.scale - lse) * 1.4426950408889634f));
-      sv = round_bf16(p * (dp - delta) * g.scale);
-    }
-    dS[m * kE + n] = sv;
   }
   __syncthreads();
 
@@ -300,7 +304,7 @@ __device__ __forceinline__ void exact_rows(const MArgs& g, int b, int h) {
 // Dynamic LDS of K2: the exact rows' rows and dS, at least kWide float4 for
 // the block totals' join.
 size_t k2_lds_bytes(int64_t D) {
-  const size_t ex = (size_t)3 * kE * (D + kPadElems) * 2 + (size_t)kE * kE * 4;
+  const size_t ex = (size_t)3 * kE * (D + kPadElems) * 2 + (size_t)(kE * kE + kE) * 4;
   const size_t bt = (size_t)kWide * 16;
   return ex > bt ? ex : bt;
 }
