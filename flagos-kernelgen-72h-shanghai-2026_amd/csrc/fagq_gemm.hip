@@ -178,6 +178,12 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g)
       (uint32_t)crow * (uint32_t)g.K + (uint32_t)swz(lane & 7, crow) * 16u,
       (uint32_t)crow * (uint32_t)g.K + (uint32_t)swz(lane & 7, crow + 8) * 16u};
 
+  // Uniform part of copy instruction inst's offset for k-block kb.  Offsets
+  // are computed in uint32: the launch checks that every one fits.
+  auto copy_off = [&](int inst, int kb) {
+    return (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)((uint32_t)inst * 8u * (uint32_t)g.K + (uint32_t)kb * (uint32_t)kBK));
+  };
   auto issue = [&](int kb, int stage) {
     uint8_t* sa_tile = lds + stage * L::STAGE_BYTES;
     uint8_t* sb_tile = sa_tile + kATileBytes;
@@ -186,15 +192,13 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g)
     for (int u = 0; u < kCopies; ++u) {   // the two tiles' copies interleaved
       if (u < L::COPY_A) {
         const int inst = wave * L::COPY_A + u;
-        const uint32_t off = cvoff[inst & 1] +
-                             (uint32_t)__builtin_amdgcn_readfirstlane(inst * 8 * g.K + kb * kBK);
+        const uint32_t off = cvoff[inst & 1] + copy_off(inst, kb);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(sa_tile + inst * 1024), 16, off,
                                                  0, 0, 0);
       }
       if (u < L::COPY_B) {
         const int inst = wave * L::COPY_B + u;
-        const uint32_t off = cvoff[inst & 1] +
-                             (uint32_t)__builtin_amdgcn_readfirstlane(inst * 8 * g.K + kb * kBK);
+        const uint32_t off = cvoff[inst & 1] + copy_off(inst, kb);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(sb_tile + inst * 1024), 16, off,
                                                  0, 0, 0);
       }
@@ -223,15 +227,16 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g)
     Scales sc;
 #pragma unroll
     for (int h = 0; h < (L::SPLIT ? 2 : 1); ++h) {
-      const uint32_t boff =
-          (uint32_t)__builtin_amdgcn_readfirstlane(((wblk + h) * g.kblocks + kb) * (int)bsb);
+      const uint32_t boff = (uint32_t)__builtin_amdgcn_readfirstlane(
+          (int)(((uint32_t)(wblk + h) * (uint32_t)g.kblocks + (uint32_t)kb) * bsb));
       sc.b[h] = BSF == SF_F32 ? __builtin_amdgcn_raw_buffer_load_b32(rbs, boff, 0, 0)
                               : (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rbs, boff, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < kTM; ++i) {
-      const uint32_t off = a_voff + (uint32_t)__builtin_amdgcn_readfirstlane(
-                                        (kb * g.as_kstride + 16 * i * g.as_mstride) * (int)asb);
+      const uint32_t e = (uint32_t)kb * (uint32_t)g.as_kstride +
+                         16u * (uint32_t)i * (uint32_t)g.as_mstride;
+      const uint32_t off = a_voff + (uint32_t)__builtin_amdgcn_readfirstlane((int)(e * asb));
       sc.a[i] = ASF == SF_F32 ? __builtin_amdgcn_raw_buffer_load_b32(ras, off, 0, 0)
                               : (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(ras, off, 0, 0);
     }
