@@ -8,18 +8,20 @@ steps are timed between device synchronisations, rotating over enough
 input/output sets that no step reads data left in L2/MALL by the previous
 one.
 
-Prints one JSON line:
-  value       whole-job achieved bandwidth: algorithmic bytes / (wall time of K
-              steps between device synchronisations / K)
-  roofline    the kernel's algorithmic bytes / its average duration (HIP events
-              recorded on the launch stream around each of K more launches), vs
-              8 TB/s; traffic = measured HBM bytes per launch from the committed
-              rocprofv3 counter summary for this workload (null if none)
+Prints one JSON line.  One timing underlies value, ms_per_step, pct_of_peak
+and roofline: one HIP event pair recorded on the launch stream around the K
+timed back-to-back steps (the host clock over the same region is reported as
+us_per_call_host_wall).
+  value       whole-job achieved bandwidth: algorithmic bytes / (event time / K)
+  roofline    the same figure against 8 TB/s; traffic = measured HBM bytes per
+              launch from the committed rocprofv3 counter summary for this
+              workload (null if none)
   us_per_call_graph_replay  device time per call of consecutive launches
               captured in a HIP graph (workloads under 64 MB only)
   cpu_baseline  the eager-PyTorch CPU restatement timed on a bounded row sample
-              of the same workload on the host cores (and checked against the
-              GPU's rows)
+              of the same workload on this host's CPU share (and checked against
+              the GPU's rows); cpu_baseline_config1 = BASELINE config 1
+              (128 x 4096) in full, with the GPU's output checked against it
 
 --config tp*_shard_*: the multi-input form (fagq_launch_parts) at one rank's
 shard of a tensor-parallel layer: nparts partial sums reduced, normalized and
@@ -34,9 +36,10 @@ output (fagq_gemm_launch); value and roofline in TFLOP/s against MI355X's
 5.0 PFLOP/s dense fp8 peak, cpu_baseline = the C oracle (oracle/gemm_oracle.c)
 on a row sample.
 
---copy BYTES and --mfma-peak time the library's two ceiling probes instead: a
-plain 16-byte copy kernel (achievable HBM bandwidth, counter calibration) and
-the GEMM's matrix instruction issued from registers (achievable MFMA rate).
+--copy BYTES and --mfma-peak time the library's ceiling probes instead: HBM
+copy, read-only and write-only streams with the operator's cache policies
+(achievable bandwidth, counter calibration), and the GEMM's matrix instruction
+issued from registers (achievable MFMA rate).
 
 Usage: python bench.py [--steps K] [--warmup W] [--config NAME] [--gpus 1]
 """
@@ -70,6 +73,57 @@ def measured_traffic(name: str):
         return None
 
 
+def timed_region(torch, dev, stream, step, steps: int):
+    """The timed region: K steps between device synchronisations, bracketed by one
+    HIP event pair recorded on the launch stream and by the host clock.  Returns
+    (device ms per step from the events, host wall ms per step).  Nothing but the
+    launches runs between the events, so back-to-back kernels are measured as the
+    stream executes them."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize(dev)
+    t1 = time.perf_counter()
+    return e0.elapsed_time(e1) / steps, (t1 - t0) * 1e3 / steps
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads() -> int:
+    """Threads for the CPU baseline: the CPUs this process may run on, capped by
+    OMP_NUM_THREADS when it is set (a GPU box gives each GPU's jobs a 16-CPU share and
+    sets OMP_NUM_THREADS to it; nproc there counts the whole host)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    if cap.isdigit() and int(cap) > 0:
+        n = min(n, int(cap))
+    return max(1, n)
+
+
+def host_info(threads: int) -> dict:
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        aff = None
+    return {"cpu_model": cpu_model(), "nproc": os.cpu_count(), "affinity_cpus": aff,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"), "threads_used": threads}
+
+
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
@@ -80,8 +134,8 @@ def parse_args():
                    help="target CPU time of the cpu_baseline leg (0 disables it)")
     p.add_argument("--cpu-rows", type=int, default=512, help="rows in the cpu_baseline sample")
     p.add_argument("--copy", type=int, default=0, metavar="BYTES",
-                   help="instead: time the library's plain 16-byte copy kernel over BYTES "
-                        "(reference for achievable bandwidth and HBM counter calibration)")
+                   help="instead: time the library's HBM copy / read / write probes over BYTES "
+                        "(achievable bandwidth, HBM counter calibration)")
     p.add_argument("--mfma-peak", action="store_true",
                    help="instead: time the library's register-only issue-rate probe of the fp8 "
                         "GEMM's matrix instruction (the compute ceiling its rate is compared with)")
@@ -89,8 +143,12 @@ def parse_args():
 
 
 def copy_bench(args, torch, pkg) -> int:
-    """Times fagq_diag_copy (read BYTES + write BYTES per launch)."""
+    """Times the library's HBM ceiling probes (fagq_diag_stream) over BYTES, with the
+    operator's cache policies: copy (BYTES read + BYTES written), read-only and
+    write-only, buffer sets rotated past the MALL, one event pair around the K
+    launches of each.  One JSON line per probe."""
     import ctypes
+    from fagq_mi355x import _lib
     dev = torch.device("cuda:0")
     lib = pkg.load_library()
     n = args.copy // 16 * 16
@@ -99,26 +157,22 @@ def copy_bench(args, torch, pkg) -> int:
              torch.empty(n, dtype=torch.uint8, device=dev)) for _ in range(nsets)]
     stream = torch.cuda.current_stream(dev)
     sp = ctypes.c_void_p(stream.cuda_stream)
+    for mode, name, moved in ((_lib.STREAM_COPY, "copy", 2 * n), (_lib.STREAM_READ, "read", n),
+                              (_lib.STREAM_WRITE, "write", n)):
+        def step(i, mode=mode):
+            s, d = bufs[i % nsets]
+            pkg._lib.check(lib.fagq_diag_stream(ctypes.c_void_p(s.data_ptr()),
+                                                ctypes.c_void_p(d.data_ptr()), n, mode, sp),
+                           "fagq_diag_stream")
 
-    def step(i):
-        s, d = bufs[i % nsets]
-        pkg._lib.check(lib.fagq_diag_copy(ctypes.c_void_p(s.data_ptr()),
-                                          ctypes.c_void_p(d.data_ptr()), n, sp), "fagq_diag_copy")
-
-    for i in range(args.warmup):
-        step(i)
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    torch.cuda.synchronize(dev)
-    for i in range(args.steps):
-        starts[i].record(stream)
-        step(i)
-        ends[i].record(stream)
-    torch.cuda.synchronize(dev)
-    ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / args.steps
-    print(json.dumps({"copy_bytes": n, "us_per_call": round(ms * 1e3, 2),
-                      "GBps_read_plus_write": round(2 * n / (ms * 1e-3) / 1e9, 1),
-                      "buffer_sets": nsets}), flush=True)
+        for i in range(args.warmup):
+            step(i)
+        ms, _ = timed_region(torch, dev, stream, step, args.steps)
+        print(json.dumps({"probe": name, "bytes_per_launch": moved, "buffer_bytes": n,
+                          "us_per_call": round(ms * 1e3, 2),
+                          "GBps": round(moved / (ms * 1e-3) / 1e9, 1),
+                          "frac_of_8000": round(moved / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                          "buffer_sets": nsets, "steps": args.steps}), flush=True)
     return 0
 
 
@@ -217,27 +271,9 @@ def main() -> int:
     torch.cuda.synchronize(dev)
     stream = torch.cuda.current_stream(dev)
 
-    # Timed region: K steps between device synchronisations (no events inside,
-    # so nothing but the launches themselves runs between the kernels).
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i)
-    torch.cuda.synchronize(dev)
-    t1 = time.perf_counter()
-    wall_ms = (t1 - t0) * 1e3 / args.steps
-
-    # Kernel duration: the same K steps again, each bracketed by HIP events
-    # recorded on the stream the kernel is launched on.
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    for i in range(args.steps):
-        starts[i].record(stream)
-        step(i)
-        ends[i].record(stream)
-    torch.cuda.synchronize(dev)
-    durs = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
-    kern_ms = sum(durs) / len(durs)
-    med_ms = durs[len(durs) // 2]
+    # Timed region: K back-to-back steps; device time from one HIP event pair on the
+    # launch stream, host wall time over the same region.
+    kern_ms, wall_ms = timed_region(torch, dev, stream, step, args.steps)
 
     # Device time per call without host launch gaps: a HIP graph of
     # consecutive launches, replayed (matters when a call is shorter than its
@@ -267,12 +303,12 @@ def main() -> int:
         torch.cuda.synchronize(dev)
         graph_us = ge0.elapsed_time(ge1) * 1e3 / (reps * per_graph)
 
-    value = set_bytes / (wall_ms * 1e-3) / 1e9
-    achieved = set_bytes / (kern_ms * 1e-3) / 1e9
+    value = set_bytes / (kern_ms * 1e-3) / 1e9
 
     traffic = measured_traffic(name)
 
-    route = pkg.route_for(w.M, w.D, w.group_size)
+    route = pkg.route_for(w.M, w.D, w.group_size, scale_ue8m0=w.scale_ue8m0,
+                          scale_col_major=w.scale_col_major)
     out = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -280,12 +316,14 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(wall_ms, 5),
+        "ms_per_step": round(kern_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
+        "timing": "value, ms_per_step, pct_of_peak and roofline.achieved all come from one "
+                  "HIP event pair on the launch stream around the K timed steps",
         "config": {"workload": name, "M": w.M, "D": w.D, "group_size": w.group_size,
                    "q": str(w.out_dtype).replace("torch.", ""),
                    "scale": ("ue8m0" if w.scale_ue8m0 else "f32") +
@@ -293,53 +331,45 @@ def main() -> int:
                    "inputs": w.dist, "algorithmic_bytes": set_bytes, "buffer_sets": nsets,
                    "route": route},
         "us_per_call": round(kern_ms * 1e3, 2),
-        "us_per_call_median": round(med_ms * 1e3, 2),
         "us_per_call_host_wall": round(wall_ms * 1e3, 2),
         "us_per_call_graph_replay": None if graph_us is None else round(graph_us, 2),
-        "pct_of_peak": round(100.0 * achieved / PEAK_HBM_GBS, 2),
+        "pct_of_peak": round(100.0 * value / PEAK_HBM_GBS, 2),
         "rows_per_s": round(w.M / (kern_ms * 1e-3), 1),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(value / PEAK_HBM_GBS, 4),
                      "traffic": traffic},
         "cpu_baseline": None,
     }
 
     if args.cpu_seconds > 0:
         out["cpu_baseline"] = cpu_baseline(w, x, res, gamma, sets[0], args, torch)
+        if name != CPU_CONFIG:
+            out["cpu_baseline_config1"] = cpu_config1(pkg, dev, args, torch)
     print(json.dumps(out), flush=True)
     return 0
 
 
-def cpu_baseline(w, x, res, gamma, gpu_set, args, torch) -> dict:
-    """Times the eager-PyTorch CPU restatement (oracle/torch_eager.py) on the
-    first rows of the same workload, and checks those rows of the GPU's
-    output against it."""
-    import numpy as np
-    from oracle.compare import compare
-    from oracle.torch_eager import fagq_torch
+CPU_CONFIG = "cpu_ref_128x4096"   # the CPU PyTorch reference path
 
-    threads = max(1, min(16, os.cpu_count() or 1))
-    torch.set_num_threads(threads)
-    rows = max(1, min(args.cpu_rows, w.M))
-    xs, rs = x[:rows].contiguous(), res[:rows].contiguous()
 
-    def run():
-        return fagq_torch(xs, rs, gamma, w.eps, w.group_size, w.out_dtype, w.scale_ue8m0,
-                          w.scale_col_major, w.rounding)
-
-    ref = run()    # warm-up
+def _time_cpu(run, min_runs: int, seconds: float, max_runs: int = 1000):
+    """Median seconds per call over at least min_runs calls (after 2 warm-ups),
+    continuing for up to `seconds`."""
+    run()
     run()
     times = []
     t_start = time.perf_counter()
-    while len(times) < 3 or (time.perf_counter() - t_start < args.cpu_seconds and len(times) < 1000):
+    while len(times) < min_runs or (time.perf_counter() - t_start < seconds and len(times) < max_runs):
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
     times.sort()
-    t = times[len(times) // 2]
-    nbytes = w.algorithmic_bytes() * rows // w.M
+    return times[len(times) // 2], len(times)
 
-    # Parity of the GPU rows against the CPU path (step 0 wrote set 0).
+
+def _gpu_rows_parity(w, gpu_set, ref, rows, torch):
+    import numpy as np
+    from oracle.compare import compare
     _, _, ro, q, sc = gpu_set
     torch.cuda.synchronize()
     scale_rows = sc[:rows]
@@ -351,14 +381,67 @@ def cpu_baseline(w, x, res, gamma, gpu_set, args, torch) -> dict:
             "q": ref[1].view(torch.uint8).numpy(), "scale": ref[2].numpy()}
     try:
         st = compare(gpu, refd, fp8=w.out_dtype == torch.float8_e4m3fn, ue8m0=w.scale_ue8m0)
-        parity = {"ok": True, "exact": st["exact"], "q_mismatch": st["q_mismatch"]}
+        return {"ok": True, "exact": st["exact"], "q_mismatch": st["q_mismatch"]}
     except AssertionError as e:
-        parity = {"ok": False, "error": str(e)[:200]}
+        return {"ok": False, "error": str(e)[:200]}
+
+
+def cpu_baseline(w, x, res, gamma, gpu_set, args, torch) -> dict:
+    """Times the eager-PyTorch CPU restatement (oracle/torch_eager.py) on the
+    first rows of the same workload, on this host's CPU share, and checks those
+    rows of the GPU's output against it."""
+    from oracle.torch_eager import fagq_torch
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    rows = max(1, min(args.cpu_rows, w.M))
+    xs, rs = x[:rows].contiguous(), res[:rows].contiguous()
+
+    def run():
+        return fagq_torch(xs, rs, gamma, w.eps, w.group_size, w.out_dtype, w.scale_ue8m0,
+                          w.scale_col_major, w.rounding)
+
+    ref = run()
+    t, n = _time_cpu(run, 3, args.cpu_seconds)
+    nbytes = w.algorithmic_bytes() * rows // w.M
     return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port", "us_per_call": round(t * 1e6, 1),
             "sample": f"first {rows} of {w.M} rows of {w.name}, eager PyTorch CPU "
-                      f"restatement (oracle/torch_eager.py), median of {len(times)} runs",
-            "parity_vs_gpu_rows": parity}
+                      f"restatement (oracle/torch_eager.py), {threads} threads, median of {n} runs",
+            "host": host_info(threads),
+            "parity_vs_gpu_rows": _gpu_rows_parity(w, gpu_set, ref, rows, torch)}
+
+
+def cpu_config1(pkg, dev, args, torch) -> dict:
+    """BASELINE config 1 in full (128 x 4096 -> fp8, fp32 row-major scales): the
+    eager-PyTorch CPU path timed on this host's CPU share (median of >= 10 runs
+    after 2 warm-ups), and the GPU operator's output on the same inputs checked
+    against it."""
+    from fagq_mi355x.workloads import CONFIGS, make_inputs
+    from oracle.torch_eager import fagq_torch
+    w = CONFIGS[CPU_CONFIG]
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    x, res, gamma = make_inputs(w)
+
+    def run():
+        return fagq_torch(x, res, gamma, w.eps, w.group_size, w.out_dtype, w.scale_ue8m0,
+                          w.scale_col_major, w.rounding)
+
+    ref = run()
+    t, n = _time_cpu(run, 10, min(args.cpu_seconds, 5.0))
+    xd, rd, gd = x.to(dev), res.to(dev), gamma.to(dev)
+    ro = torch.empty_like(rd)
+    q = torch.empty((w.M, w.D), dtype=w.out_dtype, device=dev)
+    sc = pkg.empty_scales(w.M, w.groups, device=dev)
+    pkg.fused_add_rmsnorm_group_quant(xd, rd, gd, ro, None, q, sc, w.eps, w.group_size)
+    nbytes = w.algorithmic_bytes()
+    return {"workload": w.name, "value": round(nbytes / t / 1e9, 3), "unit": "GB/s",
+            "us_per_call": round(t * 1e6, 1), "cores": threads, "kind": "port",
+            "sample": f"all {w.M} rows, eager PyTorch CPU restatement (oracle/torch_eager.py), "
+                      f"{threads} threads, median of {n} runs",
+            "host": host_info(threads),
+            "parity_vs_gpu": _gpu_rows_parity(w, (xd, rd, ro, q, sc), ref, w.M, torch)}
 
 
 def parts_bench(args, torch, pkg, w) -> int:
@@ -400,23 +483,9 @@ def parts_bench(args, torch, pkg, w) -> int:
 
     for i in range(args.warmup):
         step(i)
-    torch.cuda.synchronize(dev)
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i)
-    torch.cuda.synchronize(dev)
-    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    for i in range(args.steps):
-        starts[i].record(stream)
-        step(i)
-        ends[i].record(stream)
-    torch.cuda.synchronize(dev)
-    durs = sorted(st.elapsed_time(en) for st, en in zip(starts, ends))
-    kern_ms = sum(durs) / len(durs)
-    value = set_bytes / (wall_ms * 1e-3) / 1e9
-    achieved = set_bytes / (kern_ms * 1e-3) / 1e9
+    kern_ms, wall_ms = timed_region(torch, dev, stream, step, args.steps)
+    value = set_bytes / (kern_ms * 1e-3) / 1e9
+    achieved = value
     out = {
         "metric": "achieved HBM GB/s (% of 8 TB/s), multi-input form at one rank's shard",
         "value": round(value, 1),
@@ -424,7 +493,7 @@ def parts_bench(args, torch, pkg, w) -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(wall_ms, 5),
+        "ms_per_step": round(kern_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -434,7 +503,6 @@ def parts_bench(args, torch, pkg, w) -> int:
                    "group_size": w.group_size, "q": "float8_e4m3fn", "scale": "f32 col-major",
                    "algorithmic_bytes": set_bytes, "buffer_sets": nsets},
         "us_per_call": round(kern_ms * 1e3, 2),
-        "us_per_call_median": round(durs[len(durs) // 2] * 1e3, 2),
         "us_per_call_host_wall": round(wall_ms * 1e3, 2),
         "pct_of_peak": round(100.0 * achieved / PEAK_HBM_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
@@ -454,7 +522,7 @@ def parts_cpu_baseline(w, parts, res, gamma, gpu_set, args, torch) -> dict:
     import numpy as np
     import oracle
     from oracle.compare import compare
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = cpu_threads()
     rows = max(1, min(args.cpu_rows, w.M))
     u16 = lambda t: t[:rows].contiguous().view(torch.uint16).numpy()
     pr = [u16(p) for p in parts]
@@ -524,23 +592,9 @@ def dsa_bench(args, torch, pkg, w) -> int:
 
     for i in range(args.warmup):
         step(i)
-    torch.cuda.synchronize(dev)
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i)
-    torch.cuda.synchronize(dev)
-    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    for i in range(args.steps):
-        starts[i].record(stream)
-        step(i)
-        ends[i].record(stream)
-    torch.cuda.synchronize(dev)
-    durs = sorted(a.elapsed_time(b) for a, b in zip(starts, ends))
-    kern_ms = sum(durs) / len(durs)
-    value = nbytes / (wall_ms * 1e-3) / 1e9
-    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    kern_ms, wall_ms = timed_region(torch, dev, stream, step, args.steps)
+    value = nbytes / (kern_ms * 1e-3) / 1e9
+    achieved = value
     out = {
         "metric": "DSA top-k page-table transform: algorithmic GB/s (% of 8 TB/s) + us/call",
         "value": round(value, 1),
@@ -548,7 +602,7 @@ def dsa_bench(args, torch, pkg, w) -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(wall_ms, 5),
+        "ms_per_step": round(kern_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -558,7 +612,6 @@ def dsa_bench(args, torch, pkg, w) -> int:
                    "top_k": w.top_k, "block_size": w.block_size, "rows": w.rows,
                    "algorithmic_bytes": nbytes, "buffer_sets": nsets},
         "us_per_call": round(kern_ms * 1e3, 2),
-        "us_per_call_median": round(durs[len(durs) // 2] * 1e3, 2),
         "us_per_call_host_wall": round(wall_ms * 1e3, 2),
         "rows_per_s": round(w.rows / (kern_ms * 1e-3), 1),
         "pct_of_peak": round(100.0 * achieved / PEAK_HBM_GBS, 2),
@@ -608,23 +661,9 @@ def mla_bench(args, torch, pkg, w) -> int:
 
     for i in range(args.warmup):
         step(i)
-    torch.cuda.synchronize(dev)
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i)
-    torch.cuda.synchronize(dev)
-    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    for i in range(args.steps):
-        starts[i].record(stream)
-        step(i)
-        ends[i].record(stream)
-    torch.cuda.synchronize(dev)
-    durs = sorted(a.elapsed_time(b) for a, b in zip(starts, ends))
-    kern_ms = sum(durs) / len(durs)
-    value = nbytes / (wall_ms * 1e-3) / 1e9
-    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    kern_ms, wall_ms = timed_region(torch, dev, stream, step, args.steps)
+    value = nbytes / (kern_ms * 1e-3) / 1e9
+    achieved = value
     out_json = {
         "metric": "MLA backward (Task 03) dQ+dC: algorithmic GB/s (% of 8 TB/s) + us/call",
         "value": round(value, 1),
@@ -632,7 +671,7 @@ def mla_bench(args, torch, pkg, w) -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(wall_ms, 5),
+        "ms_per_step": round(kern_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -641,7 +680,6 @@ def mla_bench(args, torch, pkg, w) -> int:
         "config": {"workload": w.name, "B": w.B, "H": w.H, "S": w.S, "D": w.D,
                    "sm_scale": w.sm_scale, "algorithmic_bytes": nbytes, "buffer_sets": nsets},
         "us_per_call": round(kern_ms * 1e3, 2),
-        "us_per_call_median": round(durs[len(durs) // 2] * 1e3, 2),
         "us_per_call_host_wall": round(wall_ms * 1e3, 2),
         "pct_of_peak": round(100.0 * achieved / PEAK_HBM_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
@@ -661,7 +699,7 @@ def mla_cpu_baseline(w, q, c, out, do, lse, pkg, args, torch) -> dict:
     import dataclasses
     import numpy as np
     import oracle
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = cpu_threads()
     hs = min(8, w.H)
     sw = dataclasses.replace(w, B=1, H=hs)
     sq, sc, so, sd, sl = (q[:1, :hs].contiguous(), c[:1].contiguous(), out[:1, :hs].contiguous(),
@@ -703,7 +741,7 @@ def dsa_cpu_baseline(w, scores, pt, pos, kv, gpu_set, nbytes, args, torch) -> di
     checks those GPU rows against it."""
     import numpy as np
     import oracle
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = cpu_threads()
     rows = min(w.Q, w.rows)
     sub = scores[:1, :1]
     s_np = sub.contiguous().view(torch.uint16).numpy() if w.dtype == torch.bfloat16 else \
@@ -758,25 +796,11 @@ def gemm_bench(args, torch, pkg, w) -> int:
 
     for i in range(args.warmup):
         step(i)
-    torch.cuda.synchronize(dev)
     stream = torch.cuda.current_stream(dev)
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i)
-    torch.cuda.synchronize(dev)
-    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    for i in range(args.steps):
-        starts[i].record(stream)
-        step(i)
-        ends[i].record(stream)
-    torch.cuda.synchronize(dev)
-    durs = sorted(st.elapsed_time(en) for st, en in zip(starts, ends))
-    kern_ms = sum(durs) / len(durs)
+    kern_ms, wall_ms = timed_region(torch, dev, stream, step, args.steps)
     flops = w.flops()
-    value = flops / (wall_ms * 1e-3) / 1e12
-    achieved = flops / (kern_ms * 1e-3) / 1e12
+    value = flops / (kern_ms * 1e-3) / 1e12
+    achieved = value
     traffic = measured_traffic(w.name)
     out = {
         "metric": "fp8 block-scaled GEMM TFLOP/s (% of 5.0 PFLOP/s dense fp8), consumer of "
@@ -786,7 +810,7 @@ def gemm_bench(args, torch, pkg, w) -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(wall_ms, 5),
+        "ms_per_step": round(kern_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -797,7 +821,6 @@ def gemm_bench(args, torch, pkg, w) -> int:
                    "flops": flops, "min_hbm_bytes": set_bytes, "buffer_sets": nsets,
                    "route": pkg.gemm_route(w.M, w.N, w.K)},
         "us_per_call": round(kern_ms * 1e3, 2),
-        "us_per_call_median": round(durs[len(durs) // 2] * 1e3, 2),
         "us_per_call_host_wall": round(wall_ms * 1e3, 2),
         "pct_of_peak": round(100.0 * achieved / PEAK_FP8_TFLOPS, 2),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_FP8_TFLOPS,
@@ -816,7 +839,7 @@ def gemm_cpu_baseline(w, a_q, a_s, b_q, b_s, c_gpu, args, torch) -> dict:
     rows of the workload and checks those rows of the GPU's output against it."""
     import numpy as np
     import oracle
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = cpu_threads()
     rows = max(1, min(16, w.M))
     u8 = lambda t: t.contiguous().view(torch.uint8).numpy()
     aq, bq = u8(a_q[:rows]), u8(b_q)

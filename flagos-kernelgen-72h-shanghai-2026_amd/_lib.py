@@ -17,13 +17,15 @@ import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = PKG_DIR / "libfagq.so"
 
-# Enums of include/fagq.h.
+# Enums of include/fagq.h and include/fagq_diag.h.
 Q_INT8, Q_FP8_E4M3FN = 0, 1
 SCALE_F32, SCALE_UE8M0 = 0, 1
 LAYOUT_ROW_MAJOR, LAYOUT_COL_MAJOR = 0, 1
 ROUND_RNE, ROUND_TRUNC = 0, 1
 MAX_D = 32768
 MAX_PARTS, MAX_D_PARTS = 8, 16384
+MODE_INDEPENDENT, MODE_SHARED_GAMMA, MODE_WIDE_SCALES = 0, 1, 2
+STREAM_COPY, STREAM_READ, STREAM_WRITE = 0, 1, 2
 
 STATUS_NAMES = {
     0: "FAGQ_OK", 1: "FAGQ_E_NULL", 2: "FAGQ_E_SHAPE", 3: "FAGQ_E_GROUP", 4: "FAGQ_E_ALIGN",
@@ -37,9 +39,10 @@ _P, _I64, _I, _F = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
 
 class Route(ctypes.Structure):
     _fields_ = [("waves_per_row", ctypes.c_int32), ("steps_per_wave", ctypes.c_int32),
-                ("rows_per_block", ctypes.c_int32), ("rows_in_sequence", ctypes.c_int32),
-                ("block_threads", ctypes.c_int32), ("reserved", ctypes.c_int32),
-                ("grid_blocks", ctypes.c_int64)]
+                ("rows_per_block", ctypes.c_int32), ("row_group_mode", ctypes.c_int32),
+                ("block_threads", ctypes.c_int32), ("lds_bytes", ctypes.c_int32),
+                ("grid_blocks", ctypes.c_int64), ("xcd_remap", ctypes.c_int32),
+                ("reserved", ctypes.c_int32)]
 
 
 class GemmRoute(ctypes.Structure):
@@ -51,12 +54,14 @@ class GemmRoute(ctypes.Structure):
 SIGNATURES = {
     "fagq_launch": ([_P] * 7 + [_I64, _I64, _I64, _F, _I, _I, _I, _I, _P], _I),
     "fagq_launch_parts": ([_P, _I] + [_P] * 5 + [_I64, _I64, _I64, _F, _I, _I, _I, _I, _P], _I),
-    "fagq_launch_mapped": ([_P] * 7 + [_I64, _I64, _I64, _F, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
-    "fagq_query_route": ([_I64, _I64, _I64, ctypes.POINTER(Route)], _I),
+    "fagq_launch_mapped": ([_P] * 7 + [_I64, _I64, _I64, _F] + [_I] * 9 + [_P], _I),
+    "fagq_query_route": ([_I64, _I64, _I64, _I, _I, ctypes.POINTER(Route)], _I),
     "fagq_status_string": ([_I], ctypes.c_char_p),
     "fagq_version": ([], _I),
-    "fagq_diag_encode": ([_P, _P, _I64, _I, _I, _P], _I),
+    "fagq_diag_encode": ([_P, _P, _I64, _I, _I, _I, _P], _I),
     "fagq_diag_copy": ([_P, _P, _I64, _P], _I),
+    "fagq_diag_stream": ([_P, _P, _I64, _I, _P], _I),
+    "fagq_diag_scale_offsets": ([_I64, _I64, _I64, _I, _I, _I, _I64, _P, _I64], _I),
     "fagq_diag_mfma_peak": ([_P, _I64, _I, _P], _I),
     "fagq_dsa_topk_launch": ([_P, _I, _P, _P, _P, _I, _P, _P] + [_I64] * 6 + [_P], _I),
     "fagq_gemm_launch": ([_P] * 5 + [_I64, _I64, _I64, _I, _I, _I, _P], _I),
@@ -115,7 +120,9 @@ def check(status: int, what: str = "fagq_launch") -> None:
         raise FagqError(status, what)
 
 
-def query_route(M: int, D: int, group_size: int) -> dict:
+def query_route(M: int, D: int, group_size: int, scale_format: int = SCALE_F32,
+                scale_layout: int = LAYOUT_ROW_MAJOR) -> dict:
     r = Route()
-    check(load().fagq_query_route(M, D, group_size, ctypes.byref(r)), "fagq_query_route")
+    check(load().fagq_query_route(M, D, group_size, scale_format, scale_layout, ctypes.byref(r)),
+          "fagq_query_route")
     return {f: getattr(r, f) for f, _ in Route._fields_ if f != "reserved"}

@@ -19,12 +19,47 @@
 namespace fagq {
 namespace {
 
-// Plain 16-byte-vector copy, for calibrating HBM byte counters.
-__global__ void __launch_bounds__(256) fagq_copy16(const u32x4* __restrict__ src,
-                                                   u32x4* __restrict__ dst, int64_t n16) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
-    __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+// HBM ceiling probes (and byte-counter calibration): every thread moves one
+// 16-byte chunk through buffer descriptors, with the operator's cache
+// policies (non-temporal loads, sc1 | nt stores).  kStreamBlock threads per
+// workgroup, one workgroup per kStreamBlock * 16 bytes.
+constexpr int kStreamBlock = 512;
+
+__device__ __forceinline__ uint32_t chunk_bytes(int64_t bytes) {
+  const int64_t rem = bytes - (int64_t)blockIdx.x * kStreamBlock * 16;
+  return rem > kStreamBlock * 16 ? kStreamBlock * 16u : (uint32_t)rem;
+}
+
+__global__ void __launch_bounds__(kStreamBlock) fagq_stream_copy(const uint8_t* src, uint8_t* dst,
+                                                                 int64_t bytes) {
+  const int64_t base = (int64_t)blockIdx.x * kStreamBlock * 16;
+  const uint32_t n = chunk_bytes(bytes);
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(src + base, n), threadIdx.x * 16,
+                                                        0, kNonTemporal);
+  __builtin_amdgcn_raw_buffer_store_b128(v, make_rsrc(dst + base, n), threadIdx.x * 16, 0,
+                                         kStoreAux);
+}
+
+// Read-only: the loaded data is kept live by a store to dst[0..15] that runs
+// only when a chunk's four words XOR to 0x9e3779b9.
+__global__ void __launch_bounds__(kStreamBlock) fagq_stream_read(const uint8_t* src, uint8_t* dst,
+                                                                 int64_t bytes) {
+  const int64_t base = (int64_t)blockIdx.x * kStreamBlock * 16;
+  const uint32_t n = chunk_bytes(bytes);
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(src + base, n), threadIdx.x * 16,
+                                                        0, kNonTemporal);
+  if ((v[0] ^ v[1] ^ v[2] ^ v[3]) == 0x9e3779b9u)
+    __builtin_amdgcn_raw_buffer_store_b128(v, make_rsrc(dst, 16), 0, 0, 0);
+}
+
+// Write-only: each chunk gets (its byte offset, thread, 2, 3).
+__global__ void __launch_bounds__(kStreamBlock) fagq_stream_write(const uint8_t*, uint8_t* dst,
+                                                                  int64_t bytes) {
+  const int64_t base = (int64_t)blockIdx.x * kStreamBlock * 16;
+  const uint32_t n = chunk_bytes(bytes);
+  const u32x4 v = {(uint32_t)base, threadIdx.x, 2u, 3u};
+  __builtin_amdgcn_raw_buffer_store_b128(v, make_rsrc(dst + base, n), threadIdx.x * 16, 0,
+                                         kStoreAux);
 }
 
 constexpr int kVersion = 1 * 10000 + 0 * 100 + 0;
@@ -33,16 +68,18 @@ constexpr int kMaxDevices = 64;
 struct Mapping {
   int wpr;        // waves per row
   int ns;         // steps per wave
-  int rpb;        // row groups per workgroup
-  int rseq;       // rows each row group processes in turn
+  int rpb;        // row groups (rows) per workgroup
+  int mode;       // RowGroupMode
   int block;      // threads per workgroup
+  int lds;        // dynamic LDS bytes reserved per workgroup (caps workgroups per CU)
   int64_t grid;   // workgroups
 };
 
+constexpr int kMaxDynLds = 65536;
+
 // Route-table knobs, read once: FAGQ_PREFILL_ROWS is the row count from which
 // rows are split into 2-step waves (FAGQ_PREFILL_STEPS) instead of 1-step
-// waves; FAGQ_PREFILL_RSEQ sets the rows each row group processes in turn
-// (1 by default: prefetching a second row measured no faster).
+// waves.
 int env_int(const char* name, int dflt) {
   const char* s = std::getenv(name);
   const int v = s ? std::atoi(s) : 0;
@@ -59,23 +96,20 @@ int prefill_steps() {
   return v;
 }
 
-int prefill_rseq() {
-  static const int v = env_int("FAGQ_PREFILL_RSEQ", 1);
-  return v;
-}
-
 // Workgroup -> row-tile order (see tile_of_block): column-major scales put
 // neighbouring rows' scale words next to each other, so chunks of 8 (fp32)
-// or 32 (ue8m0) consecutive row tiles go to one XCD and leave its L2 as full
-// 32-byte writes; otherwise dispatch order.  FAGQ_XCD_REMAP overrides.
-int remap_for(int scale_layout, int scale_format, int rpb) {
+// or 32 (ue8m0) consecutive rows go to one XCD and leave its L2 as full
+// 32-byte writes (16 fp32 rows when a workgroup stores two rows' words at
+// once, measured best at 16384 x 7168); otherwise dispatch order.
+// FAGQ_XCD_REMAP overrides.
+int remap_for(int scale_layout, int scale_format, int rpb, int mode) {
   static const int forced = [] {
     const char* s = std::getenv("FAGQ_XCD_REMAP");
     return s ? std::atoi(s) : -1;
   }();
   if (forced >= 0) return forced;
   if (scale_layout != FAGQ_LAYOUT_COL_MAJOR) return 0;
-  const int rows = scale_format == FAGQ_SCALE_F32 ? 8 : 32;
+  const int rows = scale_format == FAGQ_SCALE_F32 ? (mode == RG_WIDE_SCALES ? 16 : 8) : 32;
   return rows / rpb > 1 ? rows / rpb : 0;
 }
 
@@ -83,33 +117,48 @@ bool valid_remap(int r) { return r == 0 || r == 1 || (r >= 2 && r <= 64 && (r & 
 
 int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
-// Completes a mapping from (wpr, rpb, rseq); returns false if it is not launchable.
-bool finish_mapping(int64_t M, int D, int wpr, int rpb, int rseq, Mapping* m) {
+// Completes a mapping from (wpr, rpb, mode, lds); returns false if it is not
+// launchable.  The shared modes need the row's steps to fit the LDS gamma
+// buffer (wpr * ns <= 16, i.e. D <= 8192); the wide-scale mode stores 2 or 4
+// rows' words at once.
+bool finish_mapping(int64_t M, int D, int wpr, int rpb, int mode, int lds, Mapping* m) {
   const int steps = ceil_div(D, kStepCols);
   if (wpr < 1 || wpr > kMaxWavesPerBlock || rpb < 1 || wpr * rpb > kMaxWavesPerBlock) return false;
-  if (rseq_index(rseq) < 0) return false;
+  if (mode < 0 || mode >= kNumModes || lds < 0 || lds > kMaxDynLds) return false;
   const int ns = ceil_div(steps, wpr);
   if (ns > kMaxStepsPerWave) return false;
+  if (mode != RG_INDEPENDENT && wpr * ns > kMaxSharedSteps) return false;
+  if (mode == RG_WIDE_SCALES && rpb != 2 && rpb != kMaxWideRows) return false;
   m->wpr = wpr;
   m->ns = ns;
   m->rpb = rpb;
-  m->rseq = rseq;
+  m->mode = mode;
   m->block = 64 * wpr * rpb;
-  const int64_t per_block = (int64_t)rpb * rseq;
-  m->grid = (M + per_block - 1) / per_block;
+  m->lds = lds;
+  m->grid = (M + rpb - 1) / rpb;
   return m->grid <= INT32_MAX;
 }
 
 // The route table.  Each row is split over waves of one workgroup so that
-// every wave streams only 1-2 KB of each input per step (dispatch-ordered
-// workgroups then keep the set of rows in flight small, which HBM rewards).
-// Prefill (M >= prefill_rows()): 2 steps per wave, one row per workgroup.
-// Decode: 1 step per wave, one row per workgroup, as many waves as the row
-// has steps (<= 16).
+// every wave streams only 1-4 KB of each input (dispatch-ordered workgroups
+// then keep the set of rows in flight small, which HBM rewards).
+// * Prefill (M >= prefill_rows()) with fp32 column-major scales and
+//   12..16 steps per row (6144 <= D <= 8192, the DeepSeek-V3 width among
+//   them): two rows per workgroup of 4-step waves, gamma loaded once per
+//   workgroup and shared through LDS, each group's two scale words stored
+//   together (RG_WIDE_SCALES).  At 16384 x 7168 this measured 129.8 us
+//   against 134.1 us for one row of 2-step waves.
+// * Other prefill: 2 steps per wave, one row per workgroup.
+// * Decode: 1 step per wave, one row per workgroup, as many waves as the row
+//   has steps (<= 16).
 // Rows of more than 16 steps use up to 4 steps per wave.
-void choose_mapping(int64_t M, int D, Mapping* m) {
+void choose_mapping(int64_t M, int D, int scale_format, int scale_layout, Mapping* m) {
   const int steps = ceil_div(D, kStepCols);
   const bool prefill = M >= prefill_rows();
+  if (prefill && scale_format == FAGQ_SCALE_F32 && scale_layout == FAGQ_LAYOUT_COL_MAJOR &&
+      steps >= 12 && steps <= kMaxSharedSteps &&
+      finish_mapping(M, D, ceil_div(steps, kMaxStepsPerWave), 2, RG_WIDE_SCALES, 0, m))
+    return;
   int ns = prefill ? prefill_steps() : 1;
   if (ns > kMaxStepsPerWave) ns = kMaxStepsPerWave;
   const int min_ns = ceil_div(steps, kMaxWavesPerBlock);
@@ -117,9 +166,7 @@ void choose_mapping(int64_t M, int D, Mapping* m) {
   if (ns > steps) ns = steps;
   const int wpr = ceil_div(steps, ns);
   const int rpb = wpr >= 4 ? 1 : 4 / wpr;
-  int rseq = prefill ? prefill_rseq() : 1;
-  if (rseq_index(rseq) < 0) rseq = 1;
-  finish_mapping(M, D, wpr, rpb, rseq, m);
+  finish_mapping(M, D, wpr, rpb, RG_INDEPENDENT, 0, m);
 }
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
@@ -144,9 +191,10 @@ int validate(const void* x, const void* residual, const void* gamma, const void*
   if (G != 64 && G != 128 && G != 256) return FAGQ_E_GROUP;
   if (M < 0 || D <= 0 || D % G != 0) return FAGQ_E_SHAPE;
   if (D > FAGQ_MAX_D || M > (int64_t)INT32_MAX) return FAGQ_E_TOO_LARGE;
-  // Column-major scales are addressed with 32-bit buffer offsets.
+  // Column-major scales are addressed with 32-bit buffer offsets, and lanes
+  // without a group store at offset 0xffffffff, which must stay outside.
   if (scale_layout == FAGQ_LAYOUT_COL_MAJOR &&
-      M * (D / G) * (scale_format == FAGQ_SCALE_F32 ? 4 : 1) > (int64_t)UINT32_MAX)
+      M * (D / G) * (scale_format == FAGQ_SCALE_F32 ? 4 : 1) > (int64_t)UINT32_MAX - 16)
     return FAGQ_E_TOO_LARGE;
   if (!(eps >= 0.0f) || !std::isfinite(eps)) return FAGQ_E_EPS;
   if (!aligned(x, 16) || !aligned(residual, 16) || !aligned(gamma, 16) ||
@@ -178,8 +226,12 @@ int validate(const void* x, const void* residual, const void* gamma, const void*
 
 }  // namespace
 
-// gfx950 check, done once per device.
+// gfx950 check, done once per device.  The launch-failure test build has no
+// device to check.
 int device_check() {
+#ifdef FAGQ_TEST_LAUNCH_FAILURE
+  return FAGQ_OK;
+#endif
   static std::atomic<int> cache[kMaxDevices];   // 0 unknown, 1 gfx950, 2 other
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -199,12 +251,12 @@ int device_check() {
 namespace {
 
 LaunchFn lookup(int q_format, int scale_format, int rounding, int lpg_idx, int steps, bool norm,
-                int rseq) {
+                int mode) {
   const int qf = q_format == FAGQ_Q_FP8_E4M3FN ? QF_FP8
                  : rounding == FAGQ_ROUND_RNE  ? QF_I8_RNE
                                                : QF_I8_TRUNC;
   const bool ue = scale_format == FAGQ_SCALE_UE8M0;
-  const int ri = rseq_index(rseq);
+  const int ri = mode;
   switch (qf) {
     case QF_FP8:
       return ue ? lookup_q0_s1(lpg_idx, steps, norm, ri) : lookup_q0_s0(lpg_idx, steps, norm, ri);
@@ -243,12 +295,12 @@ void choose_mapping_parts(int64_t M, int D, Mapping* m) {
   if (ns > steps) ns = steps;
   const int wpr = ceil_div(steps, ns);
   const int rpb = wpr >= 4 ? 1 : 4 / wpr;
-  finish_mapping(M, D, wpr, rpb, 1, m);
+  finish_mapping(M, D, wpr, rpb, RG_INDEPENDENT, 0, m);
 }
 
 void fill_args(KArgs* a, const Mapping& m, const void* x, const void* residual, const void* gamma,
                void* residual_out, void* norm_out, void* q, void* scale, int64_t M, int64_t D,
-               int64_t G, float eps, int scale_layout, int remap) {
+               int64_t G, float eps, int scale_format, int scale_layout, int remap) {
   a->x = static_cast<const uint16_t*>(x);
   a->res = static_cast<const uint16_t*>(residual);
   a->gamma = static_cast<const uint16_t*>(gamma);
@@ -266,9 +318,23 @@ void fill_args(KArgs* a, const Mapping& m, const void* x, const void* residual, 
   a->remap = remap;
   a->remap_shift = remap >= 2 ? __builtin_ctz((unsigned)remap) : 0;
   a->wpr_magic = (65536 + m.wpr - 1) / m.wpr;
+  const uintptr_t wide_bytes =
+      (uintptr_t)m.rpb * (uintptr_t)(scale_format == FAGQ_SCALE_F32 ? 4 : 1);
+  a->wide_ok = m.mode == RG_WIDE_SCALES && M % m.rpb == 0 &&
+               (reinterpret_cast<uintptr_t>(scale) % wide_bytes) == 0;
   a->nparts = 0;
   for (int p = 0; p < kMaxParts; ++p) a->xparts[p] = nullptr;
 }
+
+// Status of a kernel launch.  Built with -DFAGQ_TEST_LAUNCH_FAILURE (a test
+// build only, never the shipped library) every launch reports
+// hipErrorLaunchFailure without reaching the runtime, so that the CPU tests
+// can check how a launch failure propagates through the C ABI and Python.
+#ifdef FAGQ_TEST_LAUNCH_FAILURE
+int launch_status(hipError_t) { return -(int)hipErrorLaunchFailure; }
+#else
+int launch_status(hipError_t e) { return e == hipSuccess ? FAGQ_OK : -(int)e; }
+#endif
 
 int launch_with(const Mapping& m, const void* x, const void* residual, const void* gamma,
                 void* residual_out, void* norm_out, void* q, void* scale, int64_t M, int64_t D,
@@ -278,12 +344,11 @@ int launch_with(const Mapping& m, const void* x, const void* residual, const voi
   if (dc != FAGQ_OK) return dc;
   KArgs a;
   fill_args(&a, m, x, residual, gamma, residual_out, norm_out, q, scale, M, D, G, eps,
-            scale_layout, remap);
+            scale_format, scale_layout, remap);
   const LaunchFn fn = lookup(q_format, scale_format, rounding, lpg_index((int)G), m.ns,
-                             norm_out != nullptr, m.rseq);
-  const hipError_t e = fn(a, dim3((unsigned)m.grid), dim3((unsigned)m.block),
-                          static_cast<hipStream_t>(stream));
-  return e == hipSuccess ? FAGQ_OK : -(int)e;
+                             norm_out != nullptr, m.mode);
+  return launch_status(fn(a, dim3((unsigned)m.grid), dim3((unsigned)m.block), (unsigned)m.lds,
+                          static_cast<hipStream_t>(stream)));
 }
 
 }  // namespace
@@ -301,23 +366,25 @@ FAGQ_API int fagq_launch(const void* x, const void* residual, const void* gamma,
                          eps, q_format, scale_format, scale_layout, rounding);
   if (v != FAGQ_OK || M == 0) return v;
   Mapping m;
-  choose_mapping(M, (int)D, &m);
+  choose_mapping(M, (int)D, scale_format, scale_layout, &m);
   return launch_with(m, x, residual, gamma, residual_out, norm_out, q, scale, M, D, group_size,
                      eps, q_format, scale_format, scale_layout, rounding,
-                     remap_for(scale_layout, scale_format, m.rpb * m.rseq), stream);
+                     remap_for(scale_layout, scale_format, m.rpb, m.mode), stream);
 }
 
 FAGQ_API int fagq_launch_mapped(const void* x, const void* residual, const void* gamma,
                                 void* residual_out, void* norm_out, void* q, void* scale,
                                 int64_t M, int64_t D, int64_t group_size, float eps,
                                 int q_format, int scale_format, int scale_layout, int rounding,
-                                int waves_per_row, int rows_per_block, int rows_in_sequence,
-                                int xcd_remap, void* stream) {
+                                int waves_per_row, int rows_per_block, int row_group_mode,
+                                int xcd_remap, int lds_bytes, void* stream) {
   const int v = validate(x, residual, gamma, residual_out, norm_out, q, scale, M, D, group_size,
                          eps, q_format, scale_format, scale_layout, rounding);
   if (v != FAGQ_OK) return v;
   Mapping m;
-  if (!finish_mapping(M, (int)D, waves_per_row, rows_per_block, rows_in_sequence, &m))
+  if (!finish_mapping(M, (int)D, waves_per_row, rows_per_block, row_group_mode, lds_bytes, &m))
+    return FAGQ_E_FORMAT;
+  if (row_group_mode == RG_WIDE_SCALES && scale_layout != FAGQ_LAYOUT_COL_MAJOR)
     return FAGQ_E_FORMAT;
   if (!valid_remap(xcd_remap)) return FAGQ_E_FORMAT;
   if (M == 0) return FAGQ_OK;
@@ -359,40 +426,46 @@ FAGQ_API int fagq_launch_parts(const void* const* x_parts, int nparts, const voi
   choose_mapping_parts(M, (int)D, &m);
   KArgs a;
   fill_args(&a, m, x_parts[0], residual, gamma, residual_out, nullptr, q, scale, M, D, group_size,
-            eps, scale_layout, remap_for(scale_layout, scale_format, m.rpb));
+            eps, scale_format, scale_layout, remap_for(scale_layout, scale_format, m.rpb, m.mode));
   a.nparts = nparts;
   for (int p = 0; p < nparts; ++p) a.xparts[p] = static_cast<const uint16_t*>(x_parts[p]);
   const LaunchFn fn = lookup_parts(q_format, scale_format, rounding, lpg_index((int)group_size), m.ns);
-  const hipError_t e = fn(a, dim3((unsigned)m.grid), dim3((unsigned)m.block),
-                          static_cast<hipStream_t>(stream));
-  return e == hipSuccess ? FAGQ_OK : -(int)e;
+  return launch_status(fn(a, dim3((unsigned)m.grid), dim3((unsigned)m.block), 0u,
+                          static_cast<hipStream_t>(stream)));
 }
 
-FAGQ_API int fagq_query_route(int64_t M, int64_t D, int64_t group_size, fagq_route* route) {
+FAGQ_API int fagq_query_route(int64_t M, int64_t D, int64_t group_size, int scale_format,
+                               int scale_layout, fagq_route* route) {
   if (!route) return FAGQ_E_NULL;
   if (group_size != 64 && group_size != 128 && group_size != 256) return FAGQ_E_GROUP;
   if (M < 0 || D <= 0 || D % group_size != 0) return FAGQ_E_SHAPE;
   if (D > FAGQ_MAX_D || M > (int64_t)INT32_MAX) return FAGQ_E_TOO_LARGE;
+  if (scale_format != FAGQ_SCALE_F32 && scale_format != FAGQ_SCALE_UE8M0) return FAGQ_E_FORMAT;
+  if (scale_layout != FAGQ_LAYOUT_ROW_MAJOR && scale_layout != FAGQ_LAYOUT_COL_MAJOR)
+    return FAGQ_E_FORMAT;
   Mapping m;
-  choose_mapping(M, (int)D, &m);
+  choose_mapping(M, (int)D, scale_format, scale_layout, &m);
   route->waves_per_row = m.wpr;
   route->steps_per_wave = m.ns;
   route->rows_per_block = m.rpb;
-  route->rows_in_sequence = m.rseq;
+  route->row_group_mode = m.mode;
   route->block_threads = m.block;
-  route->reserved = 0;
+  route->lds_bytes = m.lds;
   route->grid_blocks = m.grid;
+  route->xcd_remap = remap_for(scale_layout, scale_format, m.rpb, m.mode);
+  route->reserved = 0;
   return FAGQ_OK;
 }
 
 FAGQ_API int fagq_diag_encode(const float* in, void* out, int64_t n, int q_format, int rounding,
-                              void* stream) {
+                              int clamp, void* stream) {
   if (!in || !out) return FAGQ_E_NULL;
   if (n < 0 || n % 8 != 0) return FAGQ_E_SHAPE;
   if (!aligned(in, 16) || !aligned(out, 8)) return FAGQ_E_ALIGN;
   if (q_format != FAGQ_Q_INT8 && q_format != FAGQ_Q_FP8_E4M3FN) return FAGQ_E_FORMAT;
   if (rounding != FAGQ_ROUND_RNE && rounding != FAGQ_ROUND_TRUNC) return FAGQ_E_FORMAT;
   if (q_format == FAGQ_Q_FP8_E4M3FN && rounding != FAGQ_ROUND_RNE) return FAGQ_E_FORMAT;
+  if (clamp != 0 && clamp != 1) return FAGQ_E_FORMAT;
   if (n == 0) return FAGQ_OK;
   const int dc = device_check();
   if (dc != FAGQ_OK) return dc;
@@ -403,30 +476,79 @@ FAGQ_API int fagq_diag_encode(const float* in, void* out, int64_t n, int q_forma
   u32x2* o = static_cast<u32x2*>(out);
   int64_t count8 = n8;
   void* args[] = {&src, &o, &count8};
-  const void* k = q_format == FAGQ_Q_FP8_E4M3FN ? reinterpret_cast<const void*>(&fagq_encode<QF_FP8>)
-                  : rounding == FAGQ_ROUND_RNE ? reinterpret_cast<const void*>(&fagq_encode<QF_I8_RNE>)
-                                               : reinterpret_cast<const void*>(&fagq_encode<QF_I8_TRUNC>);
-  const hipError_t e = hipLaunchKernel(k, grid, block, args, 0, s);
-  return e == hipSuccess ? FAGQ_OK : -(int)e;
+  const int qf = q_format == FAGQ_Q_FP8_E4M3FN ? QF_FP8
+                 : rounding == FAGQ_ROUND_RNE  ? QF_I8_RNE
+                                               : QF_I8_TRUNC;
+  static const void* const kernels[3][2] = {
+      {reinterpret_cast<const void*>(&fagq_encode<QF_FP8, false>),
+       reinterpret_cast<const void*>(&fagq_encode<QF_FP8, true>)},
+      {reinterpret_cast<const void*>(&fagq_encode<QF_I8_RNE, false>),
+       reinterpret_cast<const void*>(&fagq_encode<QF_I8_RNE, true>)},
+      {reinterpret_cast<const void*>(&fagq_encode<QF_I8_TRUNC, false>),
+       reinterpret_cast<const void*>(&fagq_encode<QF_I8_TRUNC, true>)}};
+  return launch_status(hipLaunchKernel(kernels[qf][clamp], grid, block, args, 0, s));
+}
+
+FAGQ_API int fagq_diag_stream(const void* src, void* dst, int64_t bytes, int mode,
+                              void* stream) {
+  if (mode < FAGQ_STREAM_COPY || mode > FAGQ_STREAM_WRITE) return FAGQ_E_FORMAT;
+  if ((mode != FAGQ_STREAM_WRITE && !src) || !dst) return FAGQ_E_NULL;
+  if (bytes < 0 || bytes % 16 != 0) return FAGQ_E_SHAPE;
+  if ((src && !aligned(src, 16)) || !aligned(dst, 16)) return FAGQ_E_ALIGN;
+  if (bytes == 0) return FAGQ_OK;
+  const int64_t blocks = (bytes + kStreamBlock * 16 - 1) / (kStreamBlock * 16);
+  if (blocks > INT32_MAX) return FAGQ_E_TOO_LARGE;
+  const int dc = device_check();
+  if (dc != FAGQ_OK) return dc;
+  const uint8_t* s8 = static_cast<const uint8_t*>(src);
+  uint8_t* d8 = static_cast<uint8_t*>(dst);
+  int64_t n = bytes;
+  void* args[] = {&s8, &d8, &n};
+  const void* k = mode == FAGQ_STREAM_COPY ? reinterpret_cast<const void*>(&fagq_stream_copy)
+                  : mode == FAGQ_STREAM_READ ? reinterpret_cast<const void*>(&fagq_stream_read)
+                                             : reinterpret_cast<const void*>(&fagq_stream_write);
+  return launch_status(hipLaunchKernel(k, dim3((unsigned)blocks), dim3(kStreamBlock), args, 0,
+                                       static_cast<hipStream_t>(stream)));
 }
 
 FAGQ_API int fagq_diag_copy(const void* src, void* dst, int64_t bytes, void* stream) {
-  if (!src || !dst) return FAGQ_E_NULL;
-  if (bytes < 0 || bytes % 16 != 0) return FAGQ_E_SHAPE;
-  if (!aligned(src, 16) || !aligned(dst, 16)) return FAGQ_E_ALIGN;
-  if (bytes == 0) return FAGQ_OK;
-  const int dc = device_check();
-  if (dc != FAGQ_OK) return dc;
-  const int64_t n16 = bytes / 16;
-  const int64_t want = (n16 + 255) / 256;
-  const dim3 grid((unsigned)(want < 8192 ? want : 8192)), block(256);
-  const u32x4* s4 = static_cast<const u32x4*>(src);
-  u32x4* d4 = static_cast<u32x4*>(dst);
-  int64_t count16 = n16;
-  void* args[] = {&s4, &d4, &count16};
-  const hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&fagq_copy16), grid, block,
-                                       args, 0, static_cast<hipStream_t>(stream));
-  return e == hipSuccess ? FAGQ_OK : -(int)e;
+  return fagq_diag_stream(src, dst, bytes, FAGQ_STREAM_COPY, stream);
+}
+
+FAGQ_API int fagq_diag_scale_offsets(int64_t M, int64_t D, int64_t group_size, int scale_format,
+                                     int scale_layout, int waves_per_row, int64_t row,
+                                     int64_t* out, int64_t cap) {
+  if (!out) return FAGQ_E_NULL;
+  if (group_size != 64 && group_size != 128 && group_size != 256) return FAGQ_E_GROUP;
+  if (M <= 0 || D <= 0 || D % group_size != 0) return FAGQ_E_SHAPE;
+  if (D > FAGQ_MAX_D || M > (int64_t)INT32_MAX) return FAGQ_E_TOO_LARGE;
+  if (scale_format != FAGQ_SCALE_F32 && scale_format != FAGQ_SCALE_UE8M0) return FAGQ_E_FORMAT;
+  if (scale_layout != FAGQ_LAYOUT_ROW_MAJOR && scale_layout != FAGQ_LAYOUT_COL_MAJOR)
+    return FAGQ_E_FORMAT;
+  const uint32_t sb = scale_format == FAGQ_SCALE_F32 ? 4u : 1u;
+  const int col = scale_layout == FAGQ_LAYOUT_COL_MAJOR;
+  if (col && M * (D / group_size) * sb > (int64_t)UINT32_MAX - 16) return FAGQ_E_TOO_LARGE;
+  if (row < 0 || row >= M) return FAGQ_E_SHAPE;
+  Mapping m;
+  if (!finish_mapping(M, (int)D, waves_per_row, 1, RG_INDEPENDENT, 0, &m)) return FAGQ_E_FORMAT;
+  if (cap < (int64_t)m.wpr * m.ns * 64) return FAGQ_E_SHAPE;
+  const int G = (int)group_size, lpg = G / 8;
+  const uint32_t gps = (uint32_t)(kStepCols / G);
+  for (int part = 0; part < m.wpr; ++part) {
+    const int c0 = part * m.ns * kStepCols;
+    const uint32_t cols = D > c0 ? (uint32_t)(D - c0) : 0u;
+    const ScaleSpan sp = scale_span(M, (int32_t)(D / G), col, sb, row, true, c0 / G, cols != 0);
+    for (int k = 0; k < m.ns; ++k)
+      for (int lane = 0; lane < 64; ++lane) {
+        const uint32_t off = scale_lane_offset((uint32_t)(lane / lpg), (uint32_t)k, gps,
+                                               sp.ngroups, sp.gstride);
+        // A store of sb bytes at `off` lands only if it fits the descriptor.
+        const bool lands = (uint64_t)off + sb <= (uint64_t)sp.bytes;
+        out[((int64_t)part * m.ns + k) * 64 + lane] =
+            lands ? sp.base + (int64_t)(off / sb) : -1;
+      }
+  }
+  return FAGQ_OK;
 }
 
 FAGQ_API const char* fagq_status_string(int status) {

@@ -10,28 +10,27 @@
 
 namespace fagq {
 
-using LaunchFn = hipError_t (*)(const KArgs&, dim3, dim3, hipStream_t);
+// (args, grid, block, dynamic LDS bytes, stream)
+using LaunchFn = hipError_t (*)(const KArgs&, dim3, dim3, unsigned, hipStream_t);
 
 constexpr int kNumLpg = 3;      // lanes per group 8, 16, 32  <->  G = 64, 128, 256
-constexpr int kNumRseq = 3;     // rows in sequence 1, 2, 4
 
 constexpr int lpg_index(int group_size) {
   return group_size == 64 ? 0 : group_size == 128 ? 1 : group_size == 256 ? 2 : -1;
 }
 
-constexpr int rseq_index(int rseq) { return rseq == 1 ? 0 : rseq == 2 ? 1 : rseq == 4 ? 2 : -1; }
 
 // FAGQ_OK if the current device is gfx950 (cached per device), else
 // FAGQ_E_DEVICE or -hipError_t.
 int device_check();
 
-// lookup_q<code>_s<scale>(lpg index, steps per wave in [1, 4], norm, rseq index).
-LaunchFn lookup_q0_s0(int lpg_idx, int steps, bool norm, int rseq_idx);   // fp8, f32
-LaunchFn lookup_q0_s1(int lpg_idx, int steps, bool norm, int rseq_idx);   // fp8, ue8m0
-LaunchFn lookup_q1_s0(int lpg_idx, int steps, bool norm, int rseq_idx);   // int8 rne, f32
-LaunchFn lookup_q1_s1(int lpg_idx, int steps, bool norm, int rseq_idx);   // int8 rne, ue8m0
-LaunchFn lookup_q2_s0(int lpg_idx, int steps, bool norm, int rseq_idx);   // int8 trunc, f32
-LaunchFn lookup_q2_s1(int lpg_idx, int steps, bool norm, int rseq_idx);   // int8 trunc, ue8m0
+// lookup_q<code>_s<scale>(lpg index, steps per wave in [1, 4], norm, row-group mode).
+LaunchFn lookup_q0_s0(int lpg_idx, int steps, bool norm, int mode);   // fp8, f32
+LaunchFn lookup_q0_s1(int lpg_idx, int steps, bool norm, int mode);   // fp8, ue8m0
+LaunchFn lookup_q1_s0(int lpg_idx, int steps, bool norm, int mode);   // int8 rne, f32
+LaunchFn lookup_q1_s1(int lpg_idx, int steps, bool norm, int mode);   // int8 rne, ue8m0
+LaunchFn lookup_q2_s0(int lpg_idx, int steps, bool norm, int mode);   // int8 trunc, f32
+LaunchFn lookup_q2_s1(int lpg_idx, int steps, bool norm, int mode);   // int8 trunc, ue8m0
 
 // Multi-input form (fagq_rows_parts): lookup_parts_q<code>_s<scale>(lpg index,
 // steps per wave in [1, kMaxStepsParts]).

@@ -1,6 +1,6 @@
 // fagq_inst.hip - instantiates fagq_rows for one (code format, scale format)
 // pair, selected with -DFAGQ_QF=<0|1|2> -DFAGQ_SF=<0|1>, for every supported
-// group size, steps per wave, norm_out choice and rows-in-sequence count,
+// group size, steps per wave, norm_out choice and row-group mode,
 // and fagq_rows_parts for every group size and steps per wave, and exports
 // their launch lookups.
 #include "fagq_dispatch.hpp"
@@ -19,37 +19,40 @@
 namespace fagq {
 namespace {
 
-template <int NS, int LPG, bool NORM, int RSEQ>
-hipError_t launch_rows(const KArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
+template <int NS, int LPG, bool NORM, int MODE>
+hipError_t launch_rows(const KArgs& a, dim3 grid, dim3 block, unsigned lds, hipStream_t stream) {
   void* args[] = {const_cast<KArgs*>(&a)};
   return hipLaunchKernel(
-      reinterpret_cast<const void*>(&fagq_rows<NS, LPG, FAGQ_QF, FAGQ_SF, NORM, RSEQ>), grid,
-      block, args, 0, stream);
+      reinterpret_cast<const void*>(&fagq_rows<NS, LPG, FAGQ_QF, FAGQ_SF, NORM, MODE>), grid,
+      block, args, lds, stream);
 }
 
 template <int NS, int LPG>
-hipError_t launch_rows_parts(const KArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
+hipError_t launch_rows_parts(const KArgs& a, dim3 grid, dim3 block, unsigned lds,
+                             hipStream_t stream) {
   void* args[] = {const_cast<KArgs*>(&a)};
   return hipLaunchKernel(
       reinterpret_cast<const void*>(&fagq_rows_parts<NS, LPG, FAGQ_QF, FAGQ_SF>), grid, block,
-      args, 0, stream);
+      args, lds, stream);
 }
 
 }  // namespace
 
 #define FAGQ_R(NS, LPG, NORM) \
-  {&launch_rows<NS, LPG, NORM, 1>, &launch_rows<NS, LPG, NORM, 2>, &launch_rows<NS, LPG, NORM, 4>}
+  {&launch_rows<NS, LPG, NORM, RG_INDEPENDENT>, &launch_rows<NS, LPG, NORM, RG_SHARED_GAMMA>, \
+   &launch_rows<NS, LPG, NORM, RG_WIDE_SCALES>}
 #define FAGQ_N(NS, LPG) {FAGQ_R(NS, LPG, false), FAGQ_R(NS, LPG, true)}
 #define FAGQ_S(LPG) {FAGQ_N(1, LPG), FAGQ_N(2, LPG), FAGQ_N(3, LPG), FAGQ_N(4, LPG)}
 
 static_assert(kMaxStepsPerWave == 4, "FAGQ_S lists 4 step counts");
+static_assert(kNumModes == 3, "FAGQ_R lists 3 row-group modes");
 
 // The table lives in a host function so that device compilation never sees
 // pointers to host launch stubs.
-LaunchFn FAGQ_LOOKUP(FAGQ_QF, FAGQ_SF)(int lpg_idx, int steps, bool norm, int rseq_idx) {
-  static const LaunchFn table[kNumLpg][kMaxStepsPerWave][2][kNumRseq] = {
+LaunchFn FAGQ_LOOKUP(FAGQ_QF, FAGQ_SF)(int lpg_idx, int steps, bool norm, int mode) {
+  static const LaunchFn table[kNumLpg][kMaxStepsPerWave][2][kNumModes] = {
       FAGQ_S(8), FAGQ_S(16), FAGQ_S(32)};
-  return table[lpg_idx][steps - 1][norm ? 1 : 0][rseq_idx];
+  return table[lpg_idx][steps - 1][norm ? 1 : 0][mode];
 }
 
 static_assert(kMaxStepsParts == 2, "the parts table lists 2 step counts");

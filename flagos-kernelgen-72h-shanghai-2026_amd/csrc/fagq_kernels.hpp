@@ -16,9 +16,10 @@
 // A row is split over wpr waves of one workgroup, each owning NS <= 4
 // consecutive steps and keeping r * gamma for them in VGPRs, so every input
 // byte is read from HBM once and no intermediate is written.  Only the fp64
-// partial sums of squares cross waves, through LDS.  A row group may process
-// RSEQ consecutive rows in turn, loading gamma once and the next row's
-// inputs while the current row is reduced and stored.
+// partial sums of squares cross waves, through LDS.  A workgroup holds rpb
+// row groups (one row each); in the shared modes row group 0 alone loads
+// gamma and hands it to the others through LDS, and may store the
+// column-major scales of all rpb rows with one wide store per group.
 //
 // Every buffer access passes its whole offset as the VGPR offset (constant
 // parts fold into the instruction's immediate offset) and a zero scalar
@@ -54,6 +55,22 @@ constexpr int kMaxStepsPerWave = 4;
 constexpr int kMaxParts = 8;        // partial sums of x in the multi-input form
 constexpr int kMaxStepsParts = 2;   // steps per wave in the multi-input form
 
+// Row-group modes of a workgroup of rpb row groups x wpr waves.
+enum RowGroupMode {
+  RG_INDEPENDENT = 0,   // every wave loads its gamma slice, every row group stores its scales
+  RG_SHARED_GAMMA = 1,  // row group 0 loads gamma and hands it to the others through LDS
+  RG_WIDE_SCALES = 2,   // RG_SHARED_GAMMA, and row group 0 stores the column-major scales of
+                        // the rpb consecutive rows of the workgroup with one store per group
+};
+constexpr int kNumModes = 3;
+constexpr int kMaxSharedSteps = 16;  // steps of gamma one workgroup can share (D <= 8192)
+constexpr int kMaxWideRows = 4;      // rows whose scales one wide store covers
+
+// Cache policy of the full-line output stores (residual_out, norm_out, codes):
+// sc1 | nt, written through L2 as streaming data.  Scale words keep the
+// default policy so that L2 merges neighbouring rows' words into whole sectors.
+constexpr int kStoreAux = 18;
+
 // Kernel arguments (element pointers; the kernels build buffer descriptors).
 struct KArgs {
   const uint16_t* x;
@@ -73,6 +90,7 @@ struct KArgs {
   int32_t remap;       // workgroup -> row-tile order, see tile_of_block
   int32_t remap_shift; // log2(remap) when remap >= 2 (remap is a power of two)
   int32_t wpr_magic;   // ceil(2^16 / wpr): wave / wpr == (wave * wpr_magic) >> 16 for wave < 64
+  int32_t wide_ok;     // RG_WIDE_SCALES: M % rpb == 0 and the scale pointer aligned to rpb words
   // Multi-input form only (fagq_rows_parts): x = x_parts[0] + ... + x_parts[nparts - 1].
   int32_t nparts;
   const uint16_t* xparts[kMaxParts];
@@ -239,6 +257,44 @@ __device__ __forceinline__ u32x2 encode8(const float (&t)[8]) {
   return out;
 }
 
+// Scale addressing of one wave, shared by the kernels and the host-side
+// diagnostic that checks it.  The wave's scale descriptor starts at the
+// scale of its first group g0 = c0 / G and ends just after the row's last
+// group: column-major scale[g * M + row] -> span (ng - 1) * M + 1 words,
+// row-major scale[row * groups + g] -> span ng words, ng = groups - g0.
+struct ScaleSpan {
+  int64_t base;          // element index of the descriptor's first word
+  uint32_t bytes;        // descriptor size in bytes
+  uint32_t ngroups;      // groups of the row at or after g0 (0: none)
+  uint32_t gstride;      // byte distance between consecutive groups of the row
+};
+
+__host__ __device__ inline ScaleSpan scale_span(int64_t M, int32_t groups, int col_major,
+                                                uint32_t sb, int64_t row, bool row_ok,
+                                                int g0, bool cols_ok) {
+  ScaleSpan r;
+  const int64_t rr = row_ok ? row : 0;
+  const uint32_t ng = row_ok && cols_ok ? (uint32_t)(groups - g0) : 0u;
+  r.base = col_major ? (int64_t)g0 * M + rr : rr * (int64_t)groups + g0;
+  const uint32_t span = col_major ? (ng ? (uint32_t)((int64_t)(ng - 1) * M + 1) : 0u) : ng;
+  r.bytes = span * sb;
+  r.ngroups = ng;
+  r.gstride = col_major ? (uint32_t)(M * (int64_t)sb) : sb;
+  return r;
+}
+
+// Byte offset (within the wave's scale descriptor) of the scale word that
+// lane group gl stores at step k.  Groups past the row's end get 0xffffffff,
+// which no descriptor reaches (scale spans are validated below 2^32 - 16), so
+// their stores are dropped; their in-range product g * gstride could wrap
+// past 2^32 into the descriptor.
+__host__ __device__ inline uint32_t scale_lane_offset(uint32_t gl, uint32_t k,
+                                                      uint32_t groups_per_step,
+                                                      uint32_t ngroups, uint32_t gstride) {
+  const uint32_t g = gl + k * groups_per_step;
+  return g < ngroups ? g * gstride : 0xffffffffu;
+}
+
 // ---------------------------------------------------------------- kernel
 
 // Row-invariant per-wave geometry.
@@ -252,7 +308,8 @@ struct WaveCtx {
 // Descriptors of one row for one wave.
 struct RowRsrc {
   rsrc_t x, res, res_out, norm, q, scale;
-  uint32_t scale_step;   // byte distance between the scales of consecutive steps
+  uint32_t ngroups;      // groups of the row this wave's scale descriptor covers
+  uint32_t gstride;      // byte distance between consecutive groups' scales
 };
 
 // The input descriptors (x, residual) are built first and their loads
@@ -277,16 +334,10 @@ __device__ __forceinline__ void row_rsrc_out(const KArgs& a, const WaveCtx& w, i
   r.res_out = make_rsrc(a.res_out + e, cols * 2u);
   if constexpr (NORM) r.norm = make_rsrc(a.norm_out + e, cols * 2u);
   r.q = make_rsrc(a.q + e, cols);
-  const int g0 = w.c0 / G;                                  // first group of this wave
-  const uint32_t ng = ok && w.cols ? (uint32_t)(a.groups - g0) : 0u;
-  // Column-major: scale[g * M + row]; this wave's groups start at g0 and the
-  // descriptor ends just after the row's last group.  Row-major:
-  // scale[row * groups + g].  Both are computed and one selected.
-  const bool col = a.col_major != 0;
-  const int64_t base = col ? (int64_t)g0 * a.M + rr : rr * (int64_t)a.groups + g0;
-  const uint32_t span = col ? (ng ? (uint32_t)((int64_t)(ng - 1) * a.M + 1) : 0u) : ng;
-  r.scale = make_rsrc(a.scale + base * sb, span * sb);
-  r.scale_step = (uint32_t)(kStepCols / G) * sb * (col ? (uint32_t)a.M : 1u);
+  const ScaleSpan sp = scale_span(a.M, a.groups, a.col_major, sb, row, ok, w.c0 / G, w.cols != 0);
+  r.scale = make_rsrc(a.scale + sp.base * sb, sp.bytes);
+  r.ngroups = sp.ngroups;
+  r.gstride = sp.gstride;
 }
 
 // Phase 1 for one row: issue the loads of x and residual for NS steps.
@@ -300,49 +351,67 @@ __device__ __forceinline__ void load_row(const RowRsrc& r, int lane, u32x4 (&xv)
   }
 }
 
-// Phase 2 for one row: r = x + residual, w = r * gamma, the fp64 sum of
-// squares, the group max of |w|; then the residual_out stores (after every
-// use of loaded data).  xs holds x in fp32 (one bf16 tensor, or the fp32 sum
-// of the partial tensors in the multi-input form).
-template <int NS, int LPG>
-__device__ __forceinline__ double row_in_f(const RowRsrc& rr, int lane, const float (&xs)[NS][8],
-                                           const u32x4 (&rv)[NS], const u32x4 (&gv)[NS],
-                                           float (&w)[NS][8], uint32_t (&gmax)[NS]) {
+// Gamma for this wave's columns (an L2 hit), NS steps.
+template <int NS>
+__device__ __forceinline__ void load_gamma(const KArgs& a, const WaveCtx& w, int lane,
+                                           u32x4 (&gv)[NS]) {
+  const rsrc_t rg = make_rsrc(a.gamma + w.c0, w.cols * 2u);
+#pragma unroll
+  for (int k = 0; k < NS; ++k)
+    gv[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, lane * 16 + k * 1024, 0, 0);
+}
+
+// Phase 2a for one row: r = x + residual into rw, the fp64 sum of squares, and
+// the residual_out stores (after every use of the loaded data).  xs holds x in
+// fp32 (one bf16 tensor, or the fp32 sum of the partial tensors in the
+// multi-input form).
+template <int NS>
+__device__ __forceinline__ double row_sum(const RowRsrc& rr, int lane, const float (&xs)[NS][8],
+                                          const u32x4 (&rv)[NS], float (&rw)[NS][8]) {
   double ss = 0.0;
   u32x4 ro[NS];
 #pragma unroll
   for (int k = 0; k < NS; ++k) {
-    float r[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      r[2 * j] = xs[k][2 * j] + bf16_lo(rv[k][j]);
-      r[2 * j + 1] = xs[k][2 * j + 1] + bf16_hi(rv[k][j]);
-      w[k][2 * j] = r[2 * j] * bf16_lo(gv[k][j]);
-      w[k][2 * j + 1] = r[2 * j + 1] * bf16_hi(gv[k][j]);
+      rw[k][2 * j] = xs[k][2 * j] + bf16_lo(rv[k][j]);
+      rw[k][2 * j + 1] = xs[k][2 * j + 1] + bf16_hi(rv[k][j]);
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const double rd = (double)r[j];
+      const double rd = (double)rw[k][j];
       ss = __builtin_fma(rd, rd, ss);   // r^2 is exact in fp64
     }
-    float m = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) m = __builtin_fmaxf(m, __builtin_fabsf(w[k][j]));
-    gmax[k] = group_max_bits<LPG>(__float_as_uint(m));
-#pragma unroll
-    for (int j = 0; j < 4; ++j) ro[k][j] = pack_bf16x2(r[2 * j], r[2 * j + 1]);
+    for (int j = 0; j < 4; ++j) ro[k][j] = pack_bf16x2(rw[k][2 * j], rw[k][2 * j + 1]);
   }
 #pragma unroll
   for (int k = 0; k < NS; ++k)
-    __builtin_amdgcn_raw_buffer_store_b128(ro[k], rr.res_out, lane * 16 + k * 1024, 0, kNonTemporal);
+    __builtin_amdgcn_raw_buffer_store_b128(ro[k], rr.res_out, lane * 16 + k * 1024, 0, kStoreAux);
   return ss;
 }
 
+// Phase 2b: w = r * gamma in place (rw holds r on entry, w on exit) and the
+// group maxima of |w|.
 template <int NS, int LPG>
-__device__ __forceinline__ double row_in(const RowRsrc& rr, int lane, const u32x4 (&xv)[NS],
-                                         const u32x4 (&rv)[NS], const u32x4 (&gv)[NS],
-                                         float (&w)[NS][8], uint32_t (&gmax)[NS]) {
-  float xs[NS][8];
+__device__ __forceinline__ void row_weight(float (&rw)[NS][8], const u32x4 (&gv)[NS],
+                                           uint32_t (&gmax)[NS]) {
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      rw[k][2 * j] = rw[k][2 * j] * bf16_lo(gv[k][j]);
+      rw[k][2 * j + 1] = rw[k][2 * j + 1] * bf16_hi(gv[k][j]);
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = __builtin_fmaxf(m, __builtin_fabsf(rw[k][j]));
+    gmax[k] = group_max_bits<LPG>(__float_as_uint(m));
+  }
+}
+
+template <int NS>
+__device__ __forceinline__ void unpack_x(const u32x4 (&xv)[NS], float (&xs)[NS][8]) {
 #pragma unroll
   for (int k = 0; k < NS; ++k)
 #pragma unroll
@@ -350,7 +419,6 @@ __device__ __forceinline__ double row_in(const RowRsrc& rr, int lane, const u32x
       xs[k][2 * j] = bf16_lo(xv[k][j]);
       xs[k][2 * j + 1] = bf16_hi(xv[k][j]);
     }
-  return row_in_f<NS, LPG>(rr, lane, xs, rv, gv, w, gmax);
 }
 
 // Multi-input form, phase 1: the row's partial tensors of x (the same row
@@ -404,22 +472,33 @@ __device__ __forceinline__ void sum_parts(int nparts, const u32x4 (&xv)[kMaxPart
   }
 }
 
-// Phase 4 for one row: scales, codes, optional norm_out.
-template <int NS, int LPG, int QF, int SF, bool NORM>
-__device__ __forceinline__ void row_out(const RowRsrc& rr, int lane, uint32_t scale_voff,
+// The scale of one group from its |w| maximum: fp32 s, or for UE8M0 the
+// exponent e = ceil(log2(s)) (at most 127).
+template <int SF>
+__device__ __forceinline__ float group_scale(uint32_t gmax_bits, float inv_q, int& e) {
+  const float s = __builtin_fmaxf(__uint_as_float(gmax_bits) * inv_q, 1.0e-12f);
+  if constexpr (SF == SF_UE8M0) {
+    e = ceil_log2_bits(s);
+    e = e > 127 ? 127 : e;
+  }
+  return s;
+}
+
+// Phase 4 for one row: codes, optional norm_out and, with STORE_SCALES, the
+// scales (every lane of a group stores the group's scale to the same
+// address, one write after coalescing; groups past the row end get an
+// offset outside the descriptor and are dropped).
+template <int NS, int LPG, int QF, int SF, bool NORM, bool STORE_SCALES = true>
+__device__ __forceinline__ void row_out(const RowRsrc& rr, int lane, uint32_t gl,
                                         const float (&w)[NS][8], const uint32_t (&gmax)[NS],
                                         float inv, float inv_q) {
+  constexpr uint32_t GPS = kStepCols / (LPG * 8);
 #pragma unroll
   for (int k = 0; k < NS; ++k) {
-    const float s = __builtin_fmaxf(__uint_as_float(gmax[k]) * inv_q, 1.0e-12f);
-    float mul = 0.0f;
     int e = 0;
-    if constexpr (SF == SF_F32) {
-      mul = 1.0f / s;
-    } else {
-      e = ceil_log2_bits(s);
-      e = e > 127 ? 127 : e;
-    }
+    const float s = group_scale<SF>(gmax[k], inv_q, e);
+    float mul = 0.0f;
+    if constexpr (SF == SF_F32) mul = 1.0f / s;
     // No clamp to [-QMAX, QMAX]: for finite inputs |t| <= QMAX * (1 + 5 * 2^-24)
     // (|n| <= gmax * inv and s >= gmax * inv / QMAX, each up to a few
     // roundings), and fp8 rounds everything below 464 to at most 448, int8
@@ -435,19 +514,16 @@ __device__ __forceinline__ void row_out(const RowRsrc& rr, int lane, uint32_t sc
       u32x4 no;
 #pragma unroll
       for (int j = 0; j < 4; ++j) no[j] = pack_bf16x2(n[2 * j], n[2 * j + 1]);
-      __builtin_amdgcn_raw_buffer_store_b128(no, rr.norm, lane * 16 + k * 1024, 0, kNonTemporal);
+      __builtin_amdgcn_raw_buffer_store_b128(no, rr.norm, lane * 16 + k * 1024, 0, kStoreAux);
     }
     const u32x2 codes = encode8<QF>(t);
-    __builtin_amdgcn_raw_buffer_store_b64(codes, rr.q, lane * 8 + k * 512, 0, kNonTemporal);
-    // Every lane of a group stores the group's scale to the same address (one
-    // write after coalescing); groups past the row end fall outside the
-    // descriptor and are dropped.
-    if constexpr (SF == SF_F32) {
-      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(s), rr.scale,
-                                            scale_voff + k * rr.scale_step, 0, 0);
-    } else {
-      __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(e + 127), rr.scale,
-                                           scale_voff + k * rr.scale_step, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b64(codes, rr.q, lane * 8 + k * 512, 0, kStoreAux);
+    if constexpr (STORE_SCALES) {
+      const uint32_t off = scale_lane_offset(gl, (uint32_t)k, GPS, rr.ngroups, rr.gstride);
+      if constexpr (SF == SF_F32)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(s), rr.scale, off, 0, 0);
+      else
+        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(e + 127), rr.scale, off, 0, 0);
     }
   }
 }
@@ -485,17 +561,37 @@ __device__ __forceinline__ void row_scale(double ss, const KArgs& a, int wave, i
   }
 }
 
-// Workgroup = rpb row groups of wpr waves.  Row group j of workgroup b owns
-// rows [(b * rpb + j) * RSEQ, ... + RSEQ) and processes them one after the
-// other (RSEQ is unrolled, so every wait for a load is exact).
-template <int NS, int LPG, int QF, int SF, bool NORM, int RSEQ>
+// Workgroup = rpb row groups of wpr waves; row group j of workgroup b owns
+// row b * rpb + j.  MODE (RowGroupMode) selects how the row groups share
+// gamma and store the scales:
+//   RG_INDEPENDENT: each wave loads its gamma slice and computes w = r * gamma
+//     before the row's reduction; each row group stores its own scales.
+//   RG_SHARED_GAMMA: only row group 0 loads gamma; it leaves its slices in
+//     LDS, and the other row groups compute w after the first barrier (the
+//     values and the operation order are the same, only the time differs).
+//   RG_WIDE_SCALES: as RG_SHARED_GAMMA, and the group maxima of every row go
+//     to LDS, so that after the second barrier row group 0 evaluates the
+//     scales of all rpb rows (the same expression each row would evaluate) and
+//     stores each group's rpb consecutive column-major words with one store.
+//     A workgroup whose rows would pass M, or a call whose scale pointer or M
+//     does not allow the wide alignment (wide_ok == 0), stores row by row.
+template <int NS, int LPG, int QF, int SF, bool NORM, int MODE>
 __global__ void __launch_bounds__(1024)
 fagq_rows(const KArgs a) {
   static_assert(NS >= 1 && NS <= kMaxStepsPerWave, "steps per wave");
+  static_assert(MODE >= 0 && MODE < kNumModes, "row-group mode");
   constexpr int G = LPG * 8;
+  constexpr int GPS = kStepCols / G;    // groups per step
   constexpr uint32_t sb = SF == SF_F32 ? 4u : 1u;
+  constexpr bool SHARED = MODE != RG_INDEPENDENT;
+  constexpr bool WIDE = MODE == RG_WIDE_SCALES;
+  constexpr float QMAX = (QF == QF_FP8) ? 448.0f : 127.0f;
   __shared__ double s_part[kMaxWavesPerBlock];
   __shared__ float s_inv[kMaxWavesPerBlock][2];
+  // Shared modes only (the arrays are not allocated otherwise): gamma slices
+  // [step of the row][lane], and the group maxima [row group][group].
+  __shared__ u32x4 s_gamma[SHARED ? kMaxSharedSteps * 64 : 1];
+  __shared__ uint32_t s_gmax[WIDE ? kMaxWideRows : 1][WIDE ? kMaxSharedSteps * GPS : 1];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -504,49 +600,127 @@ fagq_rows(const KArgs a) {
   // Row group within the workgroup and wave within the row (wpr * rpb waves).
   const int rib = (wave * a.wpr_magic) >> 16;
   const int part = wave - rib * wpr;
-  const int64_t row0 = ((int64_t)blk * a.rpb + rib) * RSEQ;
+  const int64_t row0 = (int64_t)blk * a.rpb;
+  const int64_t row = row0 + rib;
   WaveCtx wc;
   wc.lane = lane;
   wc.c0 = part * (NS * kStepCols);
   wc.cols = a.D > wc.c0 ? (uint32_t)(a.D - wc.c0) : 0u;
   wc.gl = lane / LPG;
-  const uint32_t scale_voff =
-      (uint32_t)wc.gl * (a.col_major ? (uint32_t)(a.M * (int64_t)sb) : sb);
+  const int g0 = wc.c0 / G;
 
-  // The first row's inputs go out first, then gamma for this wave's columns
-  // (an L2 hit, needed at the same time; loaded once for all RSEQ rows), then
-  // the output descriptors are computed.
+  // The row's inputs go out first, then gamma for this wave's columns (an L2
+  // hit, needed at the same time), then the output descriptors are computed.
   u32x4 xv[NS], rv[NS];
   RowRsrc rr;
-  row_rsrc_in(a, wc, row0, rr);
+  row_rsrc_in(a, wc, row, rr);
   load_row<NS>(rr, lane, xv, rv);
+  const bool gamma_loader = !SHARED || rib == 0;
   u32x4 gv[NS];
+  if (gamma_loader) load_gamma<NS>(a, wc, lane, gv);
+  row_rsrc_out<SF, NORM>(a, wc, row, G, rr);
+
+  float w[NS][8];
+  uint32_t gmax[NS];
+  double ss;
   {
-    const rsrc_t rg = make_rsrc(a.gamma + wc.c0, wc.cols * 2u);
-#pragma unroll
-    for (int k = 0; k < NS; ++k)
-      gv[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, lane * 16 + k * 1024, 0, 0);
+    float xs[NS][8];
+    unpack_x<NS>(xv, xs);
+    ss = row_sum<NS>(rr, lane, xs, rv, w);
   }
-  row_rsrc_out<SF, NORM>(a, wc, row0, G, rr);
-
+  auto publish_gmax = [&](int rg) {
+    if ((lane & (LPG - 1)) == 0) {
 #pragma unroll
-  for (int i = 0; i < RSEQ; ++i) {
-    float w[NS][8];
-    uint32_t gmax[NS];
-    double ss = row_in<NS, LPG>(rr, lane, xv, rv, gv, w, gmax);
-    RowRsrc rn;
-    if (i + 1 < RSEQ) {
-      // The next row's inputs go out now, behind this row's reduction and stores.
-      row_rsrc_in(a, wc, row0 + i + 1, rn);
-      load_row<NS>(rn, lane, xv, rv);
-      row_rsrc_out<SF, NORM>(a, wc, row0 + i + 1, G, rn);
+      for (int k = 0; k < NS; ++k) {
+        const int g = g0 + k * GPS + wc.gl;
+        if (g < a.groups) s_gmax[rg][g] = gmax[k];
+      }
     }
+  };
+  if (gamma_loader) {
+    row_weight<NS, LPG>(w, gv, gmax);
+    if constexpr (SHARED) {
+#pragma unroll
+      for (int k = 0; k < NS; ++k) s_gamma[(part * NS + k) * 64 + lane] = gv[k];
+      if constexpr (WIDE) publish_gmax(0);
+    }
+  }
 
-    float inv, inv_q;
-    row_scale<QF>(ss, a, wave, rib, part, wpr, lane, s_part, s_inv, inv, inv_q);
+  // The row's sum of squares: with several waves per row (or shared gamma),
+  // the row's first wave adds the partial sums in wave order and evaluates
+  // inv_rms once; a second barrier hands it to the others.  Both barriers
+  // are fenced for LDS only, so no global store has to complete before them.
+  float inv, inv_q;
+  ss = wave_sum(ss);
+  if (wpr > 1 || SHARED) {
+    if (lane == 0) s_part[wave] = ss;
+    lds_barrier();
+    if (SHARED && !gamma_loader) {
+#pragma unroll
+      for (int k = 0; k < NS; ++k) gv[k] = s_gamma[(part * NS + k) * 64 + lane];
+      row_weight<NS, LPG>(w, gv, gmax);
+      if constexpr (WIDE) publish_gmax(rib);
+    }
+    if (part == 0) {
+      double t = 0.0;
+      for (int p = 0; p < wpr; ++p) t += s_part[rib * wpr + p];
+      const float v = row_inv_rms(t, a.D, a.eps);
+      if (lane == 0) {
+        s_inv[rib][0] = v;
+        s_inv[rib][1] = v / QMAX;
+      }
+    }
+    lds_barrier();
+    inv = s_inv[rib][0];
+    inv_q = s_inv[rib][1];
+  } else {
+    inv = row_inv_rms(ss, a.D, a.eps);
+    inv_q = inv / QMAX;
+  }
 
-    row_out<NS, LPG, QF, SF, NORM>(rr, lane, scale_voff, w, gmax, inv, inv_q);
-    if (i + 1 < RSEQ) rr = rn;
+  if constexpr (WIDE) {
+    const int R = a.rpb;
+    const bool wide = a.wide_ok && row0 + R <= a.M;
+    if (wide) {
+      row_out<NS, LPG, QF, SF, NORM, false>(rr, lane, (uint32_t)wc.gl, w, gmax, inv, inv_q);
+      if (rib == 0 && (lane & (LPG - 1)) == 0) {
+        // Scale words g * M + row0 .. + R - 1, offsets below M * groups * sb.
+        const rsrc_t rs = make_rsrc(a.scale, (uint32_t)(a.M * a.groups * (int64_t)sb));
+#pragma unroll
+        for (int k = 0; k < NS; ++k) {
+          const int g = g0 + k * GPS + wc.gl;
+          if (g < a.groups) {
+            uint32_t v[kMaxWideRows];
+#pragma unroll
+            for (int j = 0; j < kMaxWideRows; ++j) {
+              v[j] = 0u;
+              if (j < R) {
+                int e = 0;
+                const float sj = group_scale<SF>(s_gmax[j][g], s_inv[j][1], e);
+                v[j] = SF == SF_F32 ? __float_as_uint(sj) : (uint32_t)(e + 127);
+              }
+            }
+            const uint32_t off = (uint32_t)(((int64_t)g * a.M + row0) * sb);
+            if constexpr (SF == SF_F32) {
+              if (R == 2)
+                __builtin_amdgcn_raw_buffer_store_b64(u32x2{v[0], v[1]}, rs, off, 0, 0);
+              else
+                __builtin_amdgcn_raw_buffer_store_b128(u32x4{v[0], v[1], v[2], v[3]}, rs, off, 0, 0);
+            } else {
+              if (R == 2)
+                __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(v[0] | (v[1] << 8)), rs, off, 0, 0);
+              else
+                __builtin_amdgcn_raw_buffer_store_b32(v[0] | (v[1] << 8) | (v[2] << 16) | (v[3] << 24),
+                                                      rs, off, 0, 0);
+            }
+          }
+        }
+      }
+    } else {
+      row_out<NS, LPG, QF, SF, NORM>(rr, lane, (uint32_t)wc.gl, w, gmax, inv, inv_q);
+    }
+  } else {
+    row_out<NS, LPG, QF, SF, NORM>(rr, lane, (uint32_t)wc.gl, w, gmax, inv, inv_q);
   }
 }
 
@@ -560,7 +734,6 @@ __global__ void __launch_bounds__(1024)
 fagq_rows_parts(const KArgs a) {
   static_assert(NS >= 1 && NS <= kMaxStepsParts, "steps per wave");
   constexpr int G = LPG * 8;
-  constexpr uint32_t sb = SF == SF_F32 ? 4u : 1u;
   __shared__ double s_part[kMaxWavesPerBlock];
   __shared__ float s_inv[kMaxWavesPerBlock][2];
 
@@ -576,37 +749,36 @@ fagq_rows_parts(const KArgs a) {
   wc.c0 = part * (NS * kStepCols);
   wc.cols = a.D > wc.c0 ? (uint32_t)(a.D - wc.c0) : 0u;
   wc.gl = lane / LPG;
-  const uint32_t scale_voff =
-      (uint32_t)wc.gl * (a.col_major ? (uint32_t)(a.M * (int64_t)sb) : sb);
 
   u32x4 xv[kMaxParts][NS], rv[NS];
   RowRsrc rr;
   row_rsrc_in(a, wc, row, rr);
   load_row_parts<NS>(a, wc, row, rr, lane, xv, rv);
   u32x4 gv[NS];
-  {
-    const rsrc_t rg = make_rsrc(a.gamma + wc.c0, wc.cols * 2u);
-#pragma unroll
-    for (int k = 0; k < NS; ++k)
-      gv[k] = __builtin_amdgcn_raw_buffer_load_b128(rg, lane * 16 + k * 1024, 0, 0);
-  }
+  load_gamma<NS>(a, wc, lane, gv);
   row_rsrc_out<SF, false>(a, wc, row, G, rr);
 
-  float xs[NS][8];
-  sum_parts<NS>(a.nparts, xv, xs);
   float w[NS][8];
   uint32_t gmax[NS];
-  const double ss = row_in_f<NS, LPG>(rr, lane, xs, rv, gv, w, gmax);
+  double ss;
+  {
+    float xs[NS][8];
+    sum_parts<NS>(a.nparts, xv, xs);
+    ss = row_sum<NS>(rr, lane, xs, rv, w);
+  }
+  row_weight<NS, LPG>(w, gv, gmax);
   float inv, inv_q;
   row_scale<QF>(ss, a, wave, rib, part, wpr, lane, s_part, s_inv, inv, inv_q);
-  row_out<NS, LPG, QF, SF, false>(rr, lane, scale_voff, w, gmax, inv, inv_q);
+  row_out<NS, LPG, QF, SF, false>(rr, lane, (uint32_t)wc.gl, w, gmax, inv, inv_q);
 }
 
 // ---------------------------------------------------------------- diagnostics
 
 // Encodes already-scaled fp32 values with the same device encoder as the
-// operator (after the same clamp), 8 per thread.  n % 8 == 0.
-template <int QF>
+// operator, 8 per thread, n % 8 == 0.  CLAMP applies the reference's clamp to
+// [-QMAX, QMAX] first; without it the values reach the encoder as the
+// operator's kernels pass them (they skip the clamp, see row_out).
+template <int QF, bool CLAMP>
 __global__ void __launch_bounds__(256) fagq_encode(const float* __restrict__ in,
                                                    u32x2* __restrict__ out, int64_t n8) {
   constexpr float QMAX = (QF == QF_FP8) ? 448.0f : 127.0f;
@@ -614,7 +786,8 @@ __global__ void __launch_bounds__(256) fagq_encode(const float* __restrict__ in,
   if (i >= n8) return;
   float t[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) t[j] = __builtin_fminf(__builtin_fmaxf(in[i * 8 + j], -QMAX), QMAX);
+  for (int j = 0; j < 8; ++j)
+    t[j] = CLAMP ? __builtin_fminf(__builtin_fmaxf(in[i * 8 + j], -QMAX), QMAX) : in[i * 8 + j];
   out[i] = encode8<QF>(t);
 }
 

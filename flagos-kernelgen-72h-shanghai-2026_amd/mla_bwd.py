@@ -38,6 +38,20 @@ def workspace_bytes(B: int, S: int, D: int) -> int:
     return n
 
 
+def check_workspace(workspace: torch.Tensor, need: int, dev: torch.device) -> None:
+    """A caller's workspace must be a contiguous tensor on ``dev`` whose own bytes
+    and whose storage past its offset both hold ``need`` bytes: the kernels write
+    ``need`` contiguous bytes from ``data_ptr()``, so a strided or expanded view
+    would let them write outside the view or its storage."""
+    if workspace.device != dev or not workspace.is_contiguous():
+        raise ValueError(f"workspace must be a contiguous tensor on {dev}")
+    nbytes = workspace.numel() * workspace.element_size()
+    room = (workspace.untyped_storage().nbytes()
+            - workspace.storage_offset() * workspace.element_size())
+    if min(nbytes, room) < need:
+        raise ValueError(f"workspace must hold {need} bytes on {dev}, got {min(nbytes, room)}")
+
+
 def mla_bwd_nope_dkdv(q: torch.Tensor, c_kv: torch.Tensor, out: torch.Tensor, do: torch.Tensor,
                       lse: torch.Tensor, dq: torch.Tensor, dc_kv: torch.Tensor, sm_scale: float,
                       workspace: torch.Tensor | None = None):
@@ -65,8 +79,8 @@ def mla_bwd_nope_dkdv(q: torch.Tensor, c_kv: torch.Tensor, out: torch.Tensor, do
     need = workspace_bytes(B, S, D)
     if workspace is None:
         workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
-    elif workspace.device != dev or workspace.numel() * workspace.element_size() < need:
-        raise ValueError(f"workspace must hold {need} bytes on {dev}")
+    else:
+        check_workspace(workspace, need, dev)
     lib = _lib.load()
     P = lambda t: ctypes.c_void_p(t.data_ptr())
     with torch.cuda.device(dev):

@@ -32,23 +32,23 @@ _FP8 = torch.float8_e4m3fn
 
 
 def _q_format(x_q: torch.Tensor) -> int:
-    if x_q.dtype == torch.int8:
-        return _lib.Q_INT8
-    if x_q.dtype == _FP8:
+    if x_q.dtype is _FP8:
         return _lib.Q_FP8_E4M3FN
+    if x_q.dtype is torch.int8:
+        return _lib.Q_INT8
     raise TypeError(f"x_q must be int8 or float8_e4m3fn, got {x_q.dtype}")
 
 
 def _scale_format(x_scale: torch.Tensor) -> int:
-    if x_scale.dtype == torch.float32:
+    if x_scale.dtype is torch.float32:
         return _lib.SCALE_F32
-    if x_scale.dtype == torch.uint8:
+    if x_scale.dtype is torch.uint8:
         return _lib.SCALE_UE8M0
     raise TypeError(f"x_scale must be float32 or uint8 (ue8m0), got {x_scale.dtype}")
 
 
 def _scale_layout(x_scale: torch.Tensor, M: int, groups: int) -> int:
-    if tuple(x_scale.shape) != (M, groups):
+    if x_scale.shape != (M, groups):
         raise ValueError(f"x_scale must have shape ({M}, {groups}), got {tuple(x_scale.shape)}")
     if x_scale.is_contiguous():
         return _lib.LAYOUT_ROW_MAJOR
@@ -85,6 +85,37 @@ def _ptr(t: torch.Tensor | None):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+# Per-call host work is what bounds decode-sized calls (the kernel takes about
+# 3 us), so the hot path reads the current device and stream through torch's
+# raw accessors (no torch.device / Stream objects), enters a device guard only
+# when the tensors are not on the current device, and checks each tensor with
+# one combined test, falling back to the detailed checks only to word the error.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_raw_device = getattr(torch._C, "_cuda_getDevice", None)
+
+
+def _current_stream(dev: int) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(dev)
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _is_current(dev: int) -> bool:
+    return (_raw_device() if _raw_device is not None else torch.cuda.current_device()) == dev
+
+
+def _rows_ok(t, shape, dev: int) -> bool:
+    return (t.dtype is _BF16 and t.shape == shape and t.get_device() == dev
+            and t.is_contiguous())
+
+
+def _launch(fn, dev: int, args) -> int:
+    if _is_current(dev):
+        return fn(*args, _current_stream(dev))
+    with torch.cuda.device(dev):
+        return fn(*args, _current_stream(dev))
+
+
 def fused_add_rmsnorm_group_quant(
     x: torch.Tensor,
     residual: torch.Tensor,
@@ -106,36 +137,42 @@ def fused_add_rmsnorm_group_quant(
     """
     if x.dim() != 2:
         raise ValueError(f"x must be 2-D [M, D], got shape {tuple(x.shape)}")
-    M, D = (int(s) for s in x.shape)
-    if not x.is_cuda:
+    shape = x.shape
+    M, D = int(shape[0]), int(shape[1])
+    dev = x.get_device()
+    if dev < 0:
         raise ValueError("x must be a GPU (HIP) tensor; this operator has no CPU path")
-    device = x.device
-    _check_rows("x", x, (M, D), device)
-    _check_rows("residual", residual, (M, D), device)
-    _check_rows("gamma", gamma, (D,), device)
-    _check_rows("residual_out", residual_out, (M, D), device)
-    if norm_out is not None:
-        _check_rows("norm_out", norm_out, (M, D), device)
+    if not (_rows_ok(x, shape, dev) and _rows_ok(residual, shape, dev)
+            and _rows_ok(residual_out, shape, dev)
+            and (norm_out is None or _rows_ok(norm_out, shape, dev))
+            and gamma.dtype is _BF16 and gamma.shape == (D,) and gamma.get_device() == dev
+            and gamma.is_contiguous()):
+        device = x.device
+        _check_rows("x", x, (M, D), device)
+        _check_rows("residual", residual, (M, D), device)
+        _check_rows("gamma", gamma, (D,), device)
+        _check_rows("residual_out", residual_out, (M, D), device)
+        if norm_out is not None:
+            _check_rows("norm_out", norm_out, (M, D), device)
     group_size = int(group_size)
     if group_size <= 0 or D % group_size != 0:
         raise ValueError(f"group_size {group_size} must divide D = {D}")
     qf = _q_format(x_q)
-    if x_q.device != device or tuple(x_q.shape) != (M, D) or not x_q.is_contiguous():
-        raise ValueError(f"x_q must be a contiguous ({M}, {D}) tensor on {device}")
-    if x_scale.device != device:
-        raise ValueError(f"x_scale is on {x_scale.device}, expected {device}")
+    if x_q.shape != shape or x_q.get_device() != dev or not x_q.is_contiguous():
+        raise ValueError(f"x_q must be a contiguous ({M}, {D}) tensor on {x.device}")
+    if x_scale.get_device() != dev:
+        raise ValueError(f"x_scale is on {x_scale.device}, expected {x.device}")
     sf = _scale_format(x_scale)
     layout = _scale_layout(x_scale, M, D // group_size)
     rnd = _rounding(rounding, qf)
     if M == 0:
         return residual_out, norm_out, x_q, x_scale
-    lib = _lib.load()
-    stream = torch.cuda.current_stream(device).cuda_stream
-    with torch.cuda.device(device):
-        st = lib.fagq_launch(_ptr(x), _ptr(residual), _ptr(gamma), _ptr(residual_out),
-                             _ptr(norm_out), _ptr(x_q), _ptr(x_scale), M, D, group_size,
-                             float(eps), qf, sf, layout, rnd, ctypes.c_void_p(stream))
-    _lib.check(st)
+    st = _launch(_lib.load().fagq_launch, dev,
+                 (x.data_ptr(), residual.data_ptr(), gamma.data_ptr(), residual_out.data_ptr(),
+                  None if norm_out is None else norm_out.data_ptr(), x_q.data_ptr(),
+                  x_scale.data_ptr(), M, D, group_size, float(eps), qf, sf, layout, rnd))
+    if st:
+        _lib.check(st)
     return residual_out, norm_out, x_q, x_scale
 
 
@@ -228,18 +265,18 @@ def fused_reduce_add_rmsnorm_group_quant(
     rnd = _rounding(None if out_dtype == _FP8 else rounding, qf)
     if M == 0:
         return residual_out, q, scale
-    lib = _lib.load()
     arr = (ctypes.c_void_p * len(parts))(*[t.data_ptr() for t in parts])
-    stream = torch.cuda.current_stream(device).cuda_stream
-    with torch.cuda.device(device):
-        st = lib.fagq_launch_parts(ctypes.cast(arr, ctypes.c_void_p), len(parts), _ptr(residual),
-                                   _ptr(weight), _ptr(residual_out), _ptr(q), _ptr(scale), M, D,
-                                   group_size, float(eps), qf, sf, layout, rnd,
-                                   ctypes.c_void_p(stream))
+    st = _launch(_lib.load().fagq_launch_parts, x0.get_device(),
+                 (ctypes.cast(arr, ctypes.c_void_p), len(parts), residual.data_ptr(),
+                  weight.data_ptr(), residual_out.data_ptr(), q.data_ptr(), scale.data_ptr(), M, D,
+                  group_size, float(eps), qf, sf, layout, rnd))
     _lib.check(st, "fagq_launch_parts")
     return residual_out, q, scale
 
 
-def route_for(M: int, D: int, group_size: int = 128) -> dict:
-    """The launch mapping the library chooses for a shape."""
-    return _lib.query_route(M, D, group_size)
+def route_for(M: int, D: int, group_size: int = 128, *, scale_ue8m0: bool = False,
+              scale_col_major: bool = False) -> dict:
+    """The launch mapping the library chooses for a shape and scale format."""
+    return _lib.query_route(M, D, group_size,
+                            _lib.SCALE_UE8M0 if scale_ue8m0 else _lib.SCALE_F32,
+                            _lib.LAYOUT_COL_MAJOR if scale_col_major else _lib.LAYOUT_ROW_MAJOR)

@@ -140,22 +140,26 @@ FAGQ_API int fagq_launch_parts(const void* const* x_parts, int nparts, const voi
                                int q_format, int scale_format, int scale_layout, int rounding,
                                void* stream);
 
-/* Route description chosen by fagq_launch for a shape (for tests and the
- * benchmark).  waves_per_row * steps_per_wave * 512 >= D. */
+/* Route description chosen by fagq_launch for a shape and scale format (for
+ * tests and the benchmark).  waves_per_row * steps_per_wave * 512 >= D. */
 typedef struct fagq_route {
   int32_t waves_per_row;    /* waves that split one row (1 = wave-per-row) */
   int32_t steps_per_wave;   /* 512-column steps each wave keeps in VGPRs */
-  int32_t rows_per_block;   /* row groups (of waves_per_row waves) per workgroup */
-  int32_t rows_in_sequence; /* consecutive rows each row group processes in turn */
+  int32_t rows_per_block;   /* rows (row groups of waves_per_row waves) per workgroup */
+  int32_t row_group_mode;   /* 0: independent rows; 1: gamma loaded once per workgroup and
+                               shared through LDS; 2: as 1, and the column-major scales of
+                               the workgroup's rows stored together */
   int32_t block_threads;    /* workgroup size */
-  int32_t reserved;         /* zero */
+  int32_t lds_bytes;        /* dynamic LDS reserved per workgroup (0: none) */
   int64_t grid_blocks;      /* workgroups launched */
+  int32_t xcd_remap;        /* workgroup -> row order (see fagq_launch_mapped) */
+  int32_t reserved;         /* zero */
 } fagq_route;
 
 /* Same validation as fagq_launch for the shape arguments; fills *route.
  * Never touches the device. */
-FAGQ_API int fagq_query_route(int64_t M, int64_t D, int64_t group_size,
-                              fagq_route* route);
+FAGQ_API int fagq_query_route(int64_t M, int64_t D, int64_t group_size, int scale_format,
+                              int scale_layout, fagq_route* route);
 
 /* Static description of a status code; never NULL. */
 FAGQ_API const char* fagq_status_string(int status);

@@ -22,18 +22,23 @@ extern "C" {
 /* fagq_launch with an explicit mapping instead of the route table:
  * waves_per_row in [1, 16], rows_per_block >= 1 with
  * waves_per_row * rows_per_block <= 16, steps per wave
- * ceil(ceil(D / 512) / waves_per_row) <= 16 and, when that exceeds 4,
- * waves_per_row * rows_per_block <= 4; rows_in_sequence in [1, 64] rows
- * per row group, processed in turn.  xcd_remap selects the workgroup ->
- * row-tile order: 0 dispatch order, 1 one contiguous range of tiles per XCD,
- * n in {2, 4, .., 64} chunks of n consecutive tiles per XCD.  Returns
- * FAGQ_E_FORMAT for an invalid mapping. */
+ * ceil(ceil(D / 512) / waves_per_row) <= 4.  row_group_mode: 0 independent
+ * rows; 1 gamma loaded by the workgroup's first row and shared through LDS;
+ * 2 as 1, and the first row's waves store each group's column-major scales of
+ * all rows_per_block rows with one store (column-major scales only,
+ * rows_per_block 2 or 4).  Modes 1 and 2 need
+ * waves_per_row * steps per wave <= 16 (D <= 8192).  xcd_remap selects the
+ * workgroup -> row-tile order: 0 dispatch order, 1 one contiguous range of
+ * tiles per XCD, n in {2, 4, .., 64} chunks of n consecutive tiles per XCD.
+ * lds_bytes in [0, 65536] of dynamic LDS is reserved per workgroup (the kernel
+ * does not use it; it caps the workgroups resident per CU).  Every mapping
+ * gives the same bits.  Returns FAGQ_E_FORMAT for an invalid mapping. */
 FAGQ_API int fagq_launch_mapped(const void* x, const void* residual, const void* gamma,
                                 void* residual_out, void* norm_out, void* q, void* scale,
                                 int64_t M, int64_t D, int64_t group_size, float eps,
                                 int q_format, int scale_format, int scale_layout,
                                 int rounding, int waves_per_row, int rows_per_block,
-                                int rows_in_sequence, int xcd_remap, void* stream);
+                                int row_group_mode, int xcd_remap, int lds_bytes, void* stream);
 
 /* fagq_gemm_launch with the tile width forced: block_n 192 or 256 columns
  * of C per workgroup (0: the shape's own choice, as fagq_gemm_launch).  Any
@@ -46,14 +51,37 @@ FAGQ_API int fagq_gemm_launch_mapped(const void* a_q, const void* a_scale, const
                                      int b_scale_format, int block_n, void* stream);
 
 /* Encodes n fp32 values (n % 8 == 0, 16-byte aligned) with the operator's
- * device encoder, after a clamp to [-QMAX, QMAX] (which the operator itself
- * never needs: its values are within that range): one byte per value. */
+ * device encoder: one byte per value.  clamp = 1 applies the reference's
+ * clamp to [-QMAX, QMAX] first; clamp = 0 passes the values unclamped, as the
+ * operator's kernels do (their values stay below QMAX * (1 + 5 * 2^-24)). */
 FAGQ_API int fagq_diag_encode(const float* in, void* out, int64_t n, int q_format,
-                              int rounding, void* stream);
+                              int rounding, int clamp, void* stream);
 
-/* Copies `bytes` (a multiple of 16, both pointers 16-byte aligned) with a
- * plain 16-byte-vector streaming kernel. */
+/* HBM ceiling probes with the operator's cache policies (non-temporal loads,
+ * sc1 | nt stores), one 16-byte chunk per thread, 512 threads per
+ * workgroup.  `bytes` is a multiple of 16, pointers 16-byte aligned.
+ *   FAGQ_STREAM_COPY   reads src, writes dst (bytes each)
+ *   FAGQ_STREAM_READ   reads src; dst (>= 16 bytes) is written only if a
+ *                      chunk's four words XOR to 0x9e3779b9
+ *   FAGQ_STREAM_WRITE  writes dst; src may be NULL */
+enum fagq_stream_mode { FAGQ_STREAM_COPY = 0, FAGQ_STREAM_READ = 1, FAGQ_STREAM_WRITE = 2 };
+
+FAGQ_API int fagq_diag_stream(const void* src, void* dst, int64_t bytes, int mode, void* stream);
+
+/* fagq_diag_stream(src, dst, bytes, FAGQ_STREAM_COPY, stream): the copy of
+ * known size that HBM byte counters are calibrated against. */
 FAGQ_API int fagq_diag_copy(const void* src, void* dst, int64_t bytes, void* stream);
+
+/* Host-side check of the operator's per-lane scale addressing, computed by
+ * the same functions the kernels use: for row `row` of an [M, D] call split
+ * over waves_per_row waves (one row per workgroup), writes for every wave,
+ * step and lane out[(wave * steps_per_wave + step) * 64 + lane] = the scale
+ * element index that lane's store reaches, or -1 when the buffer descriptor
+ * drops it.  cap >= waves_per_row * steps_per_wave * 64.  Never touches the
+ * device. */
+FAGQ_API int fagq_diag_scale_offsets(int64_t M, int64_t D, int64_t group_size, int scale_format,
+                                     int scale_layout, int waves_per_row, int64_t row,
+                                     int64_t* out, int64_t cap);
 
 /* Issue-rate probe of the fp8 GEMM's matrix instruction: `blocks`
  * workgroups of 4 waves (1 <= blocks <= 2^20), each wave issuing iters x 8

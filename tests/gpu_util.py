@@ -45,17 +45,23 @@ def to_numpy(ro, q, sc, norm, col):
 
 
 def run_gpu(pkg, dev, x, r, g, G, fmt, ue8m0=False, col=False, eps=1e-6, with_norm=False,
-            mapping=None, inplace=False, stream=None):
+            mapping=None, inplace=False, stream=None, scale_offset=0):
     """Runs the library on cuda tensors copied from the CPU inputs.
-    mapping = (waves_per_row, rows_per_block, rows_in_sequence, xcd_remap) forces a launch
-    mapping through fagq_launch_mapped; otherwise the public Python operator
-    (reference signature) is used."""
+    mapping = (waves_per_row, rows_per_block, row_group_mode, xcd_remap[, lds_bytes]) forces a
+    launch mapping through fagq_launch_mapped; otherwise the public Python operator
+    (reference signature) is used.  scale_offset > 0 places the scales that many
+    elements past an aligned allocation (a misaligned scale pointer)."""
     qdt, rnd, _, _ = FMTS[fmt]
     M, D = x.shape
     xd, rd, gd = x.to(dev), r.to(dev), g.to(dev)
     ro = rd if inplace else torch.empty_like(rd)
     q = torch.empty((M, D), dtype=qdt, device=dev)
-    sc = pkg.empty_scales(M, D // G, ue8m0=ue8m0, col_major=col, device=dev)
+    if scale_offset:
+        dt = torch.uint8 if ue8m0 else torch.float32
+        buf = torch.empty(M * (D // G) + scale_offset, dtype=dt, device=dev)[scale_offset:]
+        sc = buf.view(D // G, M).t() if col else buf.view(M, D // G)
+    else:
+        sc = pkg.empty_scales(M, D // G, ue8m0=ue8m0, col_major=col, device=dev)
     norm = torch.empty_like(xd) if with_norm else None
     if mapping is None:
         ctx = torch.cuda.stream(stream) if stream is not None else torch.cuda.stream(torch.cuda.current_stream(dev))
@@ -64,14 +70,15 @@ def run_gpu(pkg, dev, x, r, g, G, fmt, ue8m0=False, col=False, eps=1e-6, with_no
                                               rounding=rnd if qdt == torch.int8 else None)
     else:
         from fagq_mi355x import _lib
-        wpr, rpb, rseq, remap = mapping
+        wpr, rpb, mode, remap, *rest = mapping
+        lds = rest[0] if rest else 0
         p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())
         st = pkg.load_library().fagq_launch_mapped(
             p(xd), p(rd), p(gd), p(ro), p(norm), p(q), p(sc), M, D, G, eps,
             _lib.Q_FP8_E4M3FN if qdt == torch.float8_e4m3fn else _lib.Q_INT8,
             _lib.SCALE_UE8M0 if ue8m0 else _lib.SCALE_F32,
             _lib.LAYOUT_COL_MAJOR if col else _lib.LAYOUT_ROW_MAJOR,
-            _lib.ROUND_RNE if rnd == "rne" else _lib.ROUND_TRUNC, wpr, rpb, rseq, remap,
+            _lib.ROUND_RNE if rnd == "rne" else _lib.ROUND_TRUNC, wpr, rpb, mode, remap, lds,
             ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
         _lib.check(st, "fagq_launch_mapped")
     torch.cuda.synchronize(dev)

@@ -48,25 +48,38 @@ SHAPES = [(M, D) for M in (1, 4, 16, 32, 100, 128, 512, 4096, 16384) for D in
 
 
 @pytest.mark.parametrize("M,D", SHAPES)
-def test_route_invariants(pkg, M, D):
-    r = pkg.route_for(M, D, 128)
-    wpr, ns, rpb = r["waves_per_row"], r["steps_per_wave"], r["rows_per_block"]
-    rseq = r["rows_in_sequence"]
+@pytest.mark.parametrize("ue8m0,col", [(False, False), (False, True), (True, True)])
+def test_route_invariants(pkg, M, D, ue8m0, col):
+    r = pkg.route_for(M, D, 128, scale_ue8m0=ue8m0, scale_col_major=col)
+    wpr, ns, rpb, mode = (r["waves_per_row"], r["steps_per_wave"], r["rows_per_block"],
+                          r["row_group_mode"])
     steps = math.ceil(D / 512)
-    assert 1 <= wpr <= 16 and 1 <= ns <= 4 and rpb >= 1 and rseq in (1, 2, 4)
+    assert 1 <= wpr <= 16 and 1 <= ns <= 4 and rpb >= 1 and mode in (0, 1, 2)
     assert wpr * ns >= steps > (wpr - 1) * ns          # every wave owns >= 1 column
     assert r["block_threads"] == 64 * wpr * rpb <= 1024
-    per_block = rpb * rseq
-    assert r["grid_blocks"] * per_block >= M > (r["grid_blocks"] - 1) * per_block
-    if M >= 1024 and 2 <= steps <= 16:
-        assert (ns, rseq) == (2, 1)                      # prefill: 2-step waves
+    assert r["grid_blocks"] * rpb >= M > (r["grid_blocks"] - 1) * rpb
+    assert r["lds_bytes"] == 0
+    if mode:
+        assert wpr * ns <= 16                            # gamma fits the LDS buffer
+    if mode == 2:
+        assert col and rpb in (2, 4)
+    wide = M >= 1024 and col and not ue8m0 and 12 <= steps <= 16
+    if wide:
+        # fp32 column-major scales at 6144 <= D <= 8192: two rows per workgroup
+        # of 4-step waves, shared gamma, wide scale stores, 16 rows per XCD chunk.
+        assert (ns, rpb, mode, r["xcd_remap"]) == (4, 2, 2, 8)
+    elif M >= 1024 and 2 <= steps <= 16:
+        assert (ns, mode) == (2, 0)                      # prefill: 2-step waves
     if M <= 32 and D <= 8192:
-        assert (wpr, ns, rseq) == (steps, 1, 1)          # decode: one step per wave
+        assert (wpr, ns, mode) == (steps, 1, 0)          # decode: one step per wave
+    if not col:
+        assert r["xcd_remap"] == 0
 
 
 @pytest.mark.parametrize("args,status", [
-    ((4, 4096, 100), 3), ((4, 4000, 128), 2), ((-1, 4096, 128), 2), ((4, 0, 128), 2),
-    ((4, 65536, 128), 7),
+    ((4, 4096, 100, 0, 0), 3), ((4, 4000, 128, 0, 0), 2), ((-1, 4096, 128, 0, 0), 2),
+    ((4, 0, 128, 0, 0), 2), ((4, 65536, 128, 0, 0), 7), ((4, 4096, 128, 2, 0), 5),
+    ((4, 4096, 128, 0, 2), 5),
 ])
 def test_route_rejects_bad_shapes(lib, args, status):
     from fagq_mi355x import _lib
@@ -120,9 +133,10 @@ def test_in_place_residual_is_accepted_by_validation(lib):
 
 
 def test_mapped_launch_rejects_bad_mappings(lib):
-    def mapped(wpr, rpb, remap=1, D=7168, rseq=1):
+    def mapped(wpr, rpb, remap=1, D=7168, mode=0, lds=0, layout=0):
         return lib.fagq_launch_mapped(fake(0), fake(1), fake(2), fake(3), None, fake(4), fake(5),
-                                      8, D, 128, 1e-6, 1, 0, 0, 0, wpr, rpb, rseq, remap, None)
+                                      8, D, 128, 1e-6, 1, 0, layout, 0, wpr, rpb, mode, remap, lds,
+                                      None)
     assert mapped(0, 1) == 5
     assert mapped(17, 1) == 5
     assert mapped(4, 5) == 5          # 20 waves > 16
@@ -130,19 +144,30 @@ def test_mapped_launch_rejects_bad_mappings(lib):
     assert mapped(7, 1, remap=3) == 5
     assert mapped(7, 1, remap=128) == 5
     assert mapped(7, 1, D=65536) == 7  # D above FAGQ_MAX_D
-    assert mapped(7, 1, rseq=0) == 5
-    assert mapped(7, 1, rseq=3) == 5
-    assert mapped(7, 1, rseq=8) == 5
+    assert mapped(7, 1, mode=-1) == 5
+    assert mapped(7, 1, mode=3) == 5
+    assert mapped(4, 2, mode=2) == 5                   # wide scales: column-major only
+    assert mapped(4, 1, mode=2, layout=1) == 5         # wide scales: 2 or 4 rows
+    assert mapped(4, 3, mode=2, layout=1) == 5
+    assert mapped(8, 1, D=16384, mode=1) == 5          # 32 steps of gamma > 16 in LDS
+    assert mapped(7, 1, lds=-1) == 5
+    assert mapped(7, 1, lds=65537) == 5
 
 
 def test_diag_validation(lib):
-    assert lib.fagq_diag_encode(None, fake(1), 8, 1, 0, None) == 1
-    assert lib.fagq_diag_encode(fake(0), fake(1), 9, 1, 0, None) == 2
-    assert lib.fagq_diag_encode(fake(0), fake(1), 8, 1, 1, None) == 5
-    assert lib.fagq_diag_encode(fake(0), fake(1), 0, 1, 0, None) == 0
+    assert lib.fagq_diag_encode(None, fake(1), 8, 1, 0, 1, None) == 1
+    assert lib.fagq_diag_encode(fake(0), fake(1), 9, 1, 0, 1, None) == 2
+    assert lib.fagq_diag_encode(fake(0), fake(1), 8, 1, 1, 1, None) == 5
+    assert lib.fagq_diag_encode(fake(0), fake(1), 8, 1, 0, 2, None) == 5
+    assert lib.fagq_diag_encode(fake(0), fake(1), 0, 1, 0, 0, None) == 0
     assert lib.fagq_diag_copy(fake(0), fake(1), 15, None) == 2
     assert lib.fagq_diag_copy(None, fake(1), 16, None) == 1
     assert lib.fagq_diag_copy(fake(0), fake(1), 0, None) == 0
+    assert lib.fagq_diag_stream(fake(0), fake(1), 16, 3, None) == 5
+    assert lib.fagq_diag_stream(None, fake(1), 16, 1, None) == 1     # read needs src
+    assert lib.fagq_diag_stream(fake(0), None, 16, 2, None) == 1
+    assert lib.fagq_diag_stream(None, fake(1), 0, 2, None) == 0      # write: src may be NULL
+    assert lib.fagq_diag_stream(fake(0), ctypes.c_void_p(BASE + 8), 16, 0, None) == 4
     assert lib.fagq_diag_mfma_peak(None, 1, 1, None) == 1
     assert lib.fagq_diag_mfma_peak(fake(0), 0, 1, None) == 2
     assert lib.fagq_diag_mfma_peak(fake(0), 1, 0, None) == 2

@@ -69,46 +69,80 @@ def test_format_matrix(pkg, gpu, G, fmt, ue8m0, col):
 
 @pytest.mark.parametrize("D,G", [(7168, 128), (5120, 256), (4160, 64), (8192, 128), (1536, 64)])
 def test_every_launch_mapping(pkg, gpu, D, G):
-    """Every legal (waves_per_row, rows_per_block, rows_in_sequence, xcd_remap)
-    gives identical outputs, including row counts that leave the last row
-    groups and sequences partly empty."""
+    """Every legal (waves_per_row, rows_per_block, row_group_mode, xcd_remap)
+    gives identical outputs, including row counts that leave the last
+    workgroup's row groups partly empty (M = 19)."""
     M = 19
     x, r, w = inputs(M, D, seed=D)
     ref = None
     steps = math.ceil(D / 512)
     n = 0
     for wpr in range(1, 17):
-        if math.ceil(steps / wpr) > 4:
+        ns = math.ceil(steps / wpr)
+        if ns > 4:
             continue
         for rpb in (1, 2, 3, 4, 8, 16):
             if wpr * rpb > 16:
                 continue
-            for rseq in (1, 2, 4):
-                for remap in ((0, 1, 2, 8) if rseq == 1 else (0, 4)):
+            for mode in (0, 1, 2):
+                if mode and wpr * ns > 16:
+                    continue
+                if mode == 2 and rpb not in (2, 4):
+                    continue
+                for remap in ((0, 1, 2, 8) if mode == 0 else (0, 4)):
                     st, gpu_out = check(pkg, gpu, x, r, w, G, "fp8", col=True,
-                                        mapping=(wpr, rpb, rseq, remap),
-                                        label=f"map wpr={wpr} rpb={rpb} rseq={rseq}")
+                                        mapping=(wpr, rpb, mode, remap),
+                                        label=f"map wpr={wpr} rpb={rpb} mode={mode} remap={remap}")
                     assert st["exact"], st
                     if ref is None:
                         ref = gpu_out
                     for k in ref:
-                        assert np.array_equal(ref[k], gpu_out[k]), (wpr, rpb, rseq, remap, k)
+                        assert np.array_equal(ref[k], gpu_out[k]), (wpr, rpb, mode, remap, k)
                     n += 1
     assert n >= 20
 
 
-@pytest.mark.parametrize("rseq", [2, 4])
+@pytest.mark.parametrize("mode,rpb", [(1, 2), (1, 3), (2, 2), (2, 4)])
 @pytest.mark.parametrize("M", [37, 8])
-def test_rows_in_sequence_all_formats(pkg, gpu, rseq, M):
-    """Rows processed in turn by one row group (gamma reused, next row prefetched),
-    with M not a multiple of the rows per workgroup."""
-    x, r, w = inputs(M, 5120, seed=rseq, scale=3.0)
+def test_shared_modes_all_formats(pkg, gpu, mode, rpb, M):
+    """Gamma shared through LDS (mode 1) and wide column-major scale stores (mode 2)
+    in every code and scale format, with norm_out, for M a multiple of the rows
+    per workgroup (8) and not (37: the last workgroup stores row by row)."""
+    x, r, w = inputs(M, 5120, seed=mode * 10 + rpb, scale=3.0)
     for fmt in ("fp8", "int8_rne", "int8_trunc"):
         for ue in (False, True):
-            for wpr in (5, 10):
-                st, _ = check(pkg, gpu, x, r, w, 128, fmt, ue8m0=ue, col=ue, with_norm=True,
-                              mapping=(wpr, 1, rseq, 0), label=f"rseq={rseq} wpr={wpr}")
+            for wpr in (3, 5):
+                if wpr * rpb > 16:
+                    continue
+                st, _ = check(pkg, gpu, x, r, w, 128, fmt, ue8m0=ue, col=(mode == 2 or ue),
+                              with_norm=True, mapping=(wpr, rpb, mode, 0),
+                              label=f"mode={mode} rpb={rpb} wpr={wpr}")
                 assert st["exact"], st
+
+
+@pytest.mark.parametrize("ue8m0", [False, True])
+@pytest.mark.parametrize("offset", [1, 2, 3])
+def test_wide_scales_misaligned_pointer(pkg, gpu, ue8m0, offset):
+    """Mode 2 with a scale pointer not aligned to the wide store: every row stores
+    its own scales, and the outputs are unchanged."""
+    x, r, w = inputs(64, 7168, seed=offset)
+    st, gpu_out = check(pkg, gpu, x, r, w, 128, "fp8", ue8m0=ue8m0, col=True,
+                        mapping=(4, 2, 2, 8), scale_offset=offset, label=f"wide offset={offset}")
+    assert st["exact"], st
+
+
+def test_occupancy_cap_gives_the_same_bits(pkg, gpu):
+    """Reserving dynamic LDS per workgroup (fewer workgroups per CU) changes nothing."""
+    x, r, w = inputs(300, 7168, seed=3)
+    outs = []
+    for lds in (0, 49152, 65536):
+        st, gpu_out = check(pkg, gpu, x, r, w, 128, "fp8", col=True, mapping=(7, 1, 0, 8, lds),
+                            label=f"lds={lds}")
+        assert st["exact"], st
+        outs.append(gpu_out)
+    for o in outs[1:]:
+        for k in o:
+            assert np.array_equal(o[k], outs[0][k])
 
 
 @pytest.mark.parametrize("M,D,G", [(1, 192, 64), (5, 640, 128), (130, 4160, 64), (3, 8448, 128),
