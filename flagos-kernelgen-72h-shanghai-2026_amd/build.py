@@ -93,5 +93,47 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     return LIB_PATH
 
 
+def sanitizer_runtime() -> Path:
+    """The shared AddressSanitizer runtime of hipcc's clang (preloaded into a
+    Python process that loads a sanitizer build)."""
+    rocm = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+    found = sorted((rocm / "llvm" / "lib" / "clang").glob("*/lib/linux/libclang_rt.asan-x86_64.so"))
+    if not found:
+        raise RuntimeError("clang's AddressSanitizer runtime not found under ROCm")
+    return found[-1]
+
+
+def build_variant(name: str, *, defines: tuple[str, ...] = (), sanitize: bool = False,
+                  verbose: bool = False) -> Path:
+    """A test-only build of the same sources into _build/<name>/libfagq.so, with
+    extra -D defines (e.g. FAGQ_TEST_LAUNCH_FAILURE) and, with `sanitize`,
+    AddressSanitizer and UndefinedBehaviorSanitizer on every host function
+    (the argument validation, route table and host-side diagnostics; the
+    device code is compiled as usual).  Never the library the package loads."""
+    out_dir = OBJ_DIR / name
+    out_dir.mkdir(parents=True, exist_ok=True)
+    cc = hipcc()
+    flags = [*device_flags(), *[f"-D{d}" for d in defines]]
+    san = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+           "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host",
+           "-fno-omit-frame-pointer", "-Xarch_host", "-g"] if sanitize else []
+    units: list[tuple[Path, Path, list[str]]] = []
+    for q, sf in INST_COMBOS:
+        units.append((CSRC / "fagq_inst.hip", out_dir / f"fagq_inst_q{q}_s{sf}.o",
+                      [f"-DFAGQ_QF={q}", f"-DFAGQ_SF={sf}"]))
+    for unit in ("fagq_api", "fagq_gemm", "dsa_topk", "mla_bwd"):
+        units.append((CSRC / f"{unit}.hip", out_dir / f"{unit}.o", []))
+    with ThreadPoolExecutor(max_workers=min(len(units), max(1, min(16, os.cpu_count() or 1)))) as ex:
+        futs = [ex.submit(_run, [cc, *flags, *san, *defs, "-c", str(src), "-o", str(obj)], verbose)
+                for src, obj, defs in units]
+        for f in futs:
+            f.result()
+    lib = out_dir / "libfagq.so"
+    link_san = ["-fsanitize=address", "-fsanitize=undefined", "-shared-libsan"] if sanitize else []
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *link_san,
+          "-o", str(lib), *[str(o) for _, o, _ in units]], verbose)
+    return lib
+
+
 if __name__ == "__main__":
     print(build(verbose=True))

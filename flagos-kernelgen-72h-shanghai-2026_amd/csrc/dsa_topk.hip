@@ -8,13 +8,18 @@
 // and the first top_k block ids and their page_table[b, id] entries are
 // written (-1 past the number of selectable blocks).
 //
-// Work mapping.  One workgroup per row, one wave per 1024 blocks of it (up
-// to 4 waves); a lane holds 16 scores in VGPRs, loaded as 16-byte vectors
-// through a buffer descriptor sized to the row's valid prefix, so blocks past
-// it are never fetched, and waves wholly past the prefix exit at once (a
-// workgroup barrier waits only for the waves still running).  Cross-lane
-// steps use DPP and v_permlane32_swap; the waves of a row combine through LDS
-// and five workgroup barriers.
+// Work mapping.  One workgroup per row, one wave per 1024-block chunk of it
+// (up to 16 waves); a lane holds 16 scores in VGPRs, loaded through a buffer
+// descriptor sized to the row's valid prefix, so blocks past it are never
+// fetched, and waves wholly past the prefix exit at once (a workgroup barrier
+// waits only for the waves still running).  Rows whose base is 16-byte
+// aligned (scores pointer aligned and NB * element size a multiple of 16) are
+// read as 16-byte vectors, other rows one score per load.  A row of more than
+// 16 chunks (NB > 16384) is walked in chunks of 16 x 1024 blocks, each wave
+// taking every 16th chunk and reading the scores again in each pass (the row
+// is L2-resident after the first).  Cross-lane steps use DPP and
+// v_permlane32_swap; the waves of a row combine through LDS and five
+// workgroup barriers.
 //
 // Selection is exact and never runs a sorting network:
 //   1. The fp32 range [vmin, vmax] of the selectable scores (non-selectable
@@ -49,14 +54,12 @@ namespace dsa {
 namespace {
 
 constexpr int kEPL = 16;                    // scores per lane
-constexpr int kChunk = 64 * kEPL;            // blocks per wave
-constexpr int kMaxWaves = FAGQ_DSA_MAX_NB / kChunk;
+constexpr int kChunk = 64 * kEPL;            // blocks per wave chunk
+constexpr int kMaxWaves = 16;                // waves per row (NB <= 16384 in one chunk each)
 constexpr int kBins = 256;
 constexpr uint32_t kCap = 512;               // candidates held at most
 constexpr int kMaxTopK = FAGQ_DSA_MAX_TOP_K;
 constexpr int64_t kMaxGridYZ = 65535;        // H and B are grid dimensions y and z
-constexpr int64_t kMaxGridX = (1ll << 24) - 1;   // Q * 256 work-items < 2^32
-static_assert(kMaxWaves * kChunk == FAGQ_DSA_MAX_NB, "waves per row");
 
 struct DArgs {
   const void* scores;
@@ -276,8 +279,87 @@ __device__ __forceinline__ float vec_elem(const u32x4& d, int c) {
 
 // ----------------------------------------------------------------- kernel
 
-template <bool BF16>
-__global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
+// One 16-byte vector of scores at byte offset `off` of the row (VEC scores:
+// blocks off / esz .. + VEC - 1).  VECLD: one 16-byte load (rows 16-byte
+// aligned, the descriptor covering the prefix rounded up to whole vectors
+// inside the row); else one load per score through a descriptor sized to the
+// prefix exactly, so scores past it read as 0 (and are then masked by the
+// caller).
+template <bool BF16, bool VECLD>
+__device__ __forceinline__ u32x4 load_vec(const rsrc_t& rs, uint32_t off) {
+  if constexpr (VECLD) {
+    return __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+  } else {
+    u32x4 v;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if constexpr (BF16) {
+        const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(rs, off + 4u * c, 0, 0);
+        const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(rs, off + 4u * c + 2u, 0, 0);
+        v[c] = lo | (hi << 16);
+      } else {
+        v[c] = __builtin_amdgcn_raw_buffer_load_b32(rs, off + 4u * c, 0, 0);
+      }
+    }
+    return v;
+  }
+}
+
+// The 16 scores of a lane in the chunk starting at block wbase: vector i
+// holds blocks wbase + i * 64 * VEC + lane * VEC + c, c < VEC.
+template <bool BF16, bool VECLD>
+__device__ __forceinline__ void load_chunk(const rsrc_t& rs, int wbase, int lane,
+                                           u32x4 (&raw)[kEPL / (BF16 ? 8 : 4)]) {
+  constexpr int VEC = BF16 ? 8 : 4;
+  constexpr uint32_t esz = BF16 ? 2u : 4u;
+#pragma unroll
+  for (int i = 0; i < kEPL / VEC; ++i)
+    raw[i] = load_vec<BF16, VECLD>(rs, (uint32_t)(wbase * esz) + (uint32_t)(i * 64 + lane) * 16u);
+}
+
+// Scores of a loaded chunk: blocks at or past the prefix (rel = nvalid -
+// wbase blocks remain) become -inf.  Updates the lane's maximum and the
+// minimum over its selectable (not -inf) scores.
+template <bool BF16, bool FULL>
+__device__ __forceinline__ void chunk_scores(const u32x4 (&raw)[kEPL / (BF16 ? 8 : 4)], int lbase,
+                                             int rel, float (&sv)[kEPL], float& vmin,
+                                             float& vmax) {
+  constexpr int VEC = BF16 ? 8 : 4;
+  const float ninf = -__builtin_inff();
+  float lmin = __builtin_inff();
+#pragma unroll
+  for (int i = 0; i < kEPL / VEC; ++i) {
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      const int e = i * VEC + c;
+      const float v = vec_elem<BF16>(raw[i], c);
+      sv[e] = FULL || lbase < rel - elem_off<BF16>(e) ? v : ninf;
+      vmax = fmaxf(vmax, sv[e]);
+      // A full chunk takes the plain minimum and redoes it below in the rare
+      // case that an explicit -inf score made it -inf.
+      if constexpr (FULL) lmin = fminf(lmin, sv[e]);
+      else lmin = fminf(lmin, sv[e] != ninf ? sv[e] : __builtin_inff());
+    }
+  }
+  if (FULL && lmin == ninf) {
+    lmin = __builtin_inff();
+#pragma unroll
+    for (int e = 0; e < kEPL; ++e) lmin = fminf(lmin, sv[e] != ninf ? sv[e] : __builtin_inff());
+  }
+  vmin = fminf(vmin, lmin);
+}
+
+// KIND: kSmallRows (at most 4 chunks, 256-thread workgroups) or kRows (at
+// most 16) keep one chunk per wave in VGPRs from the first pass to the last;
+// kLongRows (more than 16 chunks): every wave walks chunks w, w + nwv, ... in
+// each pass, reading its scores again.
+enum RowKind { kSmallRows = 0, kRows = 1, kLongRows = 2 };
+constexpr int kSmallWaves = 4;
+
+template <bool BF16, bool VECLD, int KIND>
+__global__ void __launch_bounds__(KIND == kSmallRows ? 64 * kSmallWaves : 64 * kMaxWaves)
+dsa_topk_rows(const DArgs g) {
+  constexpr bool MULTI = KIND == kLongRows;
   constexpr int VEC = BF16 ? 8 : 4;
   __shared__ Lds lds;
   const int lane = threadIdx.x & 63;
@@ -306,7 +388,8 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
     vb = vb < g.NB ? vb : g.NB;
     nvalid = (int)(lastp < vb - 1 ? lastp : vb - 1) + 1;
   }
-  const int nwv = nvalid > kChunk ? (nvalid + kChunk - 1) / kChunk : 1;   // waves with work
+  const int nchunk = nvalid > kChunk ? (nvalid + kChunk - 1) / kChunk : 1;
+  const int nwv = nchunk < (int)(blockDim.x >> 6) ? nchunk : (int)(blockDim.x >> 6);  // waves with work
   if (w >= nwv) return;
 
   if (w == 0) {
@@ -315,48 +398,45 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
     if (lane == 0) lds.ncur = 0u;
   }
 
-  // Scores of the valid prefix; non-selectable blocks hold -inf.  The
-  // descriptor covers the prefix rounded up to whole 16-byte vectors (inside
-  // the row: NB is a multiple of VEC), so no vector straddles its end.  A
-  // wave whose blocks all lie in the prefix skips the per-block id test.
+  // Scores of the valid prefix; non-selectable blocks hold -inf.  With vector
+  // loads the descriptor covers the prefix rounded up to whole 16-byte vectors
+  // (inside the row: NB is a multiple of VEC), so no vector straddles its end;
+  // with per-score loads it covers the prefix exactly.  A chunk whose blocks
+  // all lie in the prefix skips the per-block id test.
   constexpr uint32_t esz = BF16 ? 2u : 4u;
-  const uint32_t nload = ((uint32_t)nvalid + VEC - 1) / VEC * VEC;
+  const uint32_t nload = VECLD ? ((uint32_t)nvalid + VEC - 1) / VEC * VEC : (uint32_t)nvalid;
   const rsrc_t rs = make_rsrc((const uint8_t*)g.scores + row * (int64_t)g.NB * esz, nload * esz);
   const int lbase = lane * VEC;                  // lane's first block inside a vector span
-  const int wbase = w * kChunk;
-  const bool full = wbase + kChunk <= nvalid;
   const float ninf = -__builtin_inff();
   float sv[kEPL];
   float vmax = ninf, vmin = __builtin_inff();
-  // Every vector load is issued before the full / partial split.
-  u32x4 raw[kEPL / VEC];
-#pragma unroll
-  for (int i = 0; i < kEPL / VEC; ++i)
-    raw[i] = __builtin_amdgcn_raw_buffer_load_b128(
-        rs, (uint32_t)(wbase * esz) + (uint32_t)(i * 64 + lane) * 16u, 0, 0);
-  auto load = [&](auto full_c) {
-#pragma unroll
-    for (int i = 0; i < kEPL / VEC; ++i) {
-#pragma unroll
-      for (int c = 0; c < VEC; ++c) {
-        const int e = i * VEC + c;
-        const float v = vec_elem<BF16>(raw[i], c);
-        sv[e] = decltype(full_c)::value || lbase < nvalid - wbase - elem_off<BF16>(e) ? v : ninf;
-        vmax = fmaxf(vmax, sv[e]);
-        // A full wave takes the plain minimum and redoes it below in the rare
-        // case that an explicit -inf score made it -inf.
-        if constexpr (decltype(full_c)::value) vmin = fminf(vmin, sv[e]);
-        else vmin = fminf(vmin, sv[e] != ninf ? sv[e] : __builtin_inff());
-      }
-    }
-    if (decltype(full_c)::value && vmin == ninf) {
-      vmin = __builtin_inff();
-#pragma unroll
-      for (int e = 0; e < kEPL; ++e) vmin = fminf(vmin, sv[e] != ninf ? sv[e] : __builtin_inff());
+  // Runs f(wbase) for each chunk of this wave with sv holding its scores.
+  auto each_chunk = [&](auto&& f) {
+#pragma unroll 1
+    for (int ci = w; ci < nchunk; ci += nwv) {
+      const int wbase = ci * kChunk;
+      u32x4 raw[kEPL / VEC];
+      load_chunk<BF16, VECLD>(rs, wbase, lane, raw);
+      float lo = __builtin_inff(), hi = ninf;
+      if (wbase + kChunk <= nvalid) chunk_scores<BF16, true>(raw, lbase, nvalid - wbase, sv, lo, hi);
+      else chunk_scores<BF16, false>(raw, lbase, nvalid - wbase, sv, lo, hi);
+      f(wbase, wbase + kChunk <= nvalid, lo, hi);
     }
   };
-  if (full) load(BoolC<true>());
-  else load(BoolC<false>());
+  const int wbase0 = w * kChunk;               // the wave's chunk when !MULTI
+  const bool full0 = wbase0 + kChunk <= nvalid;
+  if constexpr (MULTI) {
+    each_chunk([&](int, bool, float lo, float hi) {
+      vmin = fminf(vmin, lo);
+      vmax = fmaxf(vmax, hi);
+    });
+  } else {
+    // Every load is issued before the full / partial split.
+    u32x4 raw[kEPL / VEC];
+    load_chunk<BF16, VECLD>(rs, wbase0, lane, raw);
+    if (full0) chunk_scores<BF16, true>(raw, lbase, nvalid - wbase0, sv, vmin, vmax);
+    else chunk_scores<BF16, false>(raw, lbase, nvalid - wbase0, sv, vmin, vmax);
+  }
   uint32_t kmax = wave_reduce(ord_key(vmax), UMax());
   uint32_t kmin = wave_reduce(ord_key(vmin), UMin());
   if (lane == 0) {
@@ -380,17 +460,13 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
   const bool degen = !(vmax > vmin) || !(s > 0.0f) || !__builtin_isfinite(s) ||
                      !(fabsf(vmin * s) < kMaxBinOffset);
   // Bins of the lane's scores, four 8-bit bins per word (0: not selectable).
-  // Non-selectable blocks count in bin 0 (ignored) in a full wave, where
+  // Non-selectable blocks count in bin 0 (ignored) in a full chunk, where
   // they are rare, else in the lane's own discard word.
   uint32_t pbin[kEPL / 4];
-  auto hist = [&](auto full_c, auto binf) {
+  auto bins = [&](auto binf) {
 #pragma unroll
-    for (int e = 0; e < kEPL; ++e) {
+    for (int e = 0; e < kEPL; ++e)
       pbin[e / 4] = binf(sv[e], (uint32_t)(e % 4), e % 4 ? pbin[e / 4] : 0u);
-      const uint32_t bn = (pbin[e / 4] >> (8 * (e % 4))) & 0xffu;
-      const uint32_t at = decltype(full_c)::value || bn ? bn : (uint32_t)(kBins + lane);
-      __hip_atomic_fetch_add(&lds.hist[at], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    }
   };
   auto bin_lin = [=](float v, uint32_t byte, uint32_t word) {
     return fbin_pack(v, s, c, byte, word);
@@ -398,12 +474,31 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
   auto bin_one = [=](float v, uint32_t byte, uint32_t word) {
     return word | ((v != ninf ? 1u : 0u) << (8 * byte));
   };
-  if (!degen) {
-    if (full) hist(BoolC<true>(), bin_lin);
-    else hist(BoolC<false>(), bin_lin);
+  auto make_bins = [&]() {
+    if (!degen) bins(bin_lin);
+    else bins(bin_one);
+  };
+  auto hist = [&](auto full_c) {
+#pragma unroll
+    for (int e = 0; e < kEPL; ++e) {
+      const uint32_t bn = (pbin[e / 4] >> (8 * (e % 4))) & 0xffu;
+      const uint32_t at = decltype(full_c)::value || bn ? bn : (uint32_t)(kBins + lane);
+      __hip_atomic_fetch_add(&lds.hist[at], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  };
+  auto hist_rt = [&](bool full) {
+    if (full) hist(BoolC<true>());
+    else hist(BoolC<false>());
+  };
+  if constexpr (MULTI) {
+    each_chunk([&](int, bool full, float, float) {
+      make_bins();
+      hist(BoolC<false>());
+      (void)full;
+    });
   } else {
-    if (full) hist(BoolC<true>(), bin_one);
-    else hist(BoolC<false>(), bin_one);
+    make_bins();
+    hist_rt(full0);
   }
   __syncthreads();
 
@@ -417,20 +512,30 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
     // holds the raw score bits and 0xffffffff - id; the scores become ordered
     // keys in one pass over the candidates below.
     const uint32_t bstar = bd.bin > 1u ? bd.bin : 1u;
-    const uint32_t nid = 0xffffffffu - (uint32_t)(wbase + lbase);
     __syncthreads();                      // above(b) stored by wave 0
+    auto scatter = [&](int wbase) {
+      const uint32_t nid = 0xffffffffu - (uint32_t)(wbase + lbase);
 #pragma unroll
-    for (int e = 0; e < kEPL; ++e) {
-      const uint32_t bn = (pbin[e / 4] >> (8 * (e % 4))) & 0xffu;
-      if (bn >= bstar) {
-        // The cursor returns the entry's byte offset; a bin's slots end at
-        // 8 (above(b*) + hist[b*]) = 8 nc <= 8 CAP, so no mask is needed.
-        const uint32_t off = __hip_atomic_fetch_add(&lds.above[bn], 8u, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_WORKGROUP);
-        const uint32_t lo = nid - (uint32_t)elem_off<BF16>(e);
-        *reinterpret_cast<uint64_t*>(reinterpret_cast<uint8_t*>(lds.cand) + off) =
-            ((uint64_t)__float_as_uint(sv[e]) << 32) | (uint64_t)lo;
+      for (int e = 0; e < kEPL; ++e) {
+        const uint32_t bn = (pbin[e / 4] >> (8 * (e % 4))) & 0xffu;
+        if (bn >= bstar) {
+          // The cursor returns the entry's byte offset; a bin's slots end at
+          // 8 (above(b*) + hist[b*]) = 8 nc <= 8 CAP, so no mask is needed.
+          const uint32_t off = __hip_atomic_fetch_add(&lds.above[bn], 8u, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_WORKGROUP);
+          const uint32_t lo = nid - (uint32_t)elem_off<BF16>(e);
+          *reinterpret_cast<uint64_t*>(reinterpret_cast<uint8_t*>(lds.cand) + off) =
+              ((uint64_t)__float_as_uint(sv[e]) << 32) | (uint64_t)lo;
+        }
       }
+    };
+    if constexpr (MULTI) {
+      each_chunk([&](int wbase, bool, float, float) {
+        make_bins();
+        scatter(wbase);
+      });
+    } else {
+      scatter(wbase0);
     }
   } else {
     // Radix refinement on the composite key over [lo, hi]: found blocks lie
@@ -438,15 +543,19 @@ __global__ void __launch_bounds__(64 * kMaxWaves) dsa_topk_rows(const DArgs g) {
     // memory on each pass (this path is rare), so none stay live in VGPRs.
     auto keys = [&](auto&& f) {
 #pragma unroll 1
-      for (int i = 0; i < kEPL / VEC; ++i) {
-        const u32x4 d = __builtin_amdgcn_raw_buffer_load_b128(
-            rs, (uint32_t)(wbase * esz) + (uint32_t)(i * 64 + lane) * 16u, 0, 0);
+      for (int ci = w; ci < nchunk; ci += nwv) {
+        const int wbase = ci * kChunk;
+#pragma unroll 1
+        for (int i = 0; i < kEPL / VEC; ++i) {
+          const u32x4 d = load_vec<BF16, VECLD>(
+              rs, (uint32_t)(wbase * esz) + (uint32_t)(i * 64 + lane) * 16u);
 #pragma unroll
-        for (int c = 0; c < VEC; ++c) {
-          const float v = vec_elem<BF16>(d, c);
-          const int off = i * (64 * VEC) + c;
-          if (lbase < nvalid - wbase - off && v != ninf)
-            f(composite(v, (uint32_t)(wbase + lbase + off)));
+          for (int cc = 0; cc < VEC; ++cc) {
+            const float v = vec_elem<BF16>(d, cc);
+            const int off = i * (64 * VEC) + cc;
+            if (lbase < nvalid - wbase - off && v != ninf)
+              f(composite(v, (uint32_t)(wbase + lbase + off)));
+          }
         }
       }
     };
@@ -603,12 +712,14 @@ FAGQ_API int fagq_dsa_topk_launch(const void* scores, int scores_dtype, const vo
   if (NB > FAGQ_DSA_MAX_NB || top_k > kMaxTopK || block_size > INT32_MAX) return FAGQ_E_TOO_LARGE;
   const int64_t rows = B * H * Q;
   const int64_t esz = scores_dtype == FAGQ_DSA_BF16 ? 2 : 4;
-  if (rows > (int64_t)INT32_MAX || NB * esz > (int64_t)UINT32_MAX || H > kMaxGridYZ ||
-      B > kMaxGridYZ || Q > kMaxGridX)
+  const int64_t chunks = (NB + kChunk - 1) / kChunk;
+  const int waves = (int)(chunks < kMaxWaves ? chunks : kMaxWaves);
+  // Q workgroups of 64 * waves work-items along grid x: fewer than 2^32.
+  if (rows > (int64_t)INT32_MAX || H > kMaxGridYZ || B > kMaxGridYZ ||
+      Q * 64 * waves >= (1ll << 32))
     return FAGQ_E_TOO_LARGE;
-  if (!aligned(scores, 16) || (NB * esz) % 16 != 0 || !aligned(page_table, 4) ||
-      !aligned(out_blocks, 4) || !aligned(out_pages, 4) ||
-      !aligned(q_pos, index_dtype == FAGQ_DSA_I64 ? 8 : 4) ||
+  if (!aligned(scores, (uintptr_t)esz) || !aligned(page_table, 4) || !aligned(out_blocks, 4) ||
+      !aligned(out_pages, 4) || !aligned(q_pos, index_dtype == FAGQ_DSA_I64 ? 8 : 4) ||
       !aligned(kv_lens, index_dtype == FAGQ_DSA_I64 ? 8 : 4))
     return FAGQ_E_ALIGN;
   if (rows == 0) return FAGQ_OK;
@@ -631,14 +742,23 @@ FAGQ_API int fagq_dsa_topk_launch(const void* scores, int scores_dtype, const vo
   g.top_k = (int32_t)top_k;
   g.index64 = index_dtype == FAGQ_DSA_I64;
   set_divisor(g, (uint32_t)block_size);
-  const bool bf16 = scores_dtype == FAGQ_DSA_BF16;
-  const int waves = (int)((NB + kChunk - 1) / kChunk);
+  // 16-byte vector loads need every row 16-byte aligned; rows of more than
+  // kMaxWaves chunks are walked chunk by chunk.
+  const int bf16 = scores_dtype == FAGQ_DSA_BF16;
+  const int vec = aligned(scores, 16) && (NB * esz) % 16 == 0;
+  const int kind = chunks > kMaxWaves ? kLongRows : chunks > kSmallWaves ? kRows : kSmallRows;
+#define FAGQ_DSA_K(B, V) \
+  {(const void*)&dsa_topk_rows<B, V, kSmallRows>, (const void*)&dsa_topk_rows<B, V, kRows>, \
+   (const void*)&dsa_topk_rows<B, V, kLongRows>}
+  static const void* const kernels[2][2][3] = {
+      {FAGQ_DSA_K(false, false), FAGQ_DSA_K(false, true)},
+      {FAGQ_DSA_K(true, false), FAGQ_DSA_K(true, true)}};
+#undef FAGQ_DSA_K
   void* args[] = {&g};
-  const void* k = bf16 ? (const void*)&dsa_topk_rows<true> : (const void*)&dsa_topk_rows<false>;
-  const hipError_t e = hipLaunchKernel(k, dim3((unsigned)Q, (unsigned)H, (unsigned)B),
+  return launch_status(hipLaunchKernel(kernels[bf16][vec][kind],
+                                       dim3((unsigned)Q, (unsigned)H, (unsigned)B),
                                        dim3((unsigned)(64 * waves)), args, 0,
-                                       static_cast<hipStream_t>(stream));
-  return e == hipSuccess ? FAGQ_OK : -(int)e;
+                                       static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

@@ -141,25 +141,37 @@ bool finish_mapping(int64_t M, int D, int wpr, int rpb, int mode, int lds, Mappi
 
 // The route table.  Each row is split over waves of one workgroup so that
 // every wave streams only 1-4 KB of each input (dispatch-ordered workgroups
-// then keep the set of rows in flight small, which HBM rewards).
-// * Prefill (M >= prefill_rows()) with fp32 column-major scales and
-//   12..16 steps per row (6144 <= D <= 8192, the DeepSeek-V3 width among
-//   them): two rows per workgroup of 4-step waves, gamma loaded once per
-//   workgroup and shared through LDS, each group's two scale words stored
-//   together (RG_WIDE_SCALES).  At 16384 x 7168 this measured 129.8 us
-//   against 134.1 us for one row of 2-step waves.
-// * Other prefill: 2 steps per wave, one row per workgroup.
-// * Decode: 1 step per wave, one row per workgroup, as many waves as the row
+// then keep the set of rows in flight small, which HBM rewards).  Rows below
+// refer to prefill (M >= prefill_rows()) unless stated; timings are medians of
+// interleaved runs at M = 16384 (MI355X):
+// * column-major scales, 12..16 steps (6144 <= D <= 8192): two rows per
+//   workgroup of 4-step waves, gamma loaded once and shared through LDS, each
+//   group's scale words of both rows stored together (RG_WIDE_SCALES).
+//   D = 7168 fp32: 130.2 us against 134.6 us for one row of 2-step waves;
+//   D = 7168 ue8m0: 130.8 against 134.2; D = 8192 fp32: 147.0 against 151.0.
+// * row-major, 12..14 steps: one row of 2-step waves, at most three
+//   workgroups per CU (48 KB of LDS reserved each): D = 7168: 130.3 against
+//   132.5 us; D = 6144: 112.2 against 113.5.
+// * row-major, 15..16 steps: two rows of 4-step waves sharing gamma
+//   (RG_SHARED_GAMMA): D = 8192: 149.3 against 150.5 us.
+// * 5..8 steps: 1-step waves: D = 4096: 21.3 against 21.6 us at M = 4096,
+//   74.7 against 75.5 at M = 16384; D = 3072: 57.5 against 59.0.
+// * other prefill: 2 steps per wave, one row per workgroup.
+// * decode: 1 step per wave, one row per workgroup, as many waves as the row
 //   has steps (<= 16).
 // Rows of more than 16 steps use up to 4 steps per wave.
 void choose_mapping(int64_t M, int D, int scale_format, int scale_layout, Mapping* m) {
   const int steps = ceil_div(D, kStepCols);
   const bool prefill = M >= prefill_rows();
-  if (prefill && scale_format == FAGQ_SCALE_F32 && scale_layout == FAGQ_LAYOUT_COL_MAJOR &&
-      steps >= 12 && steps <= kMaxSharedSteps &&
-      finish_mapping(M, D, ceil_div(steps, kMaxStepsPerWave), 2, RG_WIDE_SCALES, 0, m))
-    return;
-  int ns = prefill ? prefill_steps() : 1;
+  const bool col = scale_layout == FAGQ_LAYOUT_COL_MAJOR;
+  (void)scale_format;
+  if (prefill && steps >= 12 && steps <= kMaxSharedSteps) {
+    const int wpr4 = ceil_div(steps, kMaxStepsPerWave);
+    if (col && finish_mapping(M, D, wpr4, 2, RG_WIDE_SCALES, 0, m)) return;
+    if (!col && steps >= 15 && finish_mapping(M, D, wpr4, 2, RG_SHARED_GAMMA, 0, m)) return;
+    if (!col && finish_mapping(M, D, ceil_div(steps, 2), 1, RG_INDEPENDENT, 48 * 1024, m)) return;
+  }
+  int ns = prefill ? (steps >= 5 && steps <= 8 ? 1 : prefill_steps()) : 1;
   if (ns > kMaxStepsPerWave) ns = kMaxStepsPerWave;
   const int min_ns = ceil_div(steps, kMaxWavesPerBlock);
   if (ns < min_ns) ns = min_ns;
@@ -267,7 +279,7 @@ LaunchFn lookup(int q_format, int scale_format, int rounding, int lpg_idx, int s
   }
 }
 
-LaunchFn lookup_parts(int q_format, int scale_format, int rounding, int lpg_idx, int steps) {
+PartsLaunchFn lookup_parts(int q_format, int scale_format, int rounding, int lpg_idx, int steps) {
   const int qf = q_format == FAGQ_Q_FP8_E4M3FN ? QF_FP8
                  : rounding == FAGQ_ROUND_RNE  ? QF_I8_RNE
                                                : QF_I8_TRUNC;
@@ -308,33 +320,18 @@ void fill_args(KArgs* a, const Mapping& m, const void* x, const void* residual, 
   a->norm_out = static_cast<uint16_t*>(norm_out);
   a->q = static_cast<uint8_t*>(q);
   a->scale = static_cast<uint8_t*>(scale);
-  a->M = M;
+  a->M = (int32_t)M;
   a->D = (int32_t)D;
   a->groups = (int32_t)(D / G);
   a->eps = eps;
-  a->wpr = m.wpr;
-  a->rpb = m.rpb;
-  a->col_major = scale_layout == FAGQ_LAYOUT_COL_MAJOR;
-  a->remap = remap;
-  a->remap_shift = remap >= 2 ? __builtin_ctz((unsigned)remap) : 0;
-  a->wpr_magic = (65536 + m.wpr - 1) / m.wpr;
   const uintptr_t wide_bytes =
       (uintptr_t)m.rpb * (uintptr_t)(scale_format == FAGQ_SCALE_F32 ? 4 : 1);
-  a->wide_ok = m.mode == RG_WIDE_SCALES && M % m.rpb == 0 &&
-               (reinterpret_cast<uintptr_t>(scale) % wide_bytes) == 0;
-  a->nparts = 0;
-  for (int p = 0; p < kMaxParts; ++p) a->xparts[p] = nullptr;
+  const int wide_ok = m.mode == RG_WIDE_SCALES && M % m.rpb == 0 &&
+                      (reinterpret_cast<uintptr_t>(scale) % wide_bytes) == 0;
+  a->cfg = KArgs::pack_cfg(m.wpr, m.rpb, remap, remap >= 2 ? __builtin_ctz((unsigned)remap) : 0,
+                           scale_layout == FAGQ_LAYOUT_COL_MAJOR, wide_ok);
+  a->wpr_magic = (65536 + m.wpr - 1) / m.wpr;
 }
-
-// Status of a kernel launch.  Built with -DFAGQ_TEST_LAUNCH_FAILURE (a test
-// build only, never the shipped library) every launch reports
-// hipErrorLaunchFailure without reaching the runtime, so that the CPU tests
-// can check how a launch failure propagates through the C ABI and Python.
-#ifdef FAGQ_TEST_LAUNCH_FAILURE
-int launch_status(hipError_t) { return -(int)hipErrorLaunchFailure; }
-#else
-int launch_status(hipError_t e) { return e == hipSuccess ? FAGQ_OK : -(int)e; }
-#endif
 
 int launch_with(const Mapping& m, const void* x, const void* residual, const void* gamma,
                 void* residual_out, void* norm_out, void* q, void* scale, int64_t M, int64_t D,
@@ -424,12 +421,15 @@ FAGQ_API int fagq_launch_parts(const void* const* x_parts, int nparts, const voi
   if (dc != FAGQ_OK) return dc;
   Mapping m;
   choose_mapping_parts(M, (int)D, &m);
-  KArgs a;
-  fill_args(&a, m, x_parts[0], residual, gamma, residual_out, nullptr, q, scale, M, D, group_size,
-            eps, scale_format, scale_layout, remap_for(scale_layout, scale_format, m.rpb, m.mode));
+  PArgs a;
+  fill_args(&a.k, m, x_parts[0], residual, gamma, residual_out, nullptr, q, scale, M, D,
+            group_size, eps, scale_format, scale_layout,
+            remap_for(scale_layout, scale_format, m.rpb, m.mode));
   a.nparts = nparts;
-  for (int p = 0; p < nparts; ++p) a.xparts[p] = static_cast<const uint16_t*>(x_parts[p]);
-  const LaunchFn fn = lookup_parts(q_format, scale_format, rounding, lpg_index((int)group_size), m.ns);
+  for (int p = 0; p < kMaxParts; ++p)
+    a.xparts[p] = p < nparts ? static_cast<const uint16_t*>(x_parts[p]) : nullptr;
+  const PartsLaunchFn fn =
+      lookup_parts(q_format, scale_format, rounding, lpg_index((int)group_size), m.ns);
   return launch_status(fn(a, dim3((unsigned)m.grid), dim3((unsigned)m.block), 0u,
                           static_cast<hipStream_t>(stream)));
 }

@@ -12,6 +12,7 @@ namespace fagq {
 
 // (args, grid, block, dynamic LDS bytes, stream)
 using LaunchFn = hipError_t (*)(const KArgs&, dim3, dim3, unsigned, hipStream_t);
+using PartsLaunchFn = hipError_t (*)(const PArgs&, dim3, dim3, unsigned, hipStream_t);
 
 constexpr int kNumLpg = 3;      // lanes per group 8, 16, 32  <->  G = 64, 128, 256
 
@@ -24,6 +25,16 @@ constexpr int lpg_index(int group_size) {
 // FAGQ_E_DEVICE or -hipError_t.
 int device_check();
 
+// Status of a kernel launch: 0 (FAGQ_OK) or -hipError_t.  Built with
+// -DFAGQ_TEST_LAUNCH_FAILURE (a test build only, never the shipped library)
+// every launch reports hipErrorLaunchFailure instead, so that the CPU tests
+// can check how a launch failure propagates through the C ABI.
+#ifdef FAGQ_TEST_LAUNCH_FAILURE
+inline int launch_status(hipError_t) { return -(int)hipErrorLaunchFailure; }
+#else
+inline int launch_status(hipError_t e) { return e == hipSuccess ? 0 : -(int)e; }
+#endif
+
 // lookup_q<code>_s<scale>(lpg index, steps per wave in [1, 4], norm, row-group mode).
 LaunchFn lookup_q0_s0(int lpg_idx, int steps, bool norm, int mode);   // fp8, f32
 LaunchFn lookup_q0_s1(int lpg_idx, int steps, bool norm, int mode);   // fp8, ue8m0
@@ -34,11 +45,11 @@ LaunchFn lookup_q2_s1(int lpg_idx, int steps, bool norm, int mode);   // int8 tr
 
 // Multi-input form (fagq_rows_parts): lookup_parts_q<code>_s<scale>(lpg index,
 // steps per wave in [1, kMaxStepsParts]).
-LaunchFn lookup_parts_q0_s0(int lpg_idx, int steps);
-LaunchFn lookup_parts_q0_s1(int lpg_idx, int steps);
-LaunchFn lookup_parts_q1_s0(int lpg_idx, int steps);
-LaunchFn lookup_parts_q1_s1(int lpg_idx, int steps);
-LaunchFn lookup_parts_q2_s0(int lpg_idx, int steps);
-LaunchFn lookup_parts_q2_s1(int lpg_idx, int steps);
+PartsLaunchFn lookup_parts_q0_s0(int lpg_idx, int steps);
+PartsLaunchFn lookup_parts_q0_s1(int lpg_idx, int steps);
+PartsLaunchFn lookup_parts_q1_s0(int lpg_idx, int steps);
+PartsLaunchFn lookup_parts_q1_s1(int lpg_idx, int steps);
+PartsLaunchFn lookup_parts_q2_s0(int lpg_idx, int steps);
+PartsLaunchFn lookup_parts_q2_s1(int lpg_idx, int steps);
 
 }  // namespace fagq

@@ -408,7 +408,7 @@ int launch(const void* a_q, const void* a_scale, const void* b_q, const void* b_
   const hipError_t e = hipLaunchKernel(kernel, dim3((unsigned)(g.m_tiles * g.n_tiles)),
                                        dim3((unsigned)Layout256::THREADS), args, 0,
                                        static_cast<hipStream_t>(stream));
-  return e == hipSuccess ? FAGQ_OK : -(int)e;
+  return launch_status(e);
 }
 
 // Issue-rate probe of the GEMM's instruction: every wave keeps 8 independent
@@ -487,7 +487,7 @@ FAGQ_API int fagq_diag_mfma_peak(float* out, int64_t blocks, int32_t iters, void
   const hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&mfma_peak_kernel),
                                        dim3((unsigned)blocks), dim3(kPeakThreads), args, 0,
                                        static_cast<hipStream_t>(stream));
-  return e == hipSuccess ? FAGQ_OK : -(int)e;
+  return launch_status(e);
 }
 
 }  // extern "C"

@@ -28,9 +28,9 @@ hipError_t launch_rows(const KArgs& a, dim3 grid, dim3 block, unsigned lds, hipS
 }
 
 template <int NS, int LPG>
-hipError_t launch_rows_parts(const KArgs& a, dim3 grid, dim3 block, unsigned lds,
+hipError_t launch_rows_parts(const PArgs& a, dim3 grid, dim3 block, unsigned lds,
                              hipStream_t stream) {
-  void* args[] = {const_cast<KArgs*>(&a)};
+  void* args[] = {const_cast<PArgs*>(&a)};
   return hipLaunchKernel(
       reinterpret_cast<const void*>(&fagq_rows_parts<NS, LPG, FAGQ_QF, FAGQ_SF>), grid, block,
       args, lds, stream);
@@ -57,8 +57,8 @@ LaunchFn FAGQ_LOOKUP(FAGQ_QF, FAGQ_SF)(int lpg_idx, int steps, bool norm, int mo
 
 static_assert(kMaxStepsParts == 2, "the parts table lists 2 step counts");
 
-LaunchFn FAGQ_LOOKUP_PARTS(FAGQ_QF, FAGQ_SF)(int lpg_idx, int steps) {
-  static const LaunchFn table[kNumLpg][kMaxStepsParts] = {
+PartsLaunchFn FAGQ_LOOKUP_PARTS(FAGQ_QF, FAGQ_SF)(int lpg_idx, int steps) {
+  static const PartsLaunchFn table[kNumLpg][kMaxStepsParts] = {
       {&launch_rows_parts<1, 8>, &launch_rows_parts<2, 8>},
       {&launch_rows_parts<1, 16>, &launch_rows_parts<2, 16>},
       {&launch_rows_parts<1, 32>, &launch_rows_parts<2, 32>}};

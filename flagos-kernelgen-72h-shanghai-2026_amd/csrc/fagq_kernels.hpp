@@ -72,6 +72,9 @@ constexpr int kMaxWideRows = 4;      // rows whose scales one wide store covers
 constexpr int kStoreAux = 18;
 
 // Kernel arguments (element pointers; the kernels build buffer descriptors).
+// Kept to 80 bytes: the host cost of a launch grows with the argument size
+// (measured 2.5 us for 16 bytes, 3.7 us for 176 on this runtime), and
+// decode-sized calls are bound by it.  The small mapping fields share cfg.
 struct KArgs {
   const uint16_t* x;
   const uint16_t* res;
@@ -80,18 +83,34 @@ struct KArgs {
   uint16_t* norm_out;  // nullptr: 3-output form
   uint8_t* q;
   uint8_t* scale;      // fp32 (SF_F32) or uint8 (SF_UE8M0) words
-  int64_t M;
+  int32_t M;           // rows (< 2^31)
   int32_t D;
   int32_t groups;      // D / G
   float eps;
-  int32_t wpr;         // waves per row
-  int32_t rpb;         // row groups per workgroup (each wpr waves)
-  int32_t col_major;   // scale layout: 0 -> [M, groups], 1 -> [groups, M]
-  int32_t remap;       // workgroup -> row-tile order, see tile_of_block
-  int32_t remap_shift; // log2(remap) when remap >= 2 (remap is a power of two)
+  // bits 0-4 waves per row, 5-9 row groups per workgroup, 10-16 remap (see
+  // tile_of_block), 17-19 log2(remap) when remap >= 2, 20 column-major scales
+  // ([groups, M]), 21 wide scale stores allowed (RG_WIDE_SCALES: M % rpb == 0
+  // and the scale pointer aligned to rpb words).
+  uint32_t cfg;
   int32_t wpr_magic;   // ceil(2^16 / wpr): wave / wpr == (wave * wpr_magic) >> 16 for wave < 64
-  int32_t wide_ok;     // RG_WIDE_SCALES: M % rpb == 0 and the scale pointer aligned to rpb words
-  // Multi-input form only (fagq_rows_parts): x = x_parts[0] + ... + x_parts[nparts - 1].
+
+  __host__ __device__ int wpr() const { return (int)(cfg & 31u); }
+  __host__ __device__ int rpb() const { return (int)((cfg >> 5) & 31u); }
+  __host__ __device__ int remap() const { return (int)((cfg >> 10) & 127u); }
+  __host__ __device__ int remap_shift() const { return (int)((cfg >> 17) & 7u); }
+  __host__ __device__ int col_major() const { return (int)((cfg >> 20) & 1u); }
+  __host__ __device__ int wide_ok() const { return (int)((cfg >> 21) & 1u); }
+  __host__ __device__ static uint32_t pack_cfg(int wpr, int rpb, int remap, int remap_shift,
+                                               int col_major, int wide_ok) {
+    return (uint32_t)wpr | ((uint32_t)rpb << 5) | ((uint32_t)remap << 10) |
+           ((uint32_t)remap_shift << 17) | ((uint32_t)col_major << 20) | ((uint32_t)wide_ok << 21);
+  }
+};
+static_assert(sizeof(KArgs) == 80, "kernel argument size");
+
+// Multi-input form (fagq_rows_parts): x = x_parts[0] + ... + x_parts[nparts - 1].
+struct PArgs {
+  KArgs k;
   int32_t nparts;
   const uint16_t* xparts[kMaxParts];
 };
@@ -334,7 +353,7 @@ __device__ __forceinline__ void row_rsrc_out(const KArgs& a, const WaveCtx& w, i
   r.res_out = make_rsrc(a.res_out + e, cols * 2u);
   if constexpr (NORM) r.norm = make_rsrc(a.norm_out + e, cols * 2u);
   r.q = make_rsrc(a.q + e, cols);
-  const ScaleSpan sp = scale_span(a.M, a.groups, a.col_major, sb, row, ok, w.c0 / G, w.cols != 0);
+  const ScaleSpan sp = scale_span(a.M, a.groups, a.col_major(), sb, row, ok, w.c0 / G, w.cols != 0);
   r.scale = make_rsrc(a.scale + sp.base * sb, sp.bytes);
   r.ngroups = sp.ngroups;
   r.gstride = sp.gstride;
@@ -424,16 +443,17 @@ __device__ __forceinline__ void unpack_x(const u32x4 (&xv)[NS], float (&xs)[NS][
 // Multi-input form, phase 1: the row's partial tensors of x (the same row
 // and columns of each) and residual.  Parts past nparts are not loaded.
 template <int NS>
-__device__ __forceinline__ void load_row_parts(const KArgs& a, const WaveCtx& w, int64_t row,
+__device__ __forceinline__ void load_row_parts(const PArgs& pa, const WaveCtx& w, int64_t row,
                                                const RowRsrc& rr, int lane,
                                                u32x4 (&xv)[kMaxParts][NS], u32x4 (&rv)[NS]) {
+  const KArgs& a = pa.k;
   const bool ok = row < a.M;
   const int64_t e = (ok ? row : 0) * (int64_t)a.D + w.c0;
   const uint32_t cols = ok ? w.cols : 0u;
 #pragma unroll
   for (int p = 0; p < kMaxParts; ++p) {
-    if (p < a.nparts) {
-      const rsrc_t rp = make_rsrc(a.xparts[p] + e, cols * 2u);
+    if (p < pa.nparts) {
+      const rsrc_t rp = make_rsrc(pa.xparts[p] + e, cols * 2u);
 #pragma unroll
       for (int k = 0; k < NS; ++k)
         xv[p][k] = __builtin_amdgcn_raw_buffer_load_b128(rp, lane * 16 + k * 1024, 0, kNonTemporal);
@@ -595,12 +615,12 @@ fagq_rows(const KArgs a) {
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wpr = a.wpr;
-  const int blk = tile_of_block((int)blockIdx.x, (int)gridDim.x, a.remap, a.remap_shift);
+  const int wpr = a.wpr();
+  const int blk = tile_of_block((int)blockIdx.x, (int)gridDim.x, a.remap(), a.remap_shift());
   // Row group within the workgroup and wave within the row (wpr * rpb waves).
   const int rib = (wave * a.wpr_magic) >> 16;
   const int part = wave - rib * wpr;
-  const int64_t row0 = (int64_t)blk * a.rpb;
+  const int64_t row0 = (int64_t)blk * a.rpb();
   const int64_t row = row0 + rib;
   WaveCtx wc;
   wc.lane = lane;
@@ -679,13 +699,13 @@ fagq_rows(const KArgs a) {
   }
 
   if constexpr (WIDE) {
-    const int R = a.rpb;
-    const bool wide = a.wide_ok && row0 + R <= a.M;
+    const int R = a.rpb();
+    const bool wide = a.wide_ok() && row0 + R <= a.M;
     if (wide) {
       row_out<NS, LPG, QF, SF, NORM, false>(rr, lane, (uint32_t)wc.gl, w, gmax, inv, inv_q);
       if (rib == 0 && (lane & (LPG - 1)) == 0) {
         // Scale words g * M + row0 .. + R - 1, offsets below M * groups * sb.
-        const rsrc_t rs = make_rsrc(a.scale, (uint32_t)(a.M * a.groups * (int64_t)sb));
+        const rsrc_t rs = make_rsrc(a.scale, (uint32_t)((int64_t)a.M * a.groups * sb));
 #pragma unroll
         for (int k = 0; k < NS; ++k) {
           const int g = g0 + k * GPS + wc.gl;
@@ -731,7 +751,8 @@ fagq_rows(const KArgs a) {
 // loads of a wave's steps are all in flight at once).
 template <int NS, int LPG, int QF, int SF>
 __global__ void __launch_bounds__(1024)
-fagq_rows_parts(const KArgs a) {
+fagq_rows_parts(const PArgs pa) {
+  const KArgs& a = pa.k;
   static_assert(NS >= 1 && NS <= kMaxStepsParts, "steps per wave");
   constexpr int G = LPG * 8;
   __shared__ double s_part[kMaxWavesPerBlock];
@@ -739,11 +760,11 @@ fagq_rows_parts(const KArgs a) {
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wpr = a.wpr;
-  const int blk = tile_of_block((int)blockIdx.x, (int)gridDim.x, a.remap, a.remap_shift);
+  const int wpr = a.wpr();
+  const int blk = tile_of_block((int)blockIdx.x, (int)gridDim.x, a.remap(), a.remap_shift());
   const int rib = (wave * a.wpr_magic) >> 16;
   const int part = wave - rib * wpr;
-  const int64_t row = (int64_t)blk * a.rpb + rib;
+  const int64_t row = (int64_t)blk * a.rpb() + rib;
   WaveCtx wc;
   wc.lane = lane;
   wc.c0 = part * (NS * kStepCols);
@@ -753,7 +774,7 @@ fagq_rows_parts(const KArgs a) {
   u32x4 xv[kMaxParts][NS], rv[NS];
   RowRsrc rr;
   row_rsrc_in(a, wc, row, rr);
-  load_row_parts<NS>(a, wc, row, rr, lane, xv, rv);
+  load_row_parts<NS>(pa, wc, row, rr, lane, xv, rv);
   u32x4 gv[NS];
   load_gamma<NS>(a, wc, lane, gv);
   row_rsrc_out<SF, false>(a, wc, row, G, rr);
@@ -763,7 +784,7 @@ fagq_rows_parts(const KArgs a) {
   double ss;
   {
     float xs[NS][8];
-    sum_parts<NS>(a.nparts, xv, xs);
+    sum_parts<NS>(pa.nparts, xv, xs);
     ss = row_sum<NS>(rr, lane, xs, rv, w);
   }
   row_weight<NS, LPG>(w, gv, gmax);

@@ -593,7 +593,7 @@ FAGQ_API int fagq_mla_bwd_launch(const void* q, const void* c_kv, const void* ou
   if (e != hipSuccess) return -(int)e;
   e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_suffix_scan),
                       dim3((unsigned)g.nblk, (unsigned)B), dim3(kWide), args, 0, st);
-  return e == hipSuccess ? FAGQ_OK : -(int)e;
+  return launch_status(e);
 }
 
 }  // extern "C"

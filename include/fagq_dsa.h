@@ -30,19 +30,22 @@
 extern "C" {
 #endif
 
-#define FAGQ_DSA_MAX_NB 4096
+#define FAGQ_DSA_MAX_NB (1 << 28)
 #define FAGQ_DSA_MAX_TOP_K 256
 
 enum fagq_dsa_scores { FAGQ_DSA_F32 = 0, FAGQ_DSA_BF16 = 1 };
 enum fagq_dsa_index { FAGQ_DSA_I32 = 0, FAGQ_DSA_I64 = 1 };
 
-/* scores      [B, H, Q, NB] fp32 or bf16 (scores_dtype), 16-byte aligned,
- *             NB * element size a multiple of 16 (NB % 4 fp32, NB % 8 bf16)
+/* scores      [B, H, Q, NB] fp32 or bf16 (scores_dtype), aligned to its element
+ *             size (rows read as 16-byte vectors when the pointer is 16-byte
+ *             aligned and NB * element size is a multiple of 16, else one score
+ *             per load)
  * page_table  int32 [B, NB]
  * q_pos       [B, Q], kv_lens [B]: int32 or int64 (index_dtype)
  * out_blocks, out_pages  int32 [B, H, Q, top_k]
  * 1 <= NB <= FAGQ_DSA_MAX_NB, 1 <= top_k <= FAGQ_DSA_MAX_TOP_K, 1 <= block_size < 2^31,
- * B and H <= 65535, Q < 2^24 (FAGQ_E_TOO_LARGE otherwise) */
+ * B and H <= 65535, B * H * Q < 2^31, Q * 64 * min(16, ceil(NB / 1024)) < 2^32
+ * (FAGQ_E_TOO_LARGE otherwise) */
 FAGQ_API int fagq_dsa_topk_launch(const void* scores, int scores_dtype, const void* page_table,
                                   const void* q_pos, const void* kv_lens, int index_dtype,
                                   void* out_blocks, void* out_pages, int64_t B, int64_t H,

@@ -24,12 +24,15 @@ bf16 tensors are passed as their uint16 bit patterns.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 import numpy as np
 
 ORACLE_DIR = Path(__file__).resolve().parent
-LIB_PATH = ORACLE_DIR / "libfagq_oracle.so"
+# FAGQ_TEST_ORACLE_LIBRARY: the tests' sanitizer run loads a sanitizer build of
+# the same sources instead.
+LIB_PATH = Path(os.environ.get("FAGQ_TEST_ORACLE_LIBRARY") or ORACLE_DIR / "libfagq_oracle.so")
 
 Q_INT8, Q_FP8 = 0, 1
 S_F32, S_UE8M0 = 0, 1

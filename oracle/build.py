@@ -37,5 +37,28 @@ def build(verbose: bool = False) -> Path:
     return LIB
 
 
+def build_sanitized(verbose: bool = False) -> Path:
+    """The same sources built with clang's AddressSanitizer and
+    UndefinedBehaviorSanitizer into oracle/_build_san/libfagq_oracle.so, for the
+    CPU tests' sanitizer run (which preloads clang's shared ASan runtime, the
+    one the product library's sanitizer build uses too)."""
+    rocm = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+    clang = rocm / "llvm" / "bin" / "clang"
+    out_dir = ORACLE_DIR / "_build_san"
+    out_dir.mkdir(exist_ok=True)
+    out = out_dir / "libfagq_oracle.so"
+    cflags = [f for f in CFLAGS if f != "-O2"] + ["-O1", "-g", "-fno-omit-frame-pointer",
+                                                  "-fsanitize=address,undefined",
+                                                  "-fno-sanitize-recover=undefined", "-shared-libsan"]
+    cmd = [str(clang), *cflags, "-o", str(out), *[str(s) for s in SRCS], "-lm",
+           f"-Wl,-rpath,{rocm / 'llvm' / 'lib'}"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"sanitized oracle build failed:\n{res.stdout}")
+    return out
+
+
 if __name__ == "__main__":
     print(build(verbose=True))

@@ -1,3 +1,4 @@
+import os
 import sys
 from pathlib import Path
 
@@ -21,6 +22,12 @@ def pkg():
 
 @pytest.fixture(scope="session")
 def lib(pkg):
+    # FAGQ_TEST_LIBRARY: the sanitizer run (tests/test_sanitizers.py) points the
+    # CPU tests at a host-sanitizer build of the same sources.
+    alt = os.environ.get("FAGQ_TEST_LIBRARY")
+    if alt:
+        from fagq_mi355x import _lib
+        _lib._lib = _lib.load(alt)
     return pkg.load_library()
 
 

@@ -58,18 +58,28 @@ def test_route_invariants(pkg, M, D, ue8m0, col):
     assert wpr * ns >= steps > (wpr - 1) * ns          # every wave owns >= 1 column
     assert r["block_threads"] == 64 * wpr * rpb <= 1024
     assert r["grid_blocks"] * rpb >= M > (r["grid_blocks"] - 1) * rpb
-    assert r["lds_bytes"] == 0
+    assert r["lds_bytes"] in (0, 49152)
     if mode:
         assert wpr * ns <= 16                            # gamma fits the LDS buffer
     if mode == 2:
         assert col and rpb in (2, 4)
-    wide = M >= 1024 and col and not ue8m0 and 12 <= steps <= 16
-    if wide:
-        # fp32 column-major scales at 6144 <= D <= 8192: two rows per workgroup
-        # of 4-step waves, shared gamma, wide scale stores, 16 rows per XCD chunk.
-        assert (ns, rpb, mode, r["xcd_remap"]) == (4, 2, 2, 8)
-    elif M >= 1024 and 2 <= steps <= 16:
+    prefill = M >= 1024
+    if prefill and 12 <= steps <= 16:
+        if col:
+            # 6144 <= D <= 8192, column-major: two rows per workgroup of 4-step
+            # waves, shared gamma, wide scale stores, 16 rows per XCD chunk
+            # (fp32) or 32 (ue8m0).
+            assert (ns, rpb, mode, r["xcd_remap"]) == (4, 2, 2, 8 if not ue8m0 else 16)
+        elif steps >= 15:
+            assert (ns, rpb, mode) == (4, 2, 1)
+        else:
+            assert (ns, rpb, mode, r["lds_bytes"]) == (2, 1, 0, 49152)
+    elif prefill and 5 <= steps <= 8:
+        assert (wpr, ns, mode) == (steps, 1, 0)          # 1-step waves
+    elif prefill and 2 <= steps <= 16:
         assert (ns, mode) == (2, 0)                      # prefill: 2-step waves
+    if not (prefill and 12 <= steps <= 14 and not col):
+        assert r["lds_bytes"] == 0
     if M <= 32 and D <= 8192:
         assert (wpr, ns, mode) == (steps, 1, 0)          # decode: one step per wave
     if not col:
@@ -314,9 +324,12 @@ def dsa_call(lib, **kw):
     (dict(ob=None), 1), (dict(op=None), 1),
     (dict(sd=2), 5), (dict(idx=-1), 5),
     (dict(B=-1), 2), (dict(NB=0), 2), (dict(bs=0), 2), (dict(k=0), 2),
-    (dict(NB=4097), 7), (dict(k=257), 7), (dict(bs=1 << 31), 7),
-    (dict(H=65536), 7), (dict(B=65536), 7), (dict(Q=1 << 24), 7),
-    (dict(s=ctypes.c_void_p(BASE + 8)), 4), (dict(NB=1022), 4), (dict(NB=1020, sd=1), 4),
+    (dict(NB=(1 << 28) + 1), 7), (dict(k=257), 7), (dict(bs=1 << 31), 7),
+    (dict(H=65536), 7), (dict(B=65536), 7),
+    (dict(Q=1 << 26), 7),                          # Q x 64 work-items (1 wave) reach 2^32
+    (dict(Q=1 << 22, NB=16384, B=1, H=1), 7),      # Q x 64 x 16 waves reach 2^32
+    (dict(Q=1 << 29), 7),                          # B x H x Q >= 2^31
+    (dict(s=ctypes.c_void_p(BASE + 2)), 4), (dict(s=ctypes.c_void_p(BASE + 1), sd=1), 4),
     (dict(qp=ctypes.c_void_p(BASE + 0x2_0000_0004), idx=1), 4),
     (dict(op=fake(4)), 9), (dict(op=ctypes.c_void_p(BASE + 0x4_0000_0100)), 9),
     (dict(Q=0), 0),

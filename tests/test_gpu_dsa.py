@@ -143,3 +143,44 @@ def test_dsa_python_errors(pkg, gpu):
         pkg.dsa_topk_page_table_transform(s, pt, pos, kv, ob[..., :4], op, 16, 8)
     with pytest.raises(pkg.FagqError):
         pkg.dsa_topk_page_table_transform(s, pt, pos, kv, ob, op, 0, 8)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("NB,k", [(4095, 128), (6000, 64), (8192, 128), (16384, 256), (1021, 32)])
+def test_dsa_any_row_length(pkg, gpu, dtype, NB, k):
+    """Row lengths that are not a multiple of the 16-byte vector (per-score
+    loads) and rows of up to 16 chunks of 1024 blocks (16 waves)."""
+    s, pt, pos, kv = case(NB + k, B=2, H=2, Q=12, NB=NB, dtype=dtype)
+    check(pkg, gpu, s, pt, pos, kv, 16, k, f"NB={NB} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("NB,ties", [(40000, None), (40001, "heavy"), (70000, "round"),
+                                     (20480, "outlier")])
+def test_dsa_rows_longer_than_16_chunks(pkg, gpu, dtype, NB, ties):
+    """More than 16 chunks: each wave walks several chunks and reads the row
+    again in every pass (also through the radix refinement with ties)."""
+    s, pt, pos, kv = case(NB, B=1, H=2, Q=6, NB=NB, dtype=dtype, ties=ties)
+    check(pkg, gpu, s, pt, pos, kv, 8, 128, f"NB={NB} ties={ties} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("offset", [1, 2, 3])
+def test_dsa_scores_not_16_byte_aligned(pkg, gpu, dtype, offset):
+    """A scores tensor that starts 1..3 elements into its allocation: rows are
+    read one score per load, with the same result."""
+    s, pt, pos, kv = case(50 + offset, B=2, H=2, Q=10, NB=2048, dtype=dtype)
+    flat = torch.empty(s.numel() + offset, dtype=dtype)
+    flat[offset:] = s.reshape(-1)
+    note(f"dsa unaligned offset={offset} {dtype}")
+    B, H, Q, NB = s.shape
+    sd = torch.empty(s.numel() + offset, dtype=dtype, device=gpu)[offset:].view(B, H, Q, NB)
+    sd.copy_(s.to(gpu))
+    assert sd.data_ptr() % 16 != 0
+    ob = torch.full((B, H, Q, 64), -7, dtype=torch.int32, device=gpu)
+    op = torch.full((B, H, Q, 64), -7, dtype=torch.int32, device=gpu)
+    pkg.dsa_topk_page_table_transform(sd, pt.to(gpu), pos.to(gpu), kv.to(gpu), ob, op, 16, 64)
+    torch.cuda.synchronize()
+    s_np = s.view(torch.uint16).numpy() if dtype == torch.bfloat16 else s.numpy()
+    rb, rp = oracle.dsa_topk(s_np, pt.numpy(), pos.numpy(), kv.numpy(), 16, 64)
+    assert np.array_equal(ob.cpu().numpy(), rb) and np.array_equal(op.cpu().numpy(), rp)

@@ -1,0 +1,65 @@
+"""A kernel launch that fails is reported, not swallowed (failure
+detection).  The library is rebuilt with -DFAGQ_TEST_LAUNCH_FAILURE, a test
+seam that makes every launch report hipErrorLaunchFailure (719) and skips the
+device check, so the whole path runs on a machine without a GPU: every entry
+point must return -719 after validation passes, keep its validation errors
+and no-op cases unchanged, and the Python layer must raise FagqError naming a
+HIP error."""
+import ctypes
+import shutil
+
+import pytest
+
+HIP_ERROR_LAUNCH_FAILURE = 719
+BASE = 0x10_0000_0000
+
+
+def fake(i):
+    return ctypes.c_void_p(BASE + i * 0x1_0000_0000)
+
+
+@pytest.fixture(scope="module")
+def seam(pkg):
+    if not shutil.which("hipcc") and not __import__("os").path.exists("/opt/rocm/bin/hipcc"):
+        pytest.skip("hipcc not available")
+    import __graft_entry__ as ge
+    from fagq_mi355x import _lib
+    build = ge._load_module("fagq_mi355x_build", ge.PKG_DIR / "build.py")
+    return _lib.load(build.build_variant("launch_failure", defines=("FAGQ_TEST_LAUNCH_FAILURE",)))
+
+
+def test_operator_launch_failure_is_returned(seam):
+    args = [fake(0), fake(1), fake(2), fake(3), None, fake(4), fake(5), 8, 4096, 128, 1e-6, 1, 0, 0,
+            0, None]
+    assert seam.fagq_launch(*args) == -HIP_ERROR_LAUNCH_FAILURE
+    args[7] = 0                                   # M = 0: nothing launched
+    assert seam.fagq_launch(*args) == 0
+    args[7], args[0] = 8, None                    # validation still comes first
+    assert seam.fagq_launch(*args) == 1
+
+
+def test_every_launching_entry_point_reports_it(seam):
+    st = seam.fagq_launch_mapped(fake(0), fake(1), fake(2), fake(3), None, fake(4), fake(5), 8, 7168,
+                                 128, 1e-6, 1, 0, 1, 0, 4, 2, 2, 8, 0, None)
+    assert st == -HIP_ERROR_LAUNCH_FAILURE
+    parts = (ctypes.c_void_p * 2)(BASE + 6 * 0x1_0000_0000, BASE + 7 * 0x1_0000_0000)
+    st = seam.fagq_launch_parts(ctypes.cast(parts, ctypes.c_void_p), 2, fake(1), fake(2), fake(3),
+                                fake(4), fake(5), 8, 4096, 128, 1e-6, 1, 0, 0, 0, None)
+    assert st == -HIP_ERROR_LAUNCH_FAILURE
+    assert seam.fagq_diag_stream(fake(0), fake(1), 4096, 0, None) == -HIP_ERROR_LAUNCH_FAILURE
+    assert seam.fagq_diag_encode(fake(0), fake(1), 64, 1, 0, 0, None) == -HIP_ERROR_LAUNCH_FAILURE
+    st = seam.fagq_dsa_topk_launch(fake(0), 0, fake(1), fake(2), fake(3), 0, fake(4), fake(5), 1, 2,
+                                   4, 1024, 64, 32, None)
+    assert st == -HIP_ERROR_LAUNCH_FAILURE
+    st = seam.fagq_gemm_launch(fake(0), fake(1), fake(2), fake(3), fake(4), 256, 256, 1024, 0, 1, 0,
+                               None)
+    assert st == -HIP_ERROR_LAUNCH_FAILURE
+
+
+def test_python_layer_raises_on_it(seam):
+    from fagq_mi355x import _lib
+    st = seam.fagq_launch(fake(0), fake(1), fake(2), fake(3), None, fake(4), fake(5), 8, 4096, 128,
+                          1e-6, 1, 0, 0, 0, None)
+    with pytest.raises(_lib.FagqError) as e:
+        _lib.check(st)
+    assert e.value.status == -HIP_ERROR_LAUNCH_FAILURE and "HIP error" in str(e.value)
