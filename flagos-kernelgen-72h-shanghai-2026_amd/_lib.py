@@ -69,6 +69,7 @@ SIGNATURES = {
     "fagq_gemm_query_route": ([_I64, _I64, _I64, ctypes.POINTER(GemmRoute)], _I),
     "fagq_mla_bwd_workspace_bytes": ([_I64, _I64, _I64], _I64),
     "fagq_mla_bwd_launch": ([_P] * 8 + [_I64] * 5 + [_F, _I, _I, _P], _I),
+    "fagq_mla_bwd_launch_noalloc": ([_P] * 7 + [_I64] * 4 + [_F, _I, _I, _P], _I),
 }
 
 

@@ -38,6 +38,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "fagq.h"
 #include "fagq_dispatch.hpp"
 #include "fagq_mla.h"
@@ -517,24 +520,36 @@ FAGQ_API int64_t fagq_mla_bwd_workspace_bytes(int64_t B, int64_t S, int64_t D) {
   return workspace_bytes(B, S, D);
 }
 
-FAGQ_API int fagq_mla_bwd_launch(const void* q, const void* c_kv, const void* out, const void* dout,
-                                 const float* lse, void* dq, void* dc_kv, void* workspace,
-                                 int64_t ws_bytes, int64_t B, int64_t H, int64_t S, int64_t D,
-                                 float sm_scale, int dq_dtype, int dc_dtype, void* stream) {
-  if (!q || !c_kv || !out || !dout || !lse || !dq || !dc_kv || !workspace) return FAGQ_E_NULL;
+}  // extern "C"
+
+namespace fagq {
+namespace mla {
+namespace {
+
+// Argument checks shared by both entry points (everything but the workspace);
+// *need receives the workspace bytes the call uses.
+int check_args(const void* q, const void* c_kv, const void* out, const void* dout,
+               const float* lse, void* dq, void* dc_kv, int64_t B, int64_t H, int64_t S,
+               int64_t D, float sm_scale, int dq_dtype, int dc_dtype, int64_t* need) {
+  if (!q || !c_kv || !out || !dout || !lse || !dq || !dc_kv) return FAGQ_E_NULL;
   if ((dq_dtype != FAGQ_MLA_F32 && dq_dtype != FAGQ_MLA_BF16) ||
       (dc_dtype != FAGQ_MLA_F32 && dc_dtype != FAGQ_MLA_BF16))
     return FAGQ_E_FORMAT;
   if (B < 0 || H < 1 || S < 1 || D < 64 || D % 64 != 0 || !(sm_scale == sm_scale))
     return FAGQ_E_SHAPE;
   if (D > kMaxD || B > 65535 || H > 65535 || H * S * D * 4 >= (1ll << 32)) return FAGQ_E_TOO_LARGE;
-  const int64_t need = workspace_bytes(B, S, D);
-  if (need < 0) return FAGQ_E_TOO_LARGE;
-  if (ws_bytes < need) return FAGQ_E_SHAPE;
+  *need = workspace_bytes(B, S, D);
+  if (*need < 0) return FAGQ_E_TOO_LARGE;
   if (!aligned(q, 16) || !aligned(c_kv, 16) || !aligned(out, 16) || !aligned(dout, 16) ||
-      !aligned(lse, 4) || !aligned(dq, 16) || !aligned(dc_kv, 16) || !aligned(workspace, 16))
+      !aligned(lse, 4) || !aligned(dq, 16) || !aligned(dc_kv, 16))
     return FAGQ_E_ALIGN;
-  if (B == 0) return FAGQ_OK;
+  return FAGQ_OK;
+}
+
+// Overlap checks with the workspace, the device check and the three launches.
+int launch(const void* q, const void* c_kv, const void* out, const void* dout, const float* lse,
+           void* dq, void* dc_kv, void* workspace, int64_t need, int64_t B, int64_t H, int64_t S,
+           int64_t D, float sm_scale, int dq_dtype, int dc_dtype, void* stream) {
   const int64_t nq = B * H * S * D * 2, nc = B * S * D * 2, nl = B * H * S * 4;
   const int64_t ndq = B * H * S * D * (dq_dtype == FAGQ_MLA_BF16 ? 2 : 4);
   const int64_t ndc = B * S * D * (dc_dtype == FAGQ_MLA_BF16 ? 2 : 4);
@@ -594,6 +609,79 @@ FAGQ_API int fagq_mla_bwd_launch(const void* q, const void* c_kv, const void* ou
   e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_suffix_scan),
                       dim3((unsigned)g.nblk, (unsigned)B), dim3(kWide), args, 0, st);
   return launch_status(e);
+}
+
+// The workspace of fagq_mla_bwd_launch_noalloc: one array per GPU the library
+// runs on, held until the process ends.  Host code never passes `scratch`
+// itself to a kernel (in host code the name is a stand-in, not the device
+// address): the device address is looked up once per device, with that
+// device current, and used instead.
+static __device__ __align__(256) uint8_t scratch[FAGQ_MLA_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void*> g_scratch_addr[kMaxScratchDevices];
+std::mutex g_scratch_mu;
+
+// Device address of the current device's `scratch`; FAGQ_OK or an error.
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return -(int)e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return FAGQ_E_DEVICE;
+  void* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return -(int)e;
+      if (!p) return FAGQ_E_DEVICE;
+      g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return FAGQ_OK;
+}
+
+}  // namespace
+}  // namespace mla
+}  // namespace fagq
+
+extern "C" {
+
+FAGQ_API int fagq_mla_bwd_launch(const void* q, const void* c_kv, const void* out, const void* dout,
+                                 const float* lse, void* dq, void* dc_kv, void* workspace,
+                                 int64_t ws_bytes, int64_t B, int64_t H, int64_t S, int64_t D,
+                                 float sm_scale, int dq_dtype, int dc_dtype, void* stream) {
+  int64_t need = 0;
+  const int v = check_args(q, c_kv, out, dout, lse, dq, dc_kv, B, H, S, D, sm_scale, dq_dtype,
+                           dc_dtype, &need);
+  if (v != FAGQ_OK) return v;
+  if (!workspace) return FAGQ_E_NULL;
+  if (ws_bytes < need) return FAGQ_E_SHAPE;
+  if (!aligned(workspace, 16)) return FAGQ_E_ALIGN;
+  if (B == 0) return FAGQ_OK;
+  return launch(q, c_kv, out, dout, lse, dq, dc_kv, workspace, need, B, H, S, D, sm_scale,
+                dq_dtype, dc_dtype, stream);
+}
+
+FAGQ_API int fagq_mla_bwd_launch_noalloc(const void* q, const void* c_kv, const void* out,
+                                         const void* dout, const float* lse, void* dq,
+                                         void* dc_kv, int64_t B, int64_t H, int64_t S, int64_t D,
+                                         float sm_scale, int dq_dtype, int dc_dtype, void* stream) {
+  int64_t need = 0;
+  const int v = check_args(q, c_kv, out, dout, lse, dq, dc_kv, B, H, S, D, sm_scale, dq_dtype,
+                           dc_dtype, &need);
+  if (v != FAGQ_OK) return v;
+  if (need > FAGQ_MLA_SCRATCH_BYTES) return FAGQ_E_TOO_LARGE;
+  if (B == 0) return FAGQ_OK;
+  const int dcheck = device_check();
+  if (dcheck != FAGQ_OK) return dcheck;
+  void* ws = nullptr;
+  const int sa = scratch_address(&ws);
+  if (sa != FAGQ_OK) return sa;
+  return launch(q, c_kv, out, dout, lse, dq, dc_kv, ws, need, B, H, S, D, sm_scale, dq_dtype,
+                dc_dtype, stream);
 }
 
 }  // extern "C"

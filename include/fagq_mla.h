@@ -57,6 +57,27 @@ FAGQ_API int fagq_mla_bwd_launch(const void* q, const void* c_kv, const void* ou
                                  int64_t D, float sm_scale, int dq_dtype, int dc_dtype,
                                  void* stream);
 
+/* Scratch bytes fagq_mla_bwd_launch_noalloc holds on each GPU it runs on. */
+#define FAGQ_MLA_SCRATCH_BYTES (32ll << 20)
+
+/* fagq_mla_bwd_launch without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference: its
+ * operator allocates its head-sum buffer per call.  The workspace is a
+ * library-owned array of FAGQ_MLA_SCRATCH_BYTES per GPU, created with the
+ * library's code on that GPU and held until the process ends; this call
+ * allocates nothing.  Calls whose workspace (fagq_mla_bwd_workspace_bytes)
+ * exceeds it return FAGQ_E_TOO_LARGE.  Every call on a GPU shares that GPU's
+ * array: calls that overlap on one GPU (other streams, or other host threads)
+ * race and must be ordered by the caller.  Nothing needs clearing between
+ * calls: every workspace word a call reads, the same call has written first.
+ * Other arguments and results as fagq_mla_bwd_launch. */
+FAGQ_API int fagq_mla_bwd_launch_noalloc(const void* q, const void* c_kv, const void* out,
+                                         const void* dout, const float* lse, void* dq,
+                                         void* dc_kv, int64_t B, int64_t H, int64_t S, int64_t D,
+                                         float sm_scale, int dq_dtype, int dc_dtype,
+                                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif
