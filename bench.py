@@ -91,6 +91,37 @@ def timed_region(torch, dev, stream, step, steps: int):
     return e0.elapsed_time(e1) / steps, (t1 - t0) * 1e3 / steps
 
 
+def heat(torch, dev, step, ms: float) -> None:
+    """Runs step back to back for ms milliseconds (synchronising every 64 calls)."""
+    t_end = time.perf_counter() + ms * 1e-3
+    i = 0
+    while time.perf_counter() < t_end:
+        step(i)
+        i += 1
+        if i % 64 == 0:
+            torch.cuda.synchronize(dev)
+    torch.cuda.synchronize(dev)
+
+
+def steady_region(args, torch, dev, stream, step):
+    """Device ms per step of K more steps after --steady-ms of load (None when
+    disabled).  Reported beside value, never as it: the device's clocks settle
+    over the first tens of milliseconds of load, which a short warm-up does not
+    cover."""
+    if args.steady_ms <= 0:
+        return None
+    heat(torch, dev, step, args.steady_ms)
+    return timed_region(torch, dev, stream, step, args.steps)[0]
+
+
+def steady_fields(steady_ms, nbytes):
+    if steady_ms is None:
+        return {"us_per_call_steady_state": None, "steady_state_pct_of_peak": None}
+    return {"us_per_call_steady_state": round(steady_ms * 1e3, 2),
+            "steady_state_pct_of_peak": round(100.0 * nbytes / (steady_ms * 1e-3) / 1e9 /
+                                              PEAK_HBM_GBS, 2)}
+
+
 def cpu_model() -> str:
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -139,6 +170,12 @@ def parse_args():
     p.add_argument("--mfma-peak", action="store_true",
                    help="instead: time the library's register-only issue-rate probe of the fp8 "
                         "GEMM's matrix instruction (the compute ceiling its rate is compared with)")
+    p.add_argument("--steady-ms", type=float, default=300.0,
+                   help="after the timed region: run the operator this long, then time K more "
+                        "steps (us_per_call_steady_state; 0 disables)")
+    p.add_argument("--rows-sweep", default="",
+                   help="instead: comma-separated row counts; the config's operator at each, after "
+                        "a warm-up of the device, with a least-squares line of time against bytes")
     return p.parse_args()
 
 
@@ -242,6 +279,8 @@ def main() -> int:
     if name in PARTS_CONFIGS:
         return parts_bench(args, torch, pkg, PARTS_CONFIGS[name])
     w = CONFIGS[name]
+    if args.rows_sweep:
+        return rows_sweep(args, torch, pkg, w)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     lib = pkg.load_library()
@@ -274,6 +313,8 @@ def main() -> int:
     # Timed region: K back-to-back steps; device time from one HIP event pair on the
     # launch stream, host wall time over the same region.
     kern_ms, wall_ms = timed_region(torch, dev, stream, step, args.steps)
+
+    steady_ms = steady_region(args, torch, dev, stream, step)
 
     # Device time per call without host launch gaps: a HIP graph of
     # consecutive launches, replayed (matters when a call is shorter than its
@@ -333,6 +374,7 @@ def main() -> int:
         "us_per_call": round(kern_ms * 1e3, 2),
         "us_per_call_host_wall": round(wall_ms * 1e3, 2),
         "us_per_call_graph_replay": None if graph_us is None else round(graph_us, 2),
+        **steady_fields(steady_ms, set_bytes),
         "pct_of_peak": round(100.0 * value / PEAK_HBM_GBS, 2),
         "rows_per_s": round(w.M / (kern_ms * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": PEAK_HBM_GBS,
@@ -350,6 +392,67 @@ def main() -> int:
 
 
 CPU_CONFIG = "cpu_ref_128x4096"   # the CPU PyTorch reference path
+
+
+def rows_sweep(args, torch, pkg, w0) -> int:
+    """The config's operator at each row count of --rows-sweep (same D, formats
+    and distribution), in one process: 300 ms of warm-up on the largest size,
+    then, in 5 interleaved rounds, K steps per size timed by one event pair
+    (buffer sets rotated past the MALL); median per size.  One JSON line per
+    size, then a least-squares line t = t0 + bytes / bw over the sizes whose
+    time is above 4 x the smallest (the launch-bound sizes excluded)."""
+    import dataclasses
+    from fagq_mi355x.workloads import make_inputs
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    sizes = sorted(int(v) for v in args.rows_sweep.split(","))
+    runs = []
+    for M in sizes:
+        w = dataclasses.replace(w0, name=f"{w0.name}@M={M}", M=M)
+        x, res, gamma = make_inputs(w)
+        nb = w.algorithmic_bytes()
+        nsets = max(2, min(64, math.ceil(ROTATE_BYTES / nb) + 1))
+        xd, rd, gd = x.to(dev), res.to(dev), gamma.to(dev)
+        sets = []
+        for i in range(nsets):
+            xs, rs = (xd, rd) if i == 0 else (xd.clone(), rd.clone())
+            sets.append((xs, rs, torch.empty_like(rs),
+                         torch.empty((M, w.D), dtype=w.out_dtype, device=dev),
+                         pkg.empty_scales(M, w.groups, ue8m0=w.scale_ue8m0,
+                                          col_major=w.scale_col_major, device=dev)))
+
+        def step(i, sets=sets, w=w):
+            xs, rs, ro, q, sc = sets[i % len(sets)]
+            pkg.fused_add_rmsnorm_group_quant(
+                xs, rs, gd, ro, None, q, sc, w.eps, w.group_size,
+                rounding=w.rounding if w.out_dtype == torch.int8 else None)
+        runs.append((M, nb, step, sets, gd))
+    heat(torch, dev, runs[-1][2], 300.0)
+    times = {M: [] for M, *_ in runs}
+    for _ in range(5):
+        for M, nb, step, *_ in runs:
+            times[M].append(timed_region(torch, dev, stream, step, args.steps)[0])
+    pts = []
+    for M, nb, *_ in runs:
+        t = sorted(times[M])[2] * 1e3
+        pts.append((M, nb, t))
+        print(json.dumps({"workload": w0.name, "M": M, "D": w0.D, "algorithmic_bytes": nb,
+                          "us_per_call_median": round(t, 2),
+                          "GBps": round(nb / (t * 1e-6) / 1e9, 1),
+                          "pct_of_peak": round(100.0 * nb / (t * 1e-6) / 1e9 / PEAK_HBM_GBS, 2)}),
+              flush=True)
+    tmin = min(t for _, _, t in pts)
+    fit = [(nb, t) for _, nb, t in pts if t > 4 * tmin]
+    if len(fit) >= 2:
+        n = len(fit)
+        mx = sum(b for b, _ in fit) / n
+        my = sum(t for _, t in fit) / n
+        slope = sum((b - mx) * (t - my) for b, t in fit) / sum((b - mx) ** 2 for b, _ in fit)
+        print(json.dumps({"fit": "t = t0 + bytes / bw", "points": n,
+                          "t0_us": round(my - slope * mx, 2),
+                          "bw_GBps": round(1.0 / slope / 1e3, 1)}), flush=True)
+    return 0
 
 
 def _time_cpu(run, min_runs: int, seconds: float, max_runs: int = 1000):
@@ -484,6 +587,7 @@ def parts_bench(args, torch, pkg, w) -> int:
     for i in range(args.warmup):
         step(i)
     kern_ms, wall_ms = timed_region(torch, dev, stream, step, args.steps)
+    steady_ms = steady_region(args, torch, dev, stream, step)
     value = set_bytes / (kern_ms * 1e-3) / 1e9
     achieved = value
     out = {
@@ -504,6 +608,7 @@ def parts_bench(args, torch, pkg, w) -> int:
                    "algorithmic_bytes": set_bytes, "buffer_sets": nsets},
         "us_per_call": round(kern_ms * 1e3, 2),
         "us_per_call_host_wall": round(wall_ms * 1e3, 2),
+        **steady_fields(steady_ms, set_bytes),
         "pct_of_peak": round(100.0 * achieved / PEAK_HBM_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
@@ -593,6 +698,7 @@ def dsa_bench(args, torch, pkg, w) -> int:
     for i in range(args.warmup):
         step(i)
     kern_ms, wall_ms = timed_region(torch, dev, stream, step, args.steps)
+    steady_ms = steady_region(args, torch, dev, stream, step)
     value = nbytes / (kern_ms * 1e-3) / 1e9
     achieved = value
     out = {
@@ -613,6 +719,7 @@ def dsa_bench(args, torch, pkg, w) -> int:
                    "algorithmic_bytes": nbytes, "buffer_sets": nsets},
         "us_per_call": round(kern_ms * 1e3, 2),
         "us_per_call_host_wall": round(wall_ms * 1e3, 2),
+        **steady_fields(steady_ms, nbytes),
         "rows_per_s": round(w.rows / (kern_ms * 1e-3), 1),
         "pct_of_peak": round(100.0 * achieved / PEAK_HBM_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
@@ -662,6 +769,7 @@ def mla_bench(args, torch, pkg, w) -> int:
     for i in range(args.warmup):
         step(i)
     kern_ms, wall_ms = timed_region(torch, dev, stream, step, args.steps)
+    steady_ms = steady_region(args, torch, dev, stream, step)
     value = nbytes / (kern_ms * 1e-3) / 1e9
     achieved = value
     out_json = {
@@ -681,6 +789,7 @@ def mla_bench(args, torch, pkg, w) -> int:
                    "sm_scale": w.sm_scale, "algorithmic_bytes": nbytes, "buffer_sets": nsets},
         "us_per_call": round(kern_ms * 1e3, 2),
         "us_per_call_host_wall": round(wall_ms * 1e3, 2),
+        **steady_fields(steady_ms, nbytes),
         "pct_of_peak": round(100.0 * achieved / PEAK_HBM_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
@@ -798,6 +907,7 @@ def gemm_bench(args, torch, pkg, w) -> int:
         step(i)
     stream = torch.cuda.current_stream(dev)
     kern_ms, wall_ms = timed_region(torch, dev, stream, step, args.steps)
+    steady_ms = steady_region(args, torch, dev, stream, step)
     flops = w.flops()
     value = flops / (kern_ms * 1e-3) / 1e12
     achieved = value
@@ -822,6 +932,7 @@ def gemm_bench(args, torch, pkg, w) -> int:
                    "route": pkg.gemm_route(w.M, w.N, w.K)},
         "us_per_call": round(kern_ms * 1e3, 2),
         "us_per_call_host_wall": round(wall_ms * 1e3, 2),
+        "us_per_call_steady_state": None if steady_ms is None else round(steady_ms * 1e3, 2),
         "pct_of_peak": round(100.0 * achieved / PEAK_FP8_TFLOPS, 2),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_FP8_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP8_TFLOPS, 4),
