@@ -109,6 +109,33 @@ def load(path: str | Path | None = None) -> ctypes.CDLL:
         return lib
 
 
+_fast = None          # the bound _fagq_py.launch, once looked up
+_fast_tried = False
+
+
+def fast_launch():
+    """launch() of the CPython binding (csrc/fagq_py.cpp), bound to this
+    process's libfagq.so, or None when that module is not built or does not
+    import (the ctypes path then serves every call; both reach fagq_launch)."""
+    global _fast, _fast_tried
+    if _fast_tried:
+        return _fast
+    lib = load()          # takes _lock itself (not reentrant): before the block below
+    with _lock:
+        if not _fast_tried:
+            try:
+                from . import _fagq_py
+                _fagq_py.bind(ctypes.cast(lib.fagq_launch, ctypes.c_void_p).value)
+                _fast = _fagq_py.launch
+            except ImportError:
+                _fast = None
+            _fast_tried = True
+    return _fast
+
+
+FAST_ARG_ERROR = 1000   # _fagq_py.ARG_ERROR: a tensor argument was rejected by the binding
+
+
 def describe(status: int) -> str:
     try:
         return load().fagq_status_string(status).decode()

@@ -67,8 +67,30 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print("\n".join(lines), flush=True)
 
 
+def pyext_path() -> Path:
+    import sysconfig
+    return PKG_DIR / ("_fagq_py" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def pyext_command() -> list[str]:
+    """g++ line of the CPython binding (csrc/fagq_py.cpp) against torch's headers.
+    Host code only: it calls fagq_launch through a pointer it is handed at import."""
+    import sysconfig
+    import torch
+    from torch.utils import cpp_extension
+    abi = int(bool(torch._C._GLIBCXX_USE_CXX11_ABI))
+    return ["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-fvisibility=hidden",
+            f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+            *[f"-I{p}" for p in cpp_extension.include_paths()],
+            f"-I{sysconfig.get_paths()['include']}", f"-I{INCLUDE}",
+            str(CSRC / "fagq_py.cpp"), "-o", str(pyext_path().with_suffix(".so.tmp")),
+            *[f"-L{p}" for p in cpp_extension.library_paths()],
+            "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python"]
+
+
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compiles every HIP unit for gfx950 and links libfagq.so; returns its path."""
+    """Compiles every HIP unit for gfx950 and links libfagq.so (and the CPython
+    binding of the operator's per-call path); returns the library's path."""
     OBJ_DIR.mkdir(exist_ok=True)
     cc = hipcc()
     flags = device_flags()
@@ -80,12 +102,14 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     units.append((CSRC / "fagq_gemm.hip", OBJ_DIR / "fagq_gemm.o", []))
     units.append((CSRC / "dsa_topk.hip", OBJ_DIR / "dsa_topk.o", []))
     units.append((CSRC / "mla_bwd.hip", OBJ_DIR / "mla_bwd.o", []))
-    jobs = jobs or min(len(units), max(1, min(16, os.cpu_count() or 1)))
+    jobs = jobs or min(len(units) + 1, max(1, min(16, os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         futs = [ex.submit(_run, [cc, *flags, *defs, "-c", str(src), "-o", str(obj)], verbose)
                 for src, obj, defs in units]
+        futs.append(ex.submit(_run, pyext_command(), verbose))
         for f in futs:
             f.result()
+    os.replace(pyext_path().with_suffix(".so.tmp"), pyext_path())
     tmp = LIB_PATH.with_suffix(".so.tmp")
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
           *[str(o) for _, o, _ in units]], verbose)

@@ -86,12 +86,14 @@ def _ptr(t: torch.Tensor | None):
 
 
 # Per-call host work is what bounds decode-sized calls (the kernel takes about
-# 3 us, the HIP launch about 3.3 us of host time), so the hot path reads the
-# current device and stream through torch's raw accessors (no torch.device /
-# Stream objects), enters a device guard only when the tensors are not on the
-# current device, and checks every tensor inline in one pass (no helper calls
-# on the success path), falling back to the detailed checks only to word an
-# error.
+# 3 us, the HIP launch about 3.3 us of host time).  The hot path hands the
+# tensors to the CPython binding (csrc/fagq_py.cpp), which checks them on their
+# C++ metadata and calls fagq_launch; the current device and stream come from
+# torch's raw accessors (no torch.device / Stream objects).  Without the
+# binding, or when the tensors are not on the current device, the Python path
+# below checks every tensor inline in one pass and calls fagq_launch through
+# ctypes (entering a device guard only when needed), falling back to the
+# detailed checks only to word an error.
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 _raw_device = getattr(torch._C, "_cuda_getDevice", None)
 _INT8 = torch.int8
@@ -99,6 +101,7 @@ _F32 = torch.float32
 _U8 = torch.uint8
 _Q_CODE = {_FP8: _lib.Q_FP8_E4M3FN, _INT8: _lib.Q_INT8}
 _S_CODE = {_F32: _lib.SCALE_F32, _U8: _lib.SCALE_UE8M0}
+_ROUNDING_CODE = {None: -1, "rne": 0, "trunc": 1}   # the binding's rounding argument
 
 
 def _current_stream(dev: int) -> int:
@@ -165,6 +168,19 @@ def fused_add_rmsnorm_group_quant(
     the module docstring for how the formats are chosen.  Returns
     ``(residual_out, norm_out, x_q, x_scale)``.
     """
+    fast = _lib._fast if _lib._fast_tried else _lib.fast_launch()
+    if fast is not None and _raw_device is not None and _raw_stream is not None \
+            and type(eps) is float:
+        dev = x.get_device()
+        if dev >= 0 and _raw_device() == dev:
+            st = fast(x, residual, gamma, residual_out, norm_out, x_q, x_scale, eps, group_size,
+                      _ROUNDING_CODE.get(rounding, -2) if isinstance(rounding, (str, type(None)))
+                      else -2, _raw_stream(dev))
+            if st == 0:
+                return residual_out, norm_out, x_q, x_scale
+            if st != _lib.FAST_ARG_ERROR:
+                _lib.check(st)
+            # A rejected argument: the checks below raise the detailed error.
     if x.dim() != 2:
         raise ValueError(f"x must be 2-D [M, D], got shape {tuple(x.shape)}")
     dev = x.get_device()

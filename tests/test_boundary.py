@@ -199,6 +199,29 @@ def test_cpu_tensors_are_rejected(pkg):
         pkg.fused_add_rmsnorm_group_quant(**cpu_args())
 
 
+def test_cpython_binding_is_built_and_bound(pkg):
+    # The per-call binding (csrc/fagq_py.cpp) loads, is bound to this process's
+    # libfagq.so, and hands every argument it does not accept back to the
+    # Python checks (status ARG_ERROR) instead of raising or launching.
+    from fagq_mi355x import _fagq_py, _lib
+    fast = _lib.fast_launch()
+    assert fast is _fagq_py.launch and _fagq_py.ARG_ERROR == _lib.FAST_ARG_ERROR
+    a = cpu_args()
+    args = [a["x"], a["residual"], a["gamma"], a["residual_out"], None, a["x_q"], a["x_scale"],
+            1e-6, 128, -1, 0]
+    assert fast(*args) == _lib.FAST_ARG_ERROR          # CPU tensors
+    bad = list(args)
+    bad[8] = 128.0                                     # a float group size
+    assert fast(*bad) == _lib.FAST_ARG_ERROR
+    bad = list(args)
+    bad[0] = [0.0] * 4                                 # not a tensor
+    assert fast(*bad) == _lib.FAST_ARG_ERROR
+    with pytest.raises(TypeError):
+        fast(*args[:10])
+    with pytest.raises(ValueError):
+        _fagq_py.bind(0)
+
+
 def test_format_inference(pkg):
     from fagq_mi355x import _lib, ops
     assert ops._q_format(torch.empty(1, dtype=torch.int8)) == _lib.Q_INT8

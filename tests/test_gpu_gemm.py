@@ -190,3 +190,44 @@ def test_gemm_python_errors(pkg, gpu):
     out = pkg.fp8_block_scaled_gemm(a, s, b, bs)
     torch.cuda.synchronize()
     assert out.shape == (4, 128) and out.dtype == torch.bfloat16 and not out.float().any()
+
+
+@pytest.mark.parametrize("col", [True, False])
+def test_gemm_copy_offsets_past_2_31(pkg, gpu, col):
+    """K = 8,454,144: the operand copies of a 256-row tile start up to 255 K bytes
+    (about 2.16e9, past 2^31) into the tile's buffer, so the uint32 offset
+    arithmetic (and its range check) is exercised where signed 32-bit offsets
+    would overflow.  Only five 128-column blocks are non-zero (the first two, the
+    middle one and the last two, in every row, including rows 248..255 whose
+    offsets are all past 2^31); every other block multiplies exact zeros, which
+    leave an fp32 accumulator unchanged, so the product equals the oracle's on
+    the five blocks alone, with the tolerance of that K."""
+    M = N = 256
+    kb_total = 66048
+    K = kb_total * 128
+    assert 255 * K > 2 ** 31 and 256 * K < 2 ** 32
+    blocks = [0, 1, kb_total // 2, kb_total - 2, kb_total - 1]
+    note(f"gemm K={K} (offsets past 2^31) col={col}")
+    g = torch.Generator().manual_seed(77)
+    a_small, a_s_small, b_small, b_s_small = make(M, N, 128 * len(blocks), "f32", "f32", col, seed=77)
+    a_q = torch.zeros((M, K), dtype=torch.uint8, device=gpu)
+    b_q = torch.zeros((N, K), dtype=torch.uint8, device=gpu)
+    for i, kb in enumerate(blocks):
+        a_q[:, kb * 128:(kb + 1) * 128] = a_small[:, i * 128:(i + 1) * 128].view(torch.uint8).to(gpu)
+        b_q[:, kb * 128:(kb + 1) * 128] = b_small[:, i * 128:(i + 1) * 128].view(torch.uint8).to(gpu)
+    # Scales everywhere (the zero blocks' scales are finite, so they contribute 0).
+    a_s_full = torch.exp(torch.empty((kb_total, M) if col else (M, kb_total)).uniform_(-4, 2, generator=g))
+    b_s_full = torch.exp(torch.empty(N // 128, kb_total).uniform_(-4, 2, generator=g))
+    sel = torch.tensor(blocks)
+    if col:
+        a_s_full[sel, :] = a_s_small
+    else:
+        a_s_full[:, sel] = a_s_small
+    b_s_full[:, sel] = b_s_small
+    a_scale = a_s_full.to(gpu).t() if col else a_s_full.to(gpu)
+    c = pkg.fp8_block_scaled_gemm(a_q.view(FP8), a_scale, b_q.view(FP8), b_s_full.to(gpu))
+    torch.cuda.synchronize()
+    got = c.float().cpu().numpy()
+    del a_q, b_q
+    ref, bound = run_ref(a_small, a_s_small, b_small, b_s_small, col)
+    assert_close(got, ref, bound, 128 * len(blocks), f"K={K} col={col}")

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from oracle.compare import compare
-from tests.gpu_util import note, run_gpu, run_ref
+from tests.gpu_util import FMTS, note, run_gpu, run_ref
 
 pytestmark = pytest.mark.gpu
 
@@ -259,3 +259,35 @@ def test_python_layer_rejects_bad_gpu_arguments(pkg, gpu):
     with pytest.raises(_lib.FagqError) as e:
         f(x, x, g, torch.empty_like(x), None, q, sc, -1.0, 128)
     assert e.value.status == 6
+
+
+@pytest.mark.parametrize("M,D,fmt,ue8m0,col,with_norm", [
+    (1, 8192, "int8_rne", False, False, False), (33, 4096, "int8_trunc", True, True, True),
+    (512, 7168, "fp8", False, True, False), (300, 5120, "fp8", True, False, True)])
+def test_cpython_binding_matches_ctypes_path(pkg, gpu, M, D, fmt, ue8m0, col, with_norm):
+    """The operator's per-call CPython binding and the ctypes path launch the same
+    kernel: bit-identical outputs, and the binding is the one the operator uses."""
+    from fagq_mi355x import _lib, ops
+    assert _lib.fast_launch() is not None
+    note(f"binding vs ctypes M={M} D={D} {fmt} ue8m0={ue8m0} col={col} norm={with_norm}")
+    x, r, w = inputs(M, D, seed=M + D)
+    qdt, rounding = FMTS[fmt][0], FMTS[fmt][1]
+    xd, rd, wd = x.to(gpu), r.to(gpu), w.to(gpu)
+    outs = []
+    for use_fast in (True, False):
+        ro = torch.empty_like(rd)
+        no = torch.empty_like(rd) if with_norm else None
+        q = torch.empty(M, D, dtype=qdt, device=gpu)
+        sc = pkg.empty_scales(M, D // 128, ue8m0=ue8m0, col_major=col, device=gpu)
+        saved = (_lib._fast, _lib._fast_tried)
+        if not use_fast:
+            _lib._fast, _lib._fast_tried = None, True
+        try:
+            ops.fused_add_rmsnorm_group_quant(xd, rd, wd, ro, no, q, sc, 1e-6, 128,
+                                              rounding=rounding if qdt == torch.int8 else None)
+        finally:
+            _lib._fast, _lib._fast_tried = saved
+        torch.cuda.synchronize(gpu)
+        outs.append([t.cpu().view(torch.uint8) for t in (ro, q, sc.contiguous()) + ((no,) if with_norm else ())])
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
