@@ -181,9 +181,11 @@ def parse_args():
 
 def copy_bench(args, torch, pkg) -> int:
     """Times the library's HBM ceiling probes (fagq_diag_stream) over BYTES, with the
-    operator's cache policies: copy (BYTES read + BYTES written), read-only and
-    write-only, buffer sets rotated past the MALL, one event pair around the K
-    launches of each.  One JSON line per probe."""
+    operator's cache policies: copy (BYTES read + BYTES written), read-only,
+    write-only, and the operator's byte mix without its arithmetic (two input
+    streams of BYTES/2 read, residual_out and one-byte codes written: 3.5 x BYTES/2
+    moved), buffer sets rotated past the MALL, one event pair around the K launches
+    of each.  One JSON line per probe."""
     import ctypes
     from fagq_mi355x import _lib
     dev = torch.device("cuda:0")
@@ -194,18 +196,23 @@ def copy_bench(args, torch, pkg) -> int:
              torch.empty(n, dtype=torch.uint8, device=dev)) for _ in range(nsets)]
     stream = torch.cuda.current_stream(dev)
     sp = ctypes.c_void_p(stream.cuda_stream)
-    for mode, name, moved in ((_lib.STREAM_COPY, "copy", 2 * n), (_lib.STREAM_READ, "read", n),
-                              (_lib.STREAM_WRITE, "write", n)):
-        def step(i, mode=mode):
+    # opmix: the operator's byte mix (x, residual in; residual_out, one-byte codes out)
+    # over n/2 bytes per input stream, carved from the same buffers.
+    nop = n // 2 // 32 * 32
+    for mode, name, moved, nb in ((_lib.STREAM_COPY, "copy", 2 * n, n),
+                                  (_lib.STREAM_READ, "read", n, n),
+                                  (_lib.STREAM_WRITE, "write", n, n),
+                                  (_lib.STREAM_OPMIX, "opmix", 7 * nop // 2, nop)):
+        def step(i, mode=mode, nb=nb):
             s, d = bufs[i % nsets]
             pkg._lib.check(lib.fagq_diag_stream(ctypes.c_void_p(s.data_ptr()),
-                                                ctypes.c_void_p(d.data_ptr()), n, mode, sp),
+                                                ctypes.c_void_p(d.data_ptr()), nb, mode, sp),
                            "fagq_diag_stream")
 
         for i in range(args.warmup):
             step(i)
         ms, _ = timed_region(torch, dev, stream, step, args.steps)
-        print(json.dumps({"probe": name, "bytes_per_launch": moved, "buffer_bytes": n,
+        print(json.dumps({"probe": name, "bytes_per_launch": moved, "buffer_bytes": nb,
                           "us_per_call": round(ms * 1e3, 2),
                           "GBps": round(moved / (ms * 1e-3) / 1e9, 1),
                           "frac_of_8000": round(moved / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),

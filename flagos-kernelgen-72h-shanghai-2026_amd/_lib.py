@@ -25,7 +25,7 @@ ROUND_RNE, ROUND_TRUNC = 0, 1
 MAX_D = 32768
 MAX_PARTS, MAX_D_PARTS = 8, 16384
 MODE_INDEPENDENT, MODE_SHARED_GAMMA, MODE_WIDE_SCALES = 0, 1, 2
-STREAM_COPY, STREAM_READ, STREAM_WRITE = 0, 1, 2
+STREAM_COPY, STREAM_READ, STREAM_WRITE, STREAM_OPMIX = 0, 1, 2, 3
 
 STATUS_NAMES = {
     0: "FAGQ_OK", 1: "FAGQ_E_NULL", 2: "FAGQ_E_SHAPE", 3: "FAGQ_E_GROUP", 4: "FAGQ_E_ALIGN",

@@ -62,6 +62,26 @@ __global__ void __launch_bounds__(kStreamBlock) fagq_stream_write(const uint8_t*
                                          kStoreAux);
 }
 
+// The operator's byte mix without its arithmetic: every thread reads 16
+// bytes of x and of residual (8 bf16 each) and writes 16 bytes of
+// residual_out and 8 bytes of codes.  x, residual = src, src + bytes;
+// residual_out, codes = dst, dst + bytes.
+__global__ void __launch_bounds__(kStreamBlock) fagq_stream_opmix(const uint8_t* src, uint8_t* dst,
+                                                                  int64_t bytes) {
+  const int64_t base = (int64_t)blockIdx.x * kStreamBlock * 16;
+  const uint32_t n = chunk_bytes(bytes);
+  const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(src + base, n), threadIdx.x * 16,
+                                                        0, kNonTemporal);
+  const u32x4 r = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(src + bytes + base, n),
+                                                        threadIdx.x * 16, 0, kNonTemporal);
+  const u32x4 s = x ^ r;
+  __builtin_amdgcn_raw_buffer_store_b128(s, make_rsrc(dst + base, n), threadIdx.x * 16, 0,
+                                         kStoreAux);
+  __builtin_amdgcn_raw_buffer_store_b64(u32x2{s[0] ^ s[1], s[2] ^ s[3]},
+                                        make_rsrc(dst + bytes + base / 2, n / 2), threadIdx.x * 8,
+                                        0, kStoreAux);
+}
+
 constexpr int kVersion = 1 * 10000 + 0 * 100 + 0;
 constexpr int kMaxDevices = 64;
 
@@ -156,6 +176,12 @@ bool finish_mapping(int64_t M, int D, int wpr, int rpb, int mode, int lds, Mappi
 //   (RG_SHARED_GAMMA): D = 8192: 149.3 against 150.5 us.
 // * 5..8 steps: 1-step waves: D = 4096: 21.3 against 21.6 us at M = 4096,
 //   74.7 against 75.5 at M = 16384; D = 3072: 57.5 against 59.0.
+// * 9..11 steps: 2-step waves, one row per workgroup, at most four
+//   workgroups per CU (36 KB of LDS reserved each): D = 5120, M = 16384:
+//   94.4 against 95.8 us (ue8m0 column-major), 94.8 against 96.2 (fp32
+//   column-major), 93.4 against 94.7 (fp32 row-major); M = 8192 ue8m0:
+//   49.2 against 49.8; D = 4608: 85.4 against 86.7; D = 5632: 104.8 against
+//   105.7.  Three per CU was slower than either (D = 4608: 88.2).
 // * other prefill: 2 steps per wave, one row per workgroup.
 // * decode: 1 step per wave, one row per workgroup, as many waves as the row
 //   has steps (<= 16).
@@ -178,7 +204,10 @@ void choose_mapping(int64_t M, int D, int scale_format, int scale_layout, Mappin
   if (ns > steps) ns = steps;
   const int wpr = ceil_div(steps, ns);
   const int rpb = wpr >= 4 ? 1 : 4 / wpr;
-  finish_mapping(M, D, wpr, rpb, RG_INDEPENDENT, 0, m);
+  // 36 KB per workgroup: four fit in the CU's 160 KB of LDS with the static
+  // arrays, five do not.
+  const int lds = prefill && ns == 2 && rpb == 1 && steps >= 9 && steps <= 11 ? 36 * 1024 : 0;
+  finish_mapping(M, D, wpr, rpb, RG_INDEPENDENT, lds, m);
 }
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
@@ -491,9 +520,9 @@ FAGQ_API int fagq_diag_encode(const float* in, void* out, int64_t n, int q_forma
 
 FAGQ_API int fagq_diag_stream(const void* src, void* dst, int64_t bytes, int mode,
                               void* stream) {
-  if (mode < FAGQ_STREAM_COPY || mode > FAGQ_STREAM_WRITE) return FAGQ_E_FORMAT;
+  if (mode < FAGQ_STREAM_COPY || mode > FAGQ_STREAM_OPMIX) return FAGQ_E_FORMAT;
   if ((mode != FAGQ_STREAM_WRITE && !src) || !dst) return FAGQ_E_NULL;
-  if (bytes < 0 || bytes % 16 != 0) return FAGQ_E_SHAPE;
+  if (bytes < 0 || bytes % (mode == FAGQ_STREAM_OPMIX ? 32 : 16) != 0) return FAGQ_E_SHAPE;
   if ((src && !aligned(src, 16)) || !aligned(dst, 16)) return FAGQ_E_ALIGN;
   if (bytes == 0) return FAGQ_OK;
   const int64_t blocks = (bytes + kStreamBlock * 16 - 1) / (kStreamBlock * 16);
@@ -504,9 +533,10 @@ FAGQ_API int fagq_diag_stream(const void* src, void* dst, int64_t bytes, int mod
   uint8_t* d8 = static_cast<uint8_t*>(dst);
   int64_t n = bytes;
   void* args[] = {&s8, &d8, &n};
-  const void* k = mode == FAGQ_STREAM_COPY ? reinterpret_cast<const void*>(&fagq_stream_copy)
-                  : mode == FAGQ_STREAM_READ ? reinterpret_cast<const void*>(&fagq_stream_read)
-                                             : reinterpret_cast<const void*>(&fagq_stream_write);
+  const void* k = mode == FAGQ_STREAM_COPY    ? reinterpret_cast<const void*>(&fagq_stream_copy)
+                  : mode == FAGQ_STREAM_READ  ? reinterpret_cast<const void*>(&fagq_stream_read)
+                  : mode == FAGQ_STREAM_WRITE ? reinterpret_cast<const void*>(&fagq_stream_write)
+                                              : reinterpret_cast<const void*>(&fagq_stream_opmix);
   return launch_status(hipLaunchKernel(k, dim3((unsigned)blocks), dim3(kStreamBlock), args, 0,
                                        static_cast<hipStream_t>(stream)));
 }

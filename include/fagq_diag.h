@@ -63,8 +63,18 @@ FAGQ_API int fagq_diag_encode(const float* in, void* out, int64_t n, int q_forma
  *   FAGQ_STREAM_COPY   reads src, writes dst (bytes each)
  *   FAGQ_STREAM_READ   reads src; dst (>= 16 bytes) is written only if a
  *                      chunk's four words XOR to 0x9e3779b9
- *   FAGQ_STREAM_WRITE  writes dst; src may be NULL */
-enum fagq_stream_mode { FAGQ_STREAM_COPY = 0, FAGQ_STREAM_READ = 1, FAGQ_STREAM_WRITE = 2 };
+ *   FAGQ_STREAM_WRITE  writes dst; src may be NULL
+ *   FAGQ_STREAM_OPMIX  the operator's byte mix without its arithmetic: reads
+ *                      src[0, bytes) and src[bytes, 2 bytes) (x and residual),
+ *                      writes dst[0, bytes) and dst[bytes, 1.5 bytes)
+ *                      (residual_out and one-byte codes); src holds 2 bytes,
+ *                      dst 1.5 bytes, bytes a multiple of 32 */
+enum fagq_stream_mode {
+  FAGQ_STREAM_COPY = 0,
+  FAGQ_STREAM_READ = 1,
+  FAGQ_STREAM_WRITE = 2,
+  FAGQ_STREAM_OPMIX = 3
+};
 
 FAGQ_API int fagq_diag_stream(const void* src, void* dst, int64_t bytes, int mode, void* stream);
 

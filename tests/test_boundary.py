@@ -58,7 +58,7 @@ def test_route_invariants(pkg, M, D, ue8m0, col):
     assert wpr * ns >= steps > (wpr - 1) * ns          # every wave owns >= 1 column
     assert r["block_threads"] == 64 * wpr * rpb <= 1024
     assert r["grid_blocks"] * rpb >= M > (r["grid_blocks"] - 1) * rpb
-    assert r["lds_bytes"] in (0, 49152)
+    assert r["lds_bytes"] in (0, 36864, 49152)
     if mode:
         assert wpr * ns <= 16                            # gamma fits the LDS buffer
     if mode == 2:
@@ -78,7 +78,9 @@ def test_route_invariants(pkg, M, D, ue8m0, col):
         assert (wpr, ns, mode) == (steps, 1, 0)          # 1-step waves
     elif prefill and 2 <= steps <= 16:
         assert (ns, mode) == (2, 0)                      # prefill: 2-step waves
-    if not (prefill and 12 <= steps <= 14 and not col):
+    if prefill and 9 <= steps <= 11:
+        assert (ns, rpb, r["lds_bytes"]) == (2, 1, 36864)   # at most 4 workgroups per CU
+    elif not (prefill and 12 <= steps <= 14 and not col):
         assert r["lds_bytes"] == 0
     if M <= 32 and D <= 8192:
         assert (wpr, ns, mode) == (steps, 1, 0)          # decode: one step per wave
@@ -173,7 +175,8 @@ def test_diag_validation(lib):
     assert lib.fagq_diag_copy(fake(0), fake(1), 15, None) == 2
     assert lib.fagq_diag_copy(None, fake(1), 16, None) == 1
     assert lib.fagq_diag_copy(fake(0), fake(1), 0, None) == 0
-    assert lib.fagq_diag_stream(fake(0), fake(1), 16, 3, None) == 5
+    assert lib.fagq_diag_stream(fake(0), fake(1), 16, 4, None) == 5
+    assert lib.fagq_diag_stream(fake(0), fake(1), 16, 3, None) == 2   # opmix: bytes % 32
     assert lib.fagq_diag_stream(None, fake(1), 16, 1, None) == 1     # read needs src
     assert lib.fagq_diag_stream(fake(0), None, 16, 2, None) == 1
     assert lib.fagq_diag_stream(None, fake(1), 0, 2, None) == 0      # write: src may be NULL
