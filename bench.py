@@ -221,36 +221,38 @@ def copy_bench(args, torch, pkg) -> int:
 
 
 def mfma_peak_bench(args, torch, pkg) -> int:
-    """Times fagq_diag_mfma_peak: 2048 workgroups of 4 waves, each wave issuing
-    1000 x 8 v_mfma_scale_f32_16x16x128_f8f6f4 on register operands."""
+    """Times fagq_diag_mfma_rate for both fp8 instruction shapes: 2048 workgroups of
+    4 waves, each wave issuing 1000 x 8 v_mfma_scale_f32_16x16x128_f8f6f4 (8
+    accumulators) or 1000 x 4 v_mfma_scale_f32_32x32x64_f8f6f4 (4 accumulators) on
+    register operands, the same flops per launch.  One JSON line per shape."""
     import ctypes
     dev = torch.device("cuda:0")
     lib = pkg.load_library()
     blocks, iters = 2048, 1000
-    flops = blocks * 4 * iters * 8 * 65536
     out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream(dev)
     sp = ctypes.c_void_p(stream.cuda_stream)
+    for shape, name, flops in ((0, "v_mfma_scale_f32_16x16x128_f8f6f4", blocks * 4 * iters * 8 * 65536),
+                               (1, "v_mfma_scale_f32_32x32x64_f8f6f4", blocks * 4 * iters * 4 * 131072)):
+        def step(shape=shape):
+            pkg._lib.check(lib.fagq_diag_mfma_rate(ctypes.c_void_p(out.data_ptr()), blocks, iters,
+                                                   shape, sp), "fagq_diag_mfma_rate")
 
-    def step():
-        pkg._lib.check(lib.fagq_diag_mfma_peak(ctypes.c_void_p(out.data_ptr()), blocks, iters, sp),
-                       "fagq_diag_mfma_peak")
-
-    for _ in range(args.warmup):
-        step()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize(dev)
-    e0.record(stream)
-    for _ in range(args.steps):
-        step()
-    e1.record(stream)
-    torch.cuda.synchronize(dev)
-    ms = e0.elapsed_time(e1) / args.steps
-    tflops = flops / (ms * 1e-3) / 1e12
-    print(json.dumps({"instruction": "v_mfma_scale_f32_16x16x128_f8f6f4", "flops_per_call": flops,
-                      "us_per_call": round(ms * 1e3, 2), "TFLOPs": round(tflops, 1),
-                      "frac_of_5000_TFLOPs": round(tflops / 5000.0, 4),
-                      "steps": args.steps, "warmup": args.warmup}), flush=True)
+        for _ in range(args.warmup):
+            step()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize(dev)
+        e0.record(stream)
+        for _ in range(args.steps):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        ms = e0.elapsed_time(e1) / args.steps
+        tflops = flops / (ms * 1e-3) / 1e12
+        print(json.dumps({"instruction": name, "flops_per_call": flops,
+                          "us_per_call": round(ms * 1e3, 2), "TFLOPs": round(tflops, 1),
+                          "frac_of_5000_TFLOPs": round(tflops / 5000.0, 4),
+                          "steps": args.steps, "warmup": args.warmup}), flush=True)
     return 0
 
 

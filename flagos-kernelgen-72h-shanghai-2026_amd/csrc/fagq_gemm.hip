@@ -437,6 +437,33 @@ __global__ void __launch_bounds__(kPeakThreads) mfma_peak_kernel(float* out, int
   out[(int64_t)blockIdx.x * kPeakThreads + t] = r;
 }
 
+// The 32 x 32 x 64 shape: every wave keeps 4 independent 32 x 32
+// accumulators (16 floats per lane each) and issues iters x 4 instructions,
+// each twice the flops of one 16 x 16 x 128.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+constexpr int kPeakChain32 = 4;
+__global__ void __launch_bounds__(kPeakThreads) mfma_peak32_kernel(float* out, int iters) {
+  const int t = threadIdx.x;
+  i32x8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = 0x38383838 ^ (t * 7 + i);
+    b[i] = 0x30303030 ^ (t * 3 + i);
+  }
+  f32x16 c[kPeakChain32] = {};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int j = 0; j < kPeakChain32; ++j)
+      c[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c[j], 0, 0, 0, 120, 0, 130);
+  }
+  float r = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kPeakChain32; ++j)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) r += c[j][i];
+  out[(int64_t)blockIdx.x * kPeakThreads + t] = r;
+}
+
 }  // namespace
 }  // namespace gemm
 }  // namespace fagq
@@ -476,7 +503,13 @@ FAGQ_API int fagq_gemm_query_route(int64_t M, int64_t N, int64_t K, fagq_gemm_ro
 }
 
 FAGQ_API int fagq_diag_mfma_peak(float* out, int64_t blocks, int32_t iters, void* stream) {
+  return fagq_diag_mfma_rate(out, blocks, iters, 0, stream);
+}
+
+FAGQ_API int fagq_diag_mfma_rate(float* out, int64_t blocks, int32_t iters, int shape,
+                                 void* stream) {
   if (!out) return FAGQ_E_NULL;
+  if (shape != 0 && shape != 1) return FAGQ_E_FORMAT;
   if (blocks < 1 || iters < 1) return FAGQ_E_SHAPE;
   if (blocks > (1 << 20) || iters > (1 << 20)) return FAGQ_E_TOO_LARGE;
   if (!aligned(out, 4)) return FAGQ_E_ALIGN;
@@ -484,8 +517,9 @@ FAGQ_API int fagq_diag_mfma_peak(float* out, int64_t blocks, int32_t iters, void
   if (dc != FAGQ_OK) return dc;
   int it = iters;
   void* args[] = {&out, &it};
-  const hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&mfma_peak_kernel),
-                                       dim3((unsigned)blocks), dim3(kPeakThreads), args, 0,
+  const void* k = shape == 0 ? reinterpret_cast<const void*>(&mfma_peak_kernel)
+                             : reinterpret_cast<const void*>(&mfma_peak32_kernel);
+  const hipError_t e = hipLaunchKernel(k, dim3((unsigned)blocks), dim3(kPeakThreads), args, 0,
                                        static_cast<hipStream_t>(stream));
   return launch_status(e);
 }

@@ -102,6 +102,13 @@ FAGQ_API int fagq_diag_scale_offsets(int64_t M, int64_t D, int64_t group_size, i
  * rate is compared with. */
 FAGQ_API int fagq_diag_mfma_peak(float* out, int64_t blocks, int32_t iters, void* stream);
 
+/* The same probe for either fp8 matrix-instruction shape: shape 0 is
+ * fagq_diag_mfma_peak; shape 1 issues iters x 4
+ * v_mfma_scale_f32_32x32x64_f8f6f4 per wave (4 independent 32 x 32
+ * accumulators), blocks x 4 x iters x 4 x 131072 flops per launch. */
+FAGQ_API int fagq_diag_mfma_rate(float* out, int64_t blocks, int32_t iters, int shape,
+                                 void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -184,6 +184,8 @@ def test_diag_validation(lib):
     assert lib.fagq_diag_mfma_peak(None, 1, 1, None) == 1
     assert lib.fagq_diag_mfma_peak(fake(0), 0, 1, None) == 2
     assert lib.fagq_diag_mfma_peak(fake(0), 1, 0, None) == 2
+    assert lib.fagq_diag_mfma_rate(fake(0), 1, 1, 2, None) == 5
+    assert lib.fagq_diag_mfma_rate(None, 1, 1, 1, None) == 1
     assert lib.fagq_diag_mfma_peak(fake(0), (1 << 20) + 1, 1, None) == 7
     assert lib.fagq_diag_mfma_peak(ctypes.c_void_p(BASE + 2), 1, 1, None) == 4
 
