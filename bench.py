@@ -948,10 +948,36 @@ def gemm_bench(args, torch, pkg, w) -> int:
                      "traffic": traffic},
         "cpu_baseline": None,
     }
+    out["vendor_hipblaslt"] = gemm_vendor_reference(args, torch, dev, stream, sets, nsets, w)
     if args.cpu_seconds > 0:
         out["cpu_baseline"] = gemm_cpu_baseline(w, a_q, a_s, b_q, b_s, sets[0][4], args, torch)
     print(json.dumps(out), flush=True)
     return 0
+
+
+def gemm_vendor_reference(args, torch, dev, stream, sets, nsets, w) -> dict:
+    """The vendor library on the same fp8 operands, steps and buffer rotation, for
+    comparison only: torch._scaled_mm (hipBLASLt) with one scale per tensor and with
+    row-wise scales (neither has 1 x 128 / 128 x 128 block scales).  Returns us/call
+    and TFLOP/s per scaling mode, or the error text when the call is unavailable."""
+    res = {"call": "torch._scaled_mm(a [M, K], b.t() [K, N], out_dtype=bf16)"}
+    ones_t = torch.ones((), device=dev)
+    row_a = torch.ones(w.M, 1, device=dev)
+    row_b = torch.ones(1, w.N, device=dev)
+    for mode, sa, sb in (("per_tensor", ones_t, ones_t), ("row_wise", row_a, row_b)):
+        def step(i: int, sa=sa, sb=sb):
+            a, _, b, _, _ = sets[i % nsets]
+            torch._scaled_mm(a, b.t(), scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)
+        try:
+            for i in range(args.warmup):
+                step(i)
+            ms, _ = timed_region(torch, dev, stream, step, args.steps)
+        except Exception as e:  # the op or the scaling mode missing from this torch build
+            res[mode] = {"error": str(e)[:200]}
+            continue
+        res[mode] = {"us_per_call": round(ms * 1e3, 2),
+                     "TFLOPs": round(w.flops() / (ms * 1e-3) / 1e12, 1)}
+    return res
 
 
 def gemm_cpu_baseline(w, a_q, a_s, b_q, b_s, c_gpu, args, torch) -> dict:
