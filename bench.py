@@ -39,7 +39,9 @@ on a row sample.
 --copy BYTES and --mfma-peak time the library's ceiling probes instead: HBM
 copy, read-only and write-only streams with the operator's cache policies
 (achievable bandwidth, counter calibration), and the GEMM's matrix instruction
-issued from registers (achievable MFMA rate).
+issued from registers (achievable MFMA rate).  --lds-probe times the LDS read
+patterns of fagq_diag_lds_read (run it under rocprofv3 --pmc for the bank
+conflicts of each).
 
 Usage: python bench.py [--steps K] [--warmup W] [--config NAME] [--gpus 1]
 """
@@ -170,6 +172,8 @@ def parse_args():
     p.add_argument("--mfma-peak", action="store_true",
                    help="instead: time the library's register-only issue-rate probe of the fp8 "
                         "GEMM's matrix instruction (the compute ceiling its rate is compared with)")
+    p.add_argument("--lds-probe", action="store_true",
+                   help="instead: time the library's LDS read probe for each address pattern")
     p.add_argument("--steady-ms", type=float, default=300.0,
                    help="after the timed region: run the operator this long, then time K more "
                         "steps (us_per_call_steady_state; 0 disables)")
@@ -256,6 +260,43 @@ def mfma_peak_bench(args, torch, pkg) -> int:
     return 0
 
 
+def lds_probe_bench(args, torch, pkg) -> int:
+    """Times fagq_diag_lds_read for each address pattern (1024 workgroups of 4 waves,
+    8 x 256 ds_read_b128 per wave), one launch per pattern and step, in pattern order,
+    so a rocprofv3 counter run sees the patterns as consecutive dispatches.  One JSON
+    line per pattern."""
+    import ctypes
+    dev = torch.device("cuda:0")
+    lib = pkg.load_library()
+    blocks, iters = 1024, 256
+    out = torch.empty(blocks * 256 * 4, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    names = ["lane order", "GEMM fragment, low half", "GEMM fragment, high half",
+             "fragment, chunk c ^ ((r / 2) % 8)", "fragment, chunk c ^ (r % 8)",
+             "fragment, no swizzle"]
+    for pattern, name in enumerate(names):
+        def step(pattern=pattern):
+            pkg._lib.check(lib.fagq_diag_lds_read(ctypes.c_void_p(out.data_ptr()), blocks, iters,
+                                                  pattern, sp), "fagq_diag_lds_read")
+
+        for _ in range(args.warmup):
+            step()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize(dev)
+        e0.record(stream)
+        for _ in range(args.steps):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        ms = e0.elapsed_time(e1) / args.steps
+        print(json.dumps({"probe": "fagq_diag_lds_read", "pattern": pattern, "name": name,
+                          "ds_read_b128_per_call": blocks * 4 * iters * 8,
+                          "us_per_call": round(ms * 1e3, 2),
+                          "steps": args.steps, "warmup": args.warmup}), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -277,6 +318,8 @@ def main() -> int:
         return copy_bench(args, torch, pkg)
     if args.mfma_peak:
         return mfma_peak_bench(args, torch, pkg)
+    if args.lds_probe:
+        return lds_probe_bench(args, torch, pkg)
     name = args.config or HEADLINE
     from fagq_mi355x.workloads import DSA_CONFIGS, GEMM_CONFIGS, MLA_CONFIGS, PARTS_CONFIGS
     if name in DSA_CONFIGS:

@@ -64,6 +64,7 @@ SIGNATURES = {
     "fagq_diag_scale_offsets": ([_I64, _I64, _I64, _I, _I, _I, _I64, _P, _I64], _I),
     "fagq_diag_mfma_peak": ([_P, _I64, _I, _P], _I),
     "fagq_diag_mfma_rate": ([_P, _I64, _I, _I, _P], _I),
+    "fagq_diag_lds_read": ([_P, _I64, _I, _I, _P], _I),
     "fagq_dsa_topk_launch": ([_P, _I, _P, _P, _P, _I, _P, _P] + [_I64] * 6 + [_P], _I),
     "fagq_gemm_launch": ([_P] * 5 + [_I64, _I64, _I64, _I, _I, _I, _P], _I),
     "fagq_gemm_launch_mapped": ([_P] * 5 + [_I64, _I64, _I64, _I, _I, _I, _I, _P], _I),

@@ -19,13 +19,14 @@
 // global memory straight into LDS (buffer_load_dwordx4 ... lds: each
 // instruction writes 1 KB, 16 bytes per lane, in lane order).  LDS holds
 // each 128-byte row with its eight 16-byte chunks XOR-swizzled: logical chunk
-// c of row r sits at position c ^ ((r / 2) % 8), so a lane fetches the
-// logical chunk (lane % 8) ^ ((r / 2) % 8).  A ds_read_b128 is served 16
-// lanes (256 bytes, all 64 banks) at a time, and an MFMA operand read has 16
-// consecutive rows at one logical chunk: rows of equal parity then land in
-// distinct 16-byte slots of the 256-byte bank window (a swizzle by r % 8
-// maps rows r and r + 8 to the same banks, which measured as a 2-way
-// conflict on every read).  Two LDS stages (2 x 64 KB, or 2 x 56 KB at
+// c of row r sits at position c ^ f(r), f(r) = ((r >> 1) & 1) | ((r & 4) ? 4 : 0),
+// so a lane fetches the logical chunk (lane % 8) ^ f(r).  An MFMA operand read
+// is 16 consecutive rows at one logical chunk per 16 lanes.  gfx950 serves a
+// ds_read_b128 in four passes of 16 lanes over the 64 banks (4 cycles when no
+// two lanes of a pass hit one bank at different addresses); the lanes of a
+// pass are not 16 consecutive ones.  fagq_diag_lds_read (include/fagq_diag.h)
+// measures the fragment read with this f at 4 cycles per instruction and with
+// f(r) = (r >> 1) & 7 or r & 7 at 8 (a 2-way conflict on every read).  Two LDS stages (2 x 64 KB, or 2 x 56 KB at
 // BN = 192): the next k-block's copies are issued before the current one is
 // consumed.
 //
@@ -125,14 +126,15 @@ __device__ __forceinline__ void tile_coords(int b, int m_tiles, int n_tiles, int
   nt = w / gm;
 }
 
-// Position of logical 16-byte chunk c of LDS row r.
-__device__ __forceinline__ int swz(int c, int r) { return c ^ ((r >> 1) & 7); }
+// Position of logical 16-byte chunk c of LDS row r (only r % 8 matters).
+__device__ __forceinline__ int swz_of(int r) { return ((r >> 1) & 1) | (r & 4); }
+__device__ __forceinline__ int swz(int c, int r) { return c ^ swz_of(r); }
 
 // One 16 x 128-byte MFMA operand: lane l gets row (r0 + l % 16), k bytes
 // 32 (l / 16) .. +32, from a swizzled LDS tile.
 __device__ __forceinline__ i32x8 lds_frag(const uint8_t* tile, int row, int lane) {
   const int c0 = (lane >> 4) * 2;
-  const int sw = (row >> 1) & 7;
+  const int sw = swz_of(row);
   const uint8_t* r = tile + row * kBK;
   const i32x4 lo = *reinterpret_cast<const i32x4*>(r + ((c0 ^ sw) << 4));
   const i32x4 hi = *reinterpret_cast<const i32x4*>(r + (((c0 + 1) ^ sw) << 4));
@@ -167,16 +169,14 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g)
   // COPY + u of an operand tile (COPY_A for the activation tile, COPY_B for
   // the weight tile) and fills LDS rows 8 i .. +8; the lane's row within them
   // is lane / 8, its position lane % 8, and it fetches the logical chunk
-  // stored there.  For row 8 i + lane / 8, (row / 2) % 8 = 4 (i % 2) +
-  // lane / 16, so even and odd instructions need one lane offset each.
+  // stored there.  The swizzle of row 8 i + lane / 8 depends on lane / 8
+  // only, so one lane offset serves every instruction.
   // The whole offset goes in the VGPR offset and the scalar offset is zero:
   // the hardware range-checks only the VGPR offset (plus the immediate), so
   // this is what turns rows past M or N into zero reads.  The lane part is
   // kept in one VGPR and the uniform part added per instruction.
   const int crow = lane >> 3;
-  const uint32_t cvoff[2] = {
-      (uint32_t)crow * (uint32_t)g.K + (uint32_t)swz(lane & 7, crow) * 16u,
-      (uint32_t)crow * (uint32_t)g.K + (uint32_t)swz(lane & 7, crow + 8) * 16u};
+  const uint32_t cvoff = (uint32_t)crow * (uint32_t)g.K + (uint32_t)swz(lane & 7, crow) * 16u;
 
   // Uniform part of copy instruction inst's offset for k-block kb.  Offsets
   // are computed in uint32: the launch checks that every one fits.
@@ -192,13 +192,13 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g)
     for (int u = 0; u < kCopies; ++u) {   // the two tiles' copies interleaved
       if (u < L::COPY_A) {
         const int inst = wave * L::COPY_A + u;
-        const uint32_t off = cvoff[inst & 1] + copy_off(inst, kb);
+        const uint32_t off = cvoff + copy_off(inst, kb);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(sa_tile + inst * 1024), 16, off,
                                                  0, 0, 0);
       }
       if (u < L::COPY_B) {
         const int inst = wave * L::COPY_B + u;
-        const uint32_t off = cvoff[inst & 1] + copy_off(inst, kb);
+        const uint32_t off = cvoff + copy_off(inst, kb);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(sb_tile + inst * 1024), 16, off,
                                                  0, 0, 0);
       }
@@ -464,6 +464,55 @@ __global__ void __launch_bounds__(kPeakThreads) mfma_peak32_kernel(float* out, i
   out[(int64_t)blockIdx.x * kPeakThreads + t] = r;
 }
 
+// LDS bank probe.  Every lane of 4 waves reads the 16 bytes at
+// lds_probe_addr(pattern, lane % 64) with ds_read_b128, 8 x iters times, from 16
+// KB of LDS holding word i = i * 0x9E3779B1, then writes the 4 words it read.
+// Patterns 1-5 are one MFMA operand fragment of a 16-row tile of 128-byte
+// rows: lane l reads row l % 16 at logical chunk 2 (l / 16) (pattern 2: the
+// chunk after it).
+constexpr int kLdsProbeThreads = 256;
+constexpr int kLdsProbeWords = 4096;
+__device__ __forceinline__ int lds_probe_addr(int pattern, int lane) {
+  const int r = lane & 15, c = (lane >> 4) * 2 + (pattern == 2 ? 1 : 0);
+  switch (pattern) {
+    case 0: return lane * 16;                                 // 1 KB in lane order
+    case 1:
+    case 2: return r * kBK + (swz(c, r) << 4);                // the GEMM's swizzle
+    case 3: return r * kBK + ((c ^ ((r >> 1) & 7)) << 4);     // chunk c ^ ((r / 2) % 8)
+    case 4: return r * kBK + ((c ^ (r & 7)) << 4);            // chunk c ^ (r % 8)
+    default: return r * kBK + (c << 4);                       // no swizzle
+  }
+}
+
+__global__ void __launch_bounds__(kLdsProbeThreads) lds_probe_kernel(int32_t* out, int pattern,
+                                                                     int iters) {
+  __shared__ __attribute__((aligned(1024))) int32_t words[kLdsProbeWords];
+  for (int i = threadIdx.x; i < kLdsProbeWords; i += kLdsProbeThreads)
+    words[i] = (int32_t)((uint32_t)i * 0x9E3779B1u);
+  __syncthreads();
+  const uint32_t a = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int32_t*)words +
+                     (uint32_t)lds_probe_addr(pattern, threadIdx.x & 63);
+  i32x4 v = {0, 0, 0, 0};
+  for (int it = 0; it < iters; ++it) {
+    i32x4 v0, v1, v2, v3, v4, v5, v6, v7;
+    asm volatile(
+        "ds_read_b128 %0, %8\n\t"
+        "ds_read_b128 %1, %8\n\t"
+        "ds_read_b128 %2, %8\n\t"
+        "ds_read_b128 %3, %8\n\t"
+        "ds_read_b128 %4, %8\n\t"
+        "ds_read_b128 %5, %8\n\t"
+        "ds_read_b128 %6, %8\n\t"
+        "ds_read_b128 %7, %8\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=v"(v0), "=v"(v1), "=v"(v2), "=v"(v3), "=v"(v4), "=v"(v5), "=v"(v6), "=v"(v7)
+        : "v"(a));
+    v = v0 & v1 & v2 & v3 & v4 & v5 & v6 & v7;   // all eight read the same bytes
+  }
+  i32x4* o = reinterpret_cast<i32x4*>(out) + (int64_t)blockIdx.x * kLdsProbeThreads + threadIdx.x;
+  *o = v;
+}
+
 }  // namespace
 }  // namespace gemm
 }  // namespace fagq
@@ -504,6 +553,23 @@ FAGQ_API int fagq_gemm_query_route(int64_t M, int64_t N, int64_t K, fagq_gemm_ro
 
 FAGQ_API int fagq_diag_mfma_peak(float* out, int64_t blocks, int32_t iters, void* stream) {
   return fagq_diag_mfma_rate(out, blocks, iters, 0, stream);
+}
+
+FAGQ_API int fagq_diag_lds_read(int32_t* out, int64_t blocks, int32_t iters, int pattern,
+                                void* stream) {
+  if (!out) return FAGQ_E_NULL;
+  if (pattern < 0 || pattern > 5) return FAGQ_E_FORMAT;
+  if (blocks < 1 || iters < 1) return FAGQ_E_SHAPE;
+  if (blocks > (1 << 20) || iters > (1 << 20)) return FAGQ_E_TOO_LARGE;
+  if (!aligned(out, 16)) return FAGQ_E_ALIGN;
+  const int dc = device_check();
+  if (dc != FAGQ_OK) return dc;
+  int pt = pattern, it = iters;
+  void* args[] = {&out, &pt, &it};
+  const hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&lds_probe_kernel),
+                                       dim3((unsigned)blocks), dim3(kLdsProbeThreads), args, 0,
+                                       static_cast<hipStream_t>(stream));
+  return launch_status(e);
 }
 
 FAGQ_API int fagq_diag_mfma_rate(float* out, int64_t blocks, int32_t iters, int shape,

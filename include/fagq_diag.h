@@ -109,6 +109,22 @@ FAGQ_API int fagq_diag_mfma_peak(float* out, int64_t blocks, int32_t iters, void
 FAGQ_API int fagq_diag_mfma_rate(float* out, int64_t blocks, int32_t iters, int shape,
                                  void* stream);
 
+/* LDS bank probe of the GEMM's operand reads: `blocks` workgroups of 4
+ * waves (1 <= blocks <= 2^20); every lane reads 16 bytes with ds_read_b128,
+ * 8 x iters times (1 <= iters <= 2^20), from 16 KB of LDS holding 32-bit
+ * word i = i * 0x9E3779B1 (mod 2^32), at byte address
+ *   pattern 0: 16 (l % 64)                              (1 KB in lane order)
+ *   pattern 1: 128 r + 16 (c ^ f(r)),  f(r) = ((r >> 1) & 1) | (r & 4)
+ *   pattern 2: as 1 with c + 1 for c                    (the GEMM's swizzle)
+ *   pattern 3: 128 r + 16 (c ^ ((r >> 1) & 7))
+ *   pattern 4: 128 r + 16 (c ^ (r & 7))
+ *   pattern 5: 128 r + 16 c                             (no swizzle)
+ * with r = l % 16 and c = 2 ((l % 64) / 16) for thread l, and writes the 4
+ * words it read: `out` holds blocks x 256 x 4 int32 (16-byte aligned).
+ * Bank conflicts show in rocprofv3's SQ_LDS_BANK_CONFLICT per SQ_INSTS_LDS. */
+FAGQ_API int fagq_diag_lds_read(int32_t* out, int64_t blocks, int32_t iters, int pattern,
+                                void* stream);
+
 #ifdef __cplusplus
 }
 #endif

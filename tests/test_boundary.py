@@ -188,6 +188,13 @@ def test_diag_validation(lib):
     assert lib.fagq_diag_mfma_rate(None, 1, 1, 1, None) == 1
     assert lib.fagq_diag_mfma_peak(fake(0), (1 << 20) + 1, 1, None) == 7
     assert lib.fagq_diag_mfma_peak(ctypes.c_void_p(BASE + 2), 1, 1, None) == 4
+    assert lib.fagq_diag_lds_read(None, 1, 1, 0, None) == 1
+    assert lib.fagq_diag_lds_read(fake(0), 1, 1, 6, None) == 5
+    assert lib.fagq_diag_lds_read(fake(0), 1, 1, -1, None) == 5
+    assert lib.fagq_diag_lds_read(fake(0), 0, 1, 0, None) == 2
+    assert lib.fagq_diag_lds_read(fake(0), 1, 0, 0, None) == 2
+    assert lib.fagq_diag_lds_read(fake(0), 1, (1 << 20) + 1, 0, None) == 7
+    assert lib.fagq_diag_lds_read(ctypes.c_void_p(BASE + 8), 1, 1, 0, None) == 4
 
 
 # ----------------------------------------------------------------- Python layer

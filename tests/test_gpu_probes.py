@@ -86,3 +86,44 @@ def test_mfma_rate_probe_shapes(pkg, gpu):
             outs.append(out.cpu().clone())
         assert torch.equal(outs[-1], outs[-2])
         assert (outs[-1] != 0x7fa5a5a5).all()
+
+
+def _lds_probe_addr(pattern: int, lane: int) -> int:
+    """Byte address each lane reads, as include/fagq_diag.h states it."""
+    r, c = lane % 16, 2 * (lane // 16) + (1 if pattern == 2 else 0)
+    f = ((r >> 1) & 1) | (r & 4)
+    return {0: 16 * lane, 1: 128 * r + 16 * (c ^ f), 2: 128 * r + 16 * (c ^ f),
+            3: 128 * r + 16 * (c ^ ((r >> 1) & 7)), 4: 128 * r + 16 * (c ^ (r & 7)),
+            5: 128 * r + 16 * c}[pattern]
+
+
+@pytest.mark.parametrize("pattern", range(6))
+def test_lds_read_probe_addresses(pkg, gpu, pattern):
+    """Every thread returns the four 32-bit words at its documented address."""
+    from fagq_mi355x import _lib
+    lib = _lib.load()
+    note(f"case lds read probe pattern={pattern}")
+    blocks = 3
+    out = torch.full((blocks * 256 * 4,), -1, dtype=torch.int32, device=gpu)
+    st = lib.fagq_diag_lds_read(ctypes.c_void_p(out.data_ptr()), blocks, 2, pattern,
+                                ctypes.c_void_p(torch.cuda.current_stream(gpu).cuda_stream))
+    assert st == 0, st
+    torch.cuda.synchronize(gpu)
+    got = out.cpu().numpy().view(np.uint32).reshape(blocks, 256, 4)
+    words = (np.arange(4096, dtype=np.uint64) * 0x9E3779B1 % (1 << 32)).astype(np.uint32)
+    for t in range(256):
+        w0 = _lds_probe_addr(pattern, t % 64) // 4
+        assert np.array_equal(got[:, t], np.broadcast_to(words[w0:w0 + 4], (blocks, 4))), t
+
+
+def test_lds_read_probe_fragment_patterns_cover_rows():
+    """The fragment patterns read 16 distinct rows at one logical chunk per 16
+    lanes, every 16-byte chunk of each row once over the two halves (1, 2) -
+    the access the GEMM's operand reads make (CPU check of the address map)."""
+    for lanes in (range(0, 16), range(16, 32), range(32, 48), range(48, 64)):
+        rows = {_lds_probe_addr(1, l) // 128 for l in lanes}
+        assert rows == set(range(16))
+    for r in range(16):
+        chunks = sorted((_lds_probe_addr(p, l) % 128) // 16 for p in (1, 2) for l in range(64)
+                        if l % 16 == r)
+        assert chunks == list(range(8))
