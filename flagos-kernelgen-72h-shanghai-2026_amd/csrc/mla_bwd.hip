@@ -35,6 +35,12 @@
 //                        0), written as dc.
 // K2 and K3 issue each thread's loads as one batch: at these sizes they are
 // latency-bound: every dependent round trip to memory adds its full latency.
+//
+// D above kSliceD (512) runs as column slices of at most kSliceD dims: K1, the
+// block totals and K3 are per column, so each slice runs them on its columns
+// (the tensors' row stride stays D, the workspace holds one slice), and the
+// exact rows, whose dot products span all of D, run once over all columns in
+// the first slice's K2, staging the rows in chunks of kSliceD dims.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -51,7 +57,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kE = FAGQ_MLA_EXACT_ROWS;
-constexpr int kMaxD = FAGQ_MLA_MAX_D;
+constexpr int kSliceD = FAGQ_MLA_SLICE_D;   // dims per column slice
 constexpr int kPadElems = 8;             // LDS row padding (bf16 elements), exact rows
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -71,7 +77,11 @@ struct MArgs {
   int32_t nblk;       // ceil(S / brows)
   int32_t hsplit;     // head groups K1 splits the heads into
   int32_t hps;        // heads per group
-  int32_t H, S, D;
+  int32_t H, S;
+  int32_t D;          // dims of this column slice (the width K1, K2's totals and K3 handle)
+  int32_t ld;         // elements between rows of q, c, out, dout, dq and dc (the full D);
+                      // their pointers point at the slice's first column
+  int32_t nexact;     // K2 workgroups (x < nexact) running exact rows: H in the first slice
   int32_t erows;      // min(16, S)
   float scale;
   int32_t dq_bf16;    // dq is bf16 (else fp32)
@@ -116,17 +126,24 @@ __global__ void __launch_bounds__(kThreads) mla_stream_do(const MArgs g) {
   const int b = (int)blockIdx.y;
   const int hbeg = (int)blockIdx.z * g.hps;
   const int hend = hbeg + g.hps < g.H ? hbeg + g.hps : g.H;
-  const uint32_t hsd = (uint32_t)g.H * (uint32_t)g.S * (uint32_t)g.D;    // elements per batch
-  const rsrc_t rdo = make_rsrc(g.dout + (int64_t)b * hsd, hsd * 2u);
+  const uint32_t hsd = (uint32_t)g.H * (uint32_t)g.S * (uint32_t)g.ld;   // elements per batch
+  // The slice's elements of batch b end at (H S - 1) ld + D (the descriptors'
+  // size, so they stay inside the tensors whatever the slice's first column).
+  const uint32_t span = hsd - (uint32_t)g.ld + (uint32_t)g.D;
+  const rsrc_t rdo = make_rsrc(g.dout + (int64_t)b * hsd, span * 2u);
   const rsrc_t rdq = make_rsrc((const uint8_t*)g.dq + (int64_t)b * hsd * (g.dq_bf16 ? 2 : 4),
-                               hsd * (g.dq_bf16 ? 2u : 4u));
+                               span * (g.dq_bf16 ? 2u : 4u));
   // Elements of the lane (head 0): 8 consecutive from ea, or with HALVES 4
   // from ea and 4 from eb = ea + D / 2, so that each of its two 16-byte fp32
-  // stores lies in a contiguous half-row span of the row's lanes.
+  // stores lies in a contiguous half-row span of the row's lanes.  wa / wb:
+  // the same elements in the workspace's head-sum plane, rows of D.
   const uint32_t li = (uint32_t)(t % lpr);
-  const uint32_t ea = (uint32_t)row * (uint32_t)g.D + li * (HALVES ? 4u : 8u);
+  const uint32_t lo = li * (HALVES ? 4u : 8u);
+  const uint32_t ea = (uint32_t)row * (uint32_t)g.ld + lo;
   const uint32_t eb = ea + (uint32_t)g.D / 2u;
-  const uint32_t hstride = (uint32_t)g.S * (uint32_t)g.D;
+  const uint32_t wa = (uint32_t)row * (uint32_t)g.D + lo;
+  const uint32_t wb = wa + (uint32_t)g.D / 2u;
+  const uint32_t hstride = (uint32_t)g.S * (uint32_t)g.ld;
   const bool write_dq = row >= g.erows;
   const bool dq_bf16 = g.dq_bf16 != 0;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -147,18 +164,18 @@ __global__ void __launch_bounds__(kThreads) mla_stream_do(const MArgs g) {
       }
     }
   };
-  // 8 fp32 values of the lane at head offset ho: one 16-byte bf16 or two
-  // 16-byte fp32 stores at ea (HALVES: the second at eb).
-  auto store_lane = [&](const rsrc_t& rs, bool bf16, uint32_t ho, const float (&v)[8]) {
+  // 8 fp32 values of the lane: one 16-byte bf16 or two 16-byte fp32 stores at
+  // element xa (HALVES: the second at xb).
+  auto store_lane = [&](const rsrc_t& rs, bool bf16, uint32_t xa, uint32_t xb, const float (&v)[8]) {
     if constexpr (HALVES) {
       const u32x4 x = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
                        __float_as_uint(v[3])};
       const u32x4 y = {__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]),
                        __float_as_uint(v[7])};
-      __builtin_amdgcn_raw_buffer_store_b128(x, rs, (ea + ho) * 4u, 0, kNonTemporal);
-      __builtin_amdgcn_raw_buffer_store_b128(y, rs, (eb + ho) * 4u, 0, kNonTemporal);
+      __builtin_amdgcn_raw_buffer_store_b128(x, rs, xa * 4u, 0, kNonTemporal);
+      __builtin_amdgcn_raw_buffer_store_b128(y, rs, xb * 4u, 0, kNonTemporal);
     } else {
-      store8(rs, bf16, ea + ho, v);
+      store8(rs, bf16, xa, v);
     }
   };
   u32x4 cur[U], nxt[U];
@@ -180,7 +197,8 @@ __global__ void __launch_bounds__(kThreads) mla_stream_do(const MArgs g) {
           float d[8];
 #pragma unroll
           for (int k = 0; k < 8; ++k) d[k] = f[k] * g.scale;
-          store_lane(rdq, dq_bf16, (uint32_t)(h0 + u) * hstride, d);
+          const uint32_t ho = (uint32_t)(h0 + u) * hstride;
+          store_lane(rdq, dq_bf16, ea + ho, eb + ho, d);
         }
       }
     }
@@ -193,7 +211,7 @@ __global__ void __launch_bounds__(kThreads) mla_stream_do(const MArgs g) {
   for (int k = 0; k < 8; ++k) o[k] = acc[k] / n1;
   const uint32_t sd = (uint32_t)g.S * (uint32_t)g.D;
   const rsrc_t rhs = make_rsrc(g.hs + (int64_t)blockIdx.z * g.hs_split + (int64_t)b * sd, sd * 4u);
-  store_lane(rhs, false, 0u, o);
+  store_lane(rhs, false, wa, wb, o);
 }
 
 // ------------------------------------------------------------------ K2: exact rows
@@ -201,74 +219,90 @@ __global__ void __launch_bounds__(kThreads) mla_stream_do(const MArgs g) {
 constexpr int kWide = 1024;               // threads of K2 and K3 (16 waves)
 
 // Exact rows 0..E-1 of (b, h), wave m owning query row m for delta and dq;
-// wave 0 computes all 16 x 16 logits and dP with MFMAs.  Every global load
-// is issued before the first LDS store: wave m loads chunk `lane` (16 bytes)
-// of its q, do and out rows, and thread t chunk t of c rows 0..E-1
-// (16 D / 8 <= 1024 chunks).  Buffer descriptors over rows 0..E-1 return
-// zeros for the rest.  Dynamic LDS: q, do and c rows 0..15 (padded by 16
-// bytes), then dS [16][16] and delta [16].
+// wave 0 computes all 16 x 16 logits and dP with MFMAs.  The rows' D = ld
+// dims go through LDS in chunks of W = min(D, kSliceD): per chunk, every
+// global load is issued before the first LDS store (wave m loads 16-byte
+// piece `lane` of its q, do and out rows, thread t piece t % (W / 8) of c
+// row t / (W / 8)); buffer descriptors over rows 0..E-1 return zeros for the
+// rest.  The logits, dP and delta accumulate over the chunks; dS follows; then
+// dq, chunk by chunk (c staged again when D > W).  Dynamic LDS: q, do and c
+// rows 0..15 of one chunk (padded by 16 bytes), then dS [16][16] and delta [16].
 __device__ __forceinline__ void exact_rows(const MArgs& g, int b, int h) {
   extern __shared__ __align__(16) uint8_t smem[];
-  const int D = g.D, E = g.erows;
-  const int ld = D + kPadElems;                   // bf16 elements per LDS row
+  const int D = g.ld, E = g.erows;
+  const int W = D < kSliceD ? D : kSliceD;
+  const int ldl = W + kPadElems;                  // bf16 elements per LDS row
   uint16_t* qs = reinterpret_cast<uint16_t*>(smem);
-  uint16_t* dos = qs + kE * ld;
-  uint16_t* cs = dos + kE * ld;
-  float* dS = reinterpret_cast<float*>(cs + kE * ld);
+  uint16_t* dos = qs + kE * ldl;
+  uint16_t* cs = dos + kE * ldl;
+  float* dS = reinterpret_cast<float*>(cs + kE * ldl);
+  float* deltas = dS + kE * kE;                   // [kE], after dS
   const int t = threadIdx.x, lane = t & 63, m = t >> 6;
   const int bh = b * g.H + h;
-  const int cpr = D / 8;                          // 16-byte chunks per row (8..64)
   const int64_t qrow0 = (int64_t)bh * g.S * D;    // q, do, out rows of (b, h)
   const uint32_t rbytes = (uint32_t)(E * D * 2);
   const rsrc_t rq = make_rsrc(g.q + qrow0, rbytes);
   const rsrc_t rdo = make_rsrc(g.dout + qrow0, rbytes);
   const rsrc_t rout = make_rsrc(g.out + qrow0, rbytes);
   const rsrc_t rc = make_rsrc(g.c + (int64_t)b * g.S * D, rbytes);
-  const uint32_t off = m < E && lane < cpr ? (uint32_t)(m * D + lane * 8) * 2u : rbytes;
-  const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0);
-  const u32x4 d = __builtin_amdgcn_raw_buffer_load_b128(rdo, off, 0, 0);
-  const u32x4 o = __builtin_amdgcn_raw_buffer_load_b128(rout, off, 0, 0);
-  const u32x4 cv = __builtin_amdgcn_raw_buffer_load_b128(rc, (uint32_t)t * 16u, 0, 0);
-  if (lane < cpr) {
-    *reinterpret_cast<u32x4*>(qs + m * ld + lane * 8) = a;
-    *reinterpret_cast<u32x4*>(dos + m * ld + lane * 8) = d;
-  }
-  if (t < kE * cpr) *reinterpret_cast<u32x4*>(cs + (t / cpr) * ld + (t % cpr) * 8) = cv;
-  // delta_m = out_m . do_m (wave-wide).
-  float delta = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    delta += bf16_lo(o[j]) * bf16_lo(d[j]);
-    delta += bf16_hi(o[j]) * bf16_hi(d[j]);
-  }
-#pragma unroll
-  for (int s = 32; s > 0; s >>= 1) delta += __shfl_xor(delta, s, 64);
-  float* deltas = dS + kE * kE;                   // [kE], after dS
-  if (lane == 0) deltas[m] = delta;
-  __syncthreads();
+  // c rows 0..15 of the W-wide chunk at dim c0 (t < 16 W / 8 <= 1024).
+  auto stage_c = [&](int c0, int cpr) {
+    const int cr = t / cpr;
+    const uint32_t coff = cr < E ? (uint32_t)(cr * D + c0 + (t % cpr) * 8) * 2u : rbytes;
+    const u32x4 cv = __builtin_amdgcn_raw_buffer_load_b128(rc, coff, 0, 0);
+    if (t < kE * cpr) *reinterpret_cast<u32x4*>(cs + cr * ldl + (t % cpr) * 8) = cv;
+  };
 
   // Logits and dP of query row qm = lane % 16 with keys n = 4 (lane / 16) +
   // r (r < 4), by wave 0 alone: v_mfma_f32_16x16x32_bf16 with A = c rows
-  // (key), B = q or dO rows (query), K = D in steps of 32.  Lane l supplies
-  // row l % 16 of both operands, 8 consecutive dims (the same ones for both)
-  // per step, and receives D[4 (l / 16) + r][l % 16] (checked on the GPU).
-  // Rows past E were staged as zeros.
-  if (m == 0) {
-    const int qm = lane & 15, k0 = (lane >> 4) * 8;
-    const uint16_t* cr = cs + qm * ld + k0;
-    const uint16_t* qr = qs + qm * ld + k0;
-    const uint16_t* dr = dos + qm * ld + k0;
-    f32x4 lg = {0.0f, 0.0f, 0.0f, 0.0f}, dpv = lg;
-    auto ld8 = [](const uint16_t* p) { return *reinterpret_cast<const bf16x8*>(p); };
-#pragma unroll 2
-    for (int k = 0; k < D; k += 64) {             // D % 64 == 0: two steps per pass
-      const bf16x8 c0 = ld8(cr + k), q0 = ld8(qr + k), d0 = ld8(dr + k);
-      const bf16x8 c1 = ld8(cr + k + 32), q1 = ld8(qr + k + 32), d1 = ld8(dr + k + 32);
-      lg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c0, q0, lg, 0, 0, 0);
-      dpv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c0, d0, dpv, 0, 0, 0);
-      lg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c1, q1, lg, 0, 0, 0);
-      dpv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c1, d1, dpv, 0, 0, 0);
+  // (key), B = q or dO rows (query), K = the chunk's dims in steps of 32.
+  // Lane l supplies row l % 16 of both operands, 8 consecutive dims (the same
+  // ones for both) per step, and receives D[4 (l / 16) + r][l % 16] (checked
+  // on the GPU).  Rows past E were staged as zeros.
+  const int qm = lane & 15, k0 = (lane >> 4) * 8;
+  f32x4 lg = {0.0f, 0.0f, 0.0f, 0.0f}, dpv = lg;
+  float delta = 0.0f;
+  for (int c0 = 0; c0 < D; c0 += W) {
+    const int w = D - c0 < W ? D - c0 : W;        // a multiple of 64
+    const int cpr = w / 8;                        // 16-byte pieces per row (8..64)
+    if (c0 > 0) __syncthreads();                  // the previous chunk's reads are done
+    const uint32_t off = m < E && lane < cpr ? (uint32_t)(m * D + c0 + lane * 8) * 2u : rbytes;
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0);
+    const u32x4 d = __builtin_amdgcn_raw_buffer_load_b128(rdo, off, 0, 0);
+    const u32x4 o = __builtin_amdgcn_raw_buffer_load_b128(rout, off, 0, 0);
+    stage_c(c0, cpr);
+    if (lane < cpr) {
+      *reinterpret_cast<u32x4*>(qs + m * ldl + lane * 8) = a;
+      *reinterpret_cast<u32x4*>(dos + m * ldl + lane * 8) = d;
     }
+    // delta_m = out_m . do_m, this lane's part.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      delta += bf16_lo(o[j]) * bf16_lo(d[j]);
+      delta += bf16_hi(o[j]) * bf16_hi(d[j]);
+    }
+    __syncthreads();
+    if (m == 0) {
+      const uint16_t* cr = cs + qm * ldl + k0;
+      const uint16_t* qr = qs + qm * ldl + k0;
+      const uint16_t* dr = dos + qm * ldl + k0;
+      auto ld8 = [](const uint16_t* p) { return *reinterpret_cast<const bf16x8*>(p); };
+#pragma unroll 2
+      for (int k = 0; k < w; k += 64) {           // w % 64 == 0: two steps per pass
+        const bf16x8 c0v = ld8(cr + k), q0 = ld8(qr + k), d0 = ld8(dr + k);
+        const bf16x8 c1v = ld8(cr + k + 32), q1 = ld8(qr + k + 32), d1 = ld8(dr + k + 32);
+        lg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c0v, q0, lg, 0, 0, 0);
+        dpv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c0v, d0, dpv, 0, 0, 0);
+        lg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c1v, q1, lg, 0, 0, 0);
+        dpv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c1v, d1, dpv, 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) delta += __shfl_xor(delta, s, 64);
+  if (lane == 0) deltas[m] = delta;
+  __syncthreads();
+  if (m == 0) {
     const float lse = qm < E ? g.lse[(int64_t)bh * g.S + qm] : 0.0f;
     const float dlt = deltas[qm];
 #pragma unroll
@@ -284,22 +318,29 @@ __device__ __forceinline__ void exact_rows(const MArgs& g, int b, int h) {
   }
   __syncthreads();
 
-  // dq row m: lane owns 8-dim groups lane, lane + 64, ...
-  if (m < E) {
-    const rsrc_t rdq = make_rsrc((const uint8_t*)g.dq + qrow0 * (g.dq_bf16 ? 2 : 4),
-                                 (uint32_t)(E * D) * (g.dq_bf16 ? 2u : 4u));
-    for (int k = lane * 8; k < D; k += 64 * 8) {
+  // dq row m, chunk by chunk: lane owns dims c0 + 8 lane .. + 7.
+  const rsrc_t rdq = make_rsrc((const uint8_t*)g.dq + qrow0 * (g.dq_bf16 ? 2 : 4),
+                               (uint32_t)(E * D) * (g.dq_bf16 ? 2u : 4u));
+  for (int c0 = 0; c0 < D; c0 += W) {
+    const int w = D - c0 < W ? D - c0 : W;
+    if (D > W) {                                  // c of this chunk (one chunk: still staged)
+      __syncthreads();
+      stage_c(c0, w / 8);
+      __syncthreads();
+    }
+    if (m < E && lane * 8 < w) {
+      const int k = lane * 8;
       float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
       for (int j = 0; j <= m; ++j) {
         const float sv = dS[m * kE + j];
-        const u32x4 c = *reinterpret_cast<const u32x4*>(cs + j * ld + k);
+        const u32x4 c = *reinterpret_cast<const u32x4*>(cs + j * ldl + k);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           acc[2 * i] = fmaf(sv, bf16_lo(c[i]), acc[2 * i]);
           acc[2 * i + 1] = fmaf(sv, bf16_hi(c[i]), acc[2 * i + 1]);
         }
       }
-      store8(rdq, g.dq_bf16 != 0, (uint32_t)(m * D + k), acc);
+      store8(rdq, g.dq_bf16 != 0, (uint32_t)(m * D + c0 + k), acc);
     }
   }
 }
@@ -307,7 +348,8 @@ __device__ __forceinline__ void exact_rows(const MArgs& g, int b, int h) {
 // Dynamic LDS of K2: the exact rows' rows and dS, at least kWide float4 for
 // the block totals' join.
 size_t k2_lds_bytes(int64_t D) {
-  const size_t ex = (size_t)3 * kE * (D + kPadElems) * 2 + (size_t)(kE * kE + kE) * 4;
+  const int64_t W = D < kSliceD ? D : kSliceD;
+  const size_t ex = (size_t)3 * kE * (W + kPadElems) * 2 + (size_t)(kE * kE + kE) * 4;
   const size_t bt = (size_t)kWide * 16;
   return ex > bt ? ex : bt;
 }
@@ -392,14 +434,15 @@ __device__ __forceinline__ void block_total(const MArgs& g, int b, int blk) {
   }
 }
 
-// grid (H + nblk, B): x < H are the exact rows of head x, the rest block
-// totals.  Uniform per workgroup, so every barrier sees all its waves.
+// grid (nexact + nblk, B): x < nexact (H in the first column slice, else 0)
+// are the exact rows of head x, the rest block totals.  Uniform per
+// workgroup, so every barrier sees all its waves.
 __global__ void __launch_bounds__(kWide) mla_exact_rows_block_total(const MArgs g) {
   const int x = (int)blockIdx.x, b = (int)blockIdx.y;
-  if (x < g.H)
+  if (x < g.nexact)
     exact_rows(g, b, x);
   else
-    block_total(g, b, x - g.H);
+    block_total(g, b, x - g.nexact);
 }
 
 // ------------------------------------------------------------------ K3
@@ -453,8 +496,8 @@ __global__ void __launch_bounds__(kWide) mla_suffix_scan(const MArgs g) {
   float4 cy = make_float4(0.f, 0.f, 0.f, 0.f);
   for (int q = 0; q < P.np; ++q) add4(cy, later[q * P.cpt + P.col]);
   for (int q = P.np - 1; q > P.p; --q) add4(cy, chunk[q * P.cpt + P.col]);
-  float* __restrict__ dcf = static_cast<float*>(g.dc) + (int64_t)b * g.S * g.D + 4 * P.col;
-  uint16_t* __restrict__ dch = static_cast<uint16_t*>(g.dc) + (int64_t)b * g.S * g.D + 4 * P.col;
+  float* __restrict__ dcf = static_cast<float*>(g.dc) + (int64_t)b * g.S * g.ld + 4 * P.col;
+  uint16_t* __restrict__ dch = static_cast<uint16_t*>(g.dc) + (int64_t)b * g.S * g.ld + 4 * P.col;
   const bool bf16 = g.dc_bf16 != 0;
 #pragma unroll
   for (int k = 0; k < kChunkRows; ++k) {
@@ -463,9 +506,9 @@ __global__ void __launch_bounds__(kWide) mla_suffix_scan(const MArgs g) {
       add4(cy, rows[k]);
       if (bf16) {
         const uint2 wv = {pack_bf16x2(cy.x, cy.y), pack_bf16x2(cy.z, cy.w)};
-        *reinterpret_cast<uint2*>(dch + (int64_t)r * g.D) = wv;
+        *reinterpret_cast<uint2*>(dch + (int64_t)r * g.ld) = wv;
       } else {
-        *reinterpret_cast<float4*>(dcf + (int64_t)r * g.D) = cy;
+        *reinterpret_cast<float4*>(dcf + (int64_t)r * g.ld) = cy;
       }
     }
   }
@@ -500,11 +543,24 @@ int64_t block_rows(int64_t S) {
   return r < 16 ? 16 : r > 64 ? 64 : r;
 }
 
+// Dims of column slice `i` of D (slices of kSliceD, the last one shorter).
+int64_t slice_dims(int64_t D, int64_t i) {
+  const int64_t rest = D - i * kSliceD;
+  return rest < kSliceD ? rest : kSliceD;
+}
+
+// The workspace holds one column slice at a time: the most any of D's slices
+// (kSliceD wide, the last one D % kSliceD when that is not 0) needs.
 int64_t workspace_bytes(int64_t B, int64_t S, int64_t D) {
-  if (B < 0 || S < 0 || D < 0 || B > (1 << 20) || S > (1ll << 31) || D > kMaxD) return -1;
-  const int64_t sp = head_split(B, S, D, kMaxHeadSplit);   // the most any H can use
+  if (B < 0 || S < 0 || D < 0 || B > (1 << 20) || S > (1ll << 31) || D > (1ll << 31)) return -1;
   const int64_t nblk = (S + block_rows(S) - 1) / block_rows(S);
-  return (sp * B * S + B * nblk) * D * 4;
+  auto slice_bytes = [&](int64_t w) {
+    const int64_t sp = head_split(B, S, w, kMaxHeadSplit);   // the most any H can use
+    return (sp * B * S + B * nblk) * w * 4;
+  };
+  const int64_t a = slice_bytes(D < kSliceD ? D : kSliceD);
+  const int64_t b = D > kSliceD && D % kSliceD ? slice_bytes(D % kSliceD) : 0;
+  return a > b ? a : b;
 }
 
 }  // namespace
@@ -537,7 +593,7 @@ int check_args(const void* q, const void* c_kv, const void* out, const void* dou
     return FAGQ_E_FORMAT;
   if (B < 0 || H < 1 || S < 1 || D < 64 || D % 64 != 0 || !(sm_scale == sm_scale))
     return FAGQ_E_SHAPE;
-  if (D > kMaxD || B > 65535 || H > 65535 || H * S * D * 4 >= (1ll << 32)) return FAGQ_E_TOO_LARGE;
+  if (B > 65535 || H > 65535 || H * S * D * 4 >= (1ll << 32)) return FAGQ_E_TOO_LARGE;
   *need = workspace_bytes(B, S, D);
   if (*need < 0) return FAGQ_E_TOO_LARGE;
   if (!aligned(q, 16) || !aligned(c_kv, 16) || !aligned(out, 16) || !aligned(dout, 16) ||
@@ -566,49 +622,61 @@ int launch(const void* q, const void* c_kv, const void* out, const void* dout, c
   const int dcheck = device_check();
   if (dcheck != FAGQ_OK) return dcheck;
 
-  MArgs g;
-  g.q = static_cast<const uint16_t*>(q);
-  g.c = static_cast<const uint16_t*>(c_kv);
-  g.out = static_cast<const uint16_t*>(out);
-  g.dout = static_cast<const uint16_t*>(dout);
-  g.lse = lse;
-  g.dq = dq;
-  g.dc = dc_kv;
-  const int64_t hsplit = head_split(B, S, D, H);
-  g.hps = (int32_t)((H + hsplit - 1) / hsplit);
-  g.hsplit = (int32_t)((H + g.hps - 1) / g.hps);          // non-empty head groups
-  g.hs = static_cast<float*>(workspace);
-  g.hs_split = B * S * D;
-  g.brows = (int32_t)block_rows(S);
-  g.nblk = (int32_t)((S + g.brows - 1) / g.brows);
-  g.tot = g.hs + g.hsplit * B * S * D;
-  g.H = (int32_t)H;
-  g.S = (int32_t)S;
-  g.D = (int32_t)D;
-  g.erows = (int32_t)(S < kE ? S : kE);
-  g.scale = sm_scale;
-  g.dq_bf16 = dq_dtype == FAGQ_MLA_BF16;
-  g.dc_bf16 = dc_dtype == FAGQ_MLA_BF16;
+  // One pass per column slice; every slice's kernels run in stream order, so
+  // each reuses the workspace after the previous slice's K3 has read it.
+  const int64_t nslice = (D + kSliceD - 1) / kSliceD;
+  const int64_t qb = dq_dtype == FAGQ_MLA_BF16 ? 2 : 4, cb = dc_dtype == FAGQ_MLA_BF16 ? 2 : 4;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  void* args[] = {&g};
-  const int rows_per_wg = kThreads / (int)(D / 8);
-  const dim3 k1_grid((unsigned)((S + rows_per_wg - 1) / rows_per_wg), (unsigned)B, (unsigned)g.hsplit);
-  const bool k1_wide = (int64_t)k1_grid.x * k1_grid.y * k1_grid.z <= kMinK1Groups;
-  const bool halves = dq_dtype == FAGQ_MLA_F32;
-  const void* k1 = halves ? (k1_wide ? reinterpret_cast<const void*>(&mla_stream_do<8, true>)
-                                     : reinterpret_cast<const void*>(&mla_stream_do<2, true>))
-                          : (k1_wide ? reinterpret_cast<const void*>(&mla_stream_do<8, false>)
-                                     : reinterpret_cast<const void*>(&mla_stream_do<2, false>));
-  hipError_t e = hipLaunchKernel(k1, k1_grid, dim3(kThreads), args, 0, st);
-  if (e != hipSuccess) return -(int)e;
-  // H + nblk < 2^17 + 2^20: nblk <= S / 16 + 1 and H S D 4 < 2^32 with D >= 64.
-  e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_exact_rows_block_total),
-                      dim3((unsigned)(H + g.nblk), (unsigned)B), dim3(kWide), args, k2_lds_bytes(D),
-                      st);
-  if (e != hipSuccess) return -(int)e;
-  e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_suffix_scan),
-                      dim3((unsigned)g.nblk, (unsigned)B), dim3(kWide), args, 0, st);
-  return launch_status(e);
+  for (int64_t sl = 0; sl < nslice; ++sl) {
+    const int64_t col = sl * kSliceD, ds = slice_dims(D, sl);
+    MArgs g;
+    g.q = static_cast<const uint16_t*>(q);         // the exact rows (first slice) read all of D
+    g.c = static_cast<const uint16_t*>(c_kv);
+    g.out = static_cast<const uint16_t*>(out);
+    g.dout = static_cast<const uint16_t*>(dout) + col;
+    g.lse = lse;
+    g.dq = static_cast<uint8_t*>(dq) + col * qb;   // K1's rows; the exact rows run with col = 0
+    g.dc = static_cast<uint8_t*>(dc_kv) + col * cb;
+    const int64_t hsplit = head_split(B, S, ds, H);
+    g.hps = (int32_t)((H + hsplit - 1) / hsplit);
+    g.hsplit = (int32_t)((H + g.hps - 1) / g.hps);        // non-empty head groups
+    g.hs = static_cast<float*>(workspace);
+    g.hs_split = B * S * ds;
+    g.brows = (int32_t)block_rows(S);
+    g.nblk = (int32_t)((S + g.brows - 1) / g.brows);
+    g.tot = g.hs + g.hsplit * B * S * ds;
+    g.H = (int32_t)H;
+    g.S = (int32_t)S;
+    g.D = (int32_t)ds;
+    g.ld = (int32_t)D;
+    g.nexact = sl == 0 ? (int32_t)H : 0;
+    g.erows = (int32_t)(S < kE ? S : kE);
+    g.scale = sm_scale;
+    g.dq_bf16 = dq_dtype == FAGQ_MLA_BF16;
+    g.dc_bf16 = dc_dtype == FAGQ_MLA_BF16;
+    void* args[] = {&g};
+    const int rows_per_wg = kThreads / (int)(ds / 8);
+    const dim3 k1_grid((unsigned)((S + rows_per_wg - 1) / rows_per_wg), (unsigned)B,
+                       (unsigned)g.hsplit);
+    const bool k1_wide = (int64_t)k1_grid.x * k1_grid.y * k1_grid.z <= kMinK1Groups;
+    const bool halves = dq_dtype == FAGQ_MLA_F32;
+    const void* k1 = halves ? (k1_wide ? reinterpret_cast<const void*>(&mla_stream_do<8, true>)
+                                       : reinterpret_cast<const void*>(&mla_stream_do<2, true>))
+                            : (k1_wide ? reinterpret_cast<const void*>(&mla_stream_do<8, false>)
+                                       : reinterpret_cast<const void*>(&mla_stream_do<2, false>));
+    hipError_t e = hipLaunchKernel(k1, k1_grid, dim3(kThreads), args, 0, st);
+    if (e != hipSuccess) return -(int)e;
+    // nexact + nblk < 2^17 + 2^20: nblk <= S / 16 + 1 and H S D 4 < 2^32 with D >= 64.
+    e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_exact_rows_block_total),
+                        dim3((unsigned)(g.nexact + g.nblk), (unsigned)B), dim3(kWide), args,
+                        k2_lds_bytes(D), st);
+    if (e != hipSuccess) return -(int)e;
+    e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_suffix_scan),
+                        dim3((unsigned)g.nblk, (unsigned)B), dim3(kWide), args, 0, st);
+    const int ls = launch_status(e);
+    if (ls != FAGQ_OK) return ls;
+  }
+  return FAGQ_OK;
 }
 
 // The workspace of fagq_mla_bwd_launch_noalloc: one array per GPU the library

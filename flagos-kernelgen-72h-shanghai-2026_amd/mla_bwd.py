@@ -20,7 +20,7 @@ from . import _lib
 
 MLA_F32, MLA_BF16 = 0, 1
 EXACT_ROWS = 16
-MAX_D = 512
+SLICE_D = 512     # dims per column slice of the kernels (include/fagq_mla.h)
 
 
 def _out_code(t: torch.Tensor, name: str) -> int:

@@ -34,14 +34,15 @@ extern "C" {
 #endif
 
 #define FAGQ_MLA_EXACT_ROWS 16
-#define FAGQ_MLA_MAX_D 512
+#define FAGQ_MLA_SLICE_D 512
 
 enum fagq_mla_dtype { FAGQ_MLA_F32 = 0, FAGQ_MLA_BF16 = 1 };
 
 /* Workspace bytes fagq_mla_bwd_launch needs for (B, S, D): fp32 partial
- * head sums [G, B, S, D] (G = 1 when the row grid fills the GPU, else up to 8
- * head groups) and the scan's block totals [B, nblk, D] (blocks of 16-64
- * rows).  Returns -1 for a negative or overflowing size. */
+ * head sums [G, B, S, W] (G = 1 when the row grid fills the GPU, else up to 8
+ * head groups) and the scan's block totals [B, nblk, W] (blocks of 16-64
+ * rows), W = min(D, FAGQ_MLA_SLICE_D).  Returns -1 for a negative or
+ * overflowing size. */
 FAGQ_API int64_t fagq_mla_bwd_workspace_bytes(int64_t B, int64_t S, int64_t D);
 
 /* q [B, H, S, D], out and dout [B, H, S, D], c_kv [B, S, D]: bfloat16,
@@ -49,8 +50,10 @@ FAGQ_API int64_t fagq_mla_bwd_workspace_bytes(int64_t B, int64_t S, int64_t D);
  * of the forward).  dq [B, H, S, D] and dc_kv [B, S, D]: fp32 or bf16
  * (dq_dtype, dc_dtype), 16-byte aligned.  workspace: at least
  * fagq_mla_bwd_workspace_bytes(B, S, D) bytes, 16-byte aligned, overwritten.
- * 64 <= D <= FAGQ_MLA_MAX_D, D % 64 == 0; B, H <= 65535; S >= 1;
- * H * S * D * 4 < 2^32.  Three kernels on `stream`. */
+ * D >= 64, D % 64 == 0; B, H <= 65535; S >= 1; H * S * D * 4 < 2^32.
+ * Three kernels on `stream` per column slice of FAGQ_MLA_SLICE_D dims (one
+ * slice for D <= 512; the reference's kernels, src/task03_mla_bwd_nope_dkdv.py:154,
+ * 166, 191, likewise walk D in 128-wide chunks with no cap). */
 FAGQ_API int fagq_mla_bwd_launch(const void* q, const void* c_kv, const void* out, const void* dout,
                                  const float* lse, void* dq, void* dc_kv, void* workspace,
                                  int64_t workspace_bytes, int64_t B, int64_t H, int64_t S,

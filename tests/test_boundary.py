@@ -389,7 +389,8 @@ def mla_call(lib, **kw):
     (dict(dqt=2), 5), (dict(dct=-1), 5),
     (dict(B=-1), 2), (dict(H=0), 2), (dict(S=0), 2), (dict(D=96), 2), (dict(D=32), 2),
     (dict(scale=float("nan")), 2), (dict(wsb=1000), 2),
-    (dict(D=576), 7), (dict(B=65536), 7), (dict(H=65536, S=64), 7), (dict(H=64, S=1 << 15), 7),
+    (dict(B=65536), 7), (dict(H=65536, S=64), 7), (dict(H=64, S=1 << 15), 7),
+    (dict(H=1, S=1 << 16, D=1 << 14), 7),
     (dict(q=ctypes.c_void_p(BASE + 8)), 4), (dict(lse=ctypes.c_void_p(BASE + 0x4_0000_0002)), 4),
     (dict(ws=ctypes.c_void_p(BASE + 0x7_0000_0004)), 4),
     (dict(dq=fake(0)), 9), (dict(dc=fake(3)), 9), (dict(ws=fake(5)), 9),
@@ -407,6 +408,9 @@ def test_mla_workspace_size(lib):
     # 16-row blocks
     assert lib.fagq_mla_bwd_workspace_bytes(1, 65, 64) == (8 * 65 + 5) * 64 * 4
     assert lib.fagq_mla_bwd_workspace_bytes(-1, 1, 64) == -1
+    # D above 512 runs in 512-wide column slices: the workspace holds one slice
+    assert lib.fagq_mla_bwd_workspace_bytes(2, 4096, 1024) == 2 * (4096 + 64) * 512 * 4
+    assert lib.fagq_mla_bwd_workspace_bytes(2, 4096, 576) == 2 * (4096 + 64) * 512 * 4
 
 
 def test_mla_workloads():

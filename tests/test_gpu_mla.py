@@ -43,11 +43,12 @@ def run_gpu(pkg, dev, q, c, out, do, lse, scale, grad_dtype, dc_dtype=None):
 
 
 def check_exact_rows(dq_gpu, dq_ref, bound, bf16_out, label):
-    E = bound.shape[3]
+    E, D = bound.shape[3], bound.shape[4]
     g = dq_gpu[:, :, :E].float().cpu().numpy().astype(np.float64)
-    # bf16 steps of P or dS, plus fp32 accumulation of the 512-term dot
-    # products behind dp - delta (2^-15 = 512 x 2^-24 of their magnitude)
-    tol = 2.0 ** -7 * bound[0] + 2.0 ** -15 * bound[1] + 1e-7
+    # bf16 steps of P or dS, plus fp32 accumulation of the D-term dot
+    # products behind dp - delta (D x 2^-24 of their magnitude, at least
+    # 512 x 2^-24)
+    tol = 2.0 ** -7 * bound[0] + max(D, 512) * 2.0 ** -24 * bound[1] + 1e-7
     if bf16_out:
         tol = tol + 2.0 ** -8 * np.abs(dq_ref[:, :, :E])
     err = np.abs(g - dq_ref[:, :, :E])
@@ -98,6 +99,16 @@ def test_mla_uneven_head_groups(pkg, gpu, B, H, S, D, dq_dtype):
     # head sums; D not a power of two leaves some scan threads idle, and with
     # fp32 dq the dO pass splits each row into two halves of D / 2
     case(pkg, gpu, B, H, S, D, dq_dtype, torch.float32, seed=B + H + S)
+
+
+@pytest.mark.parametrize("B,H,S,D", [(1, 4, 40, 576), (2, 3, 10, 1024), (1, 6, 100, 640),
+                                     (1, 2, 300, 1152)])
+@pytest.mark.parametrize("dq_dtype", [torch.bfloat16, torch.float32])
+def test_mla_column_slices(pkg, gpu, B, H, S, D, dq_dtype):
+    # D above 512 runs in 512-wide column slices (the last one 64, 512, 128
+    # and 128 wide): the exact rows stage their rows in chunks and the other
+    # kernels run once per slice
+    case(pkg, gpu, B, H, S, D, dq_dtype, seed=D + S)
 
 
 def test_mla_mixed_output_dtypes(pkg, gpu):
