@@ -26,9 +26,17 @@
 // two lanes of a pass hit one bank at different addresses); the lanes of a
 // pass are not 16 consecutive ones.  fagq_diag_lds_read (include/fagq_diag.h)
 // measures the fragment read with this f at 4 cycles per instruction and with
-// f(r) = (r >> 1) & 7 or r & 7 at 8 (a 2-way conflict on every read).  Two LDS stages (2 x 64 KB, or 2 x 56 KB at
-// BN = 192): the next k-block's copies are issued before the current one is
-// consumed.
+// f(r) = (r >> 1) & 7 or r & 7 at 8 (a 2-way conflict on every read).
+//
+// Pipelines.
+//   * Ring (both scales UE8M0, and every BN = 192 kernel): five 32 KB slots,
+//     all 160 KB of LDS, hold the tile sequence A(0), B(0), A(1), B(1), ...;
+//     while k-block kb is consumed, B(kb + 1) and A(kb + 2) are in flight, so
+//     each activation tile has two k-blocks to land.
+//   * Two stages (fp32-promoted scales at BN = 256): 2 x 64 KB, the next
+//     k-block's copies issued before the current one is consumed.  The ring
+//     measured slower there: with its copies and waits in one block the
+//     compiler stops reading the next weight fragment ahead of the products.
 //
 // Scales.  fp32 (or mixed) scales: each k-block's 16 x 16 x 128 product goes
 // to a temporary and is added to the accumulator as t * (sa * sb) with fmaf.
@@ -95,6 +103,17 @@ struct Layout {
 using Layout256 = Layout<256, 4, 2>;
 using Layout192 = Layout<192, 4, 2>;
 constexpr int kVmcnt0 = 0x0F70;          // s_waitcnt vmcnt(0) (other counters not waited)
+// s_waitcnt vmcnt(n), other counters not waited (n < 64).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
+constexpr int kSlotBytes = kATileBytes;  // ring slot: one operand tile
+constexpr int kSlots = 5;                // 160 KB, all of a gfx950 CU's LDS
+static_assert(kMaxBN * kBK <= kSlotBytes, "a weight tile fits a ring slot");
+
+// The ring pipeline for a pair of scale formats and a layout (see the header).
+template <int ASF, int BSF, class L>
+constexpr bool uses_ring() {
+  return (ASF == SF_UE8M0 && BSF == SF_UE8M0) || L::BN != 256;
+}
 
 struct GArgs {
   const uint8_t* a;       // fp8 [M, K]
@@ -146,11 +165,26 @@ __device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
   return e ? __uint_as_float(e << 23) : __uint_as_float(0x00400000u);
 }
 
+// Keeps the memory instructions on either side in issue order.
+__device__ __forceinline__ void issue_order_fence() { asm volatile("" ::: "memory"); }
+// Workgroup barrier once this wave's LDS reads have returned; the caller has
+// waited for whichever LDS copies must have landed (__syncthreads would also
+// wait for every copy still in flight).
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+// The value is computed before this point, in program order with the other
+// volatile asm statements (the compiler would otherwise sink MFMAs, which
+// have no memory operands, past the ring's wait and barrier).
+__device__ __forceinline__ void pin(const f32x4& v) { asm volatile("" ::"v"(v)); }
+
 template <int ASF, int BSF, class L>
 __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g) {
   constexpr bool kHwScale = ASF == SF_UE8M0 && BSF == SF_UE8M0;
+  constexpr bool kRing = uses_ring<ASF, BSF, L>();
   constexpr int kTM = L::TM, kTN = L::TN;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * L::STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kRing ? kSlots * kSlotBytes
+                                                              : 2 * L::STAGE_BYTES];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -184,6 +218,28 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g)
     return (uint32_t)__builtin_amdgcn_readfirstlane(
         (int)((uint32_t)inst * 8u * (uint32_t)g.K + (uint32_t)kb * (uint32_t)kBK));
   };
+  // Ring: one operand tile's copies into a slot.  (The offset goes through a
+  // local: passed to the builtin as an expression, the host pass dropped the
+  // kernel's handle.)
+  auto issue_a = [&](int kb, int slot) {
+    uint8_t* dst = lds + slot * kSlotBytes;
+#pragma unroll
+    for (int u = 0; u < L::COPY_A; ++u) {
+      const int inst = wave * L::COPY_A + u;
+      const uint32_t off = cvoff + copy_off(inst, kb);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(dst + inst * 1024), 16, off, 0, 0, 0);
+    }
+  };
+  auto issue_b = [&](int kb, int slot) {
+    uint8_t* dst = lds + slot * kSlotBytes;
+#pragma unroll
+    for (int u = 0; u < L::COPY_B; ++u) {
+      const int inst = wave * L::COPY_B + u;
+      const uint32_t off = cvoff + copy_off(inst, kb);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(dst + inst * 1024), 16, off, 0, 0, 0);
+    }
+  };
+  // Two stages: both tiles of k-block kb into a stage, their copies interleaved.
   auto issue = [&](int kb, int stage) {
     uint8_t* sa_tile = lds + stage * L::STAGE_BYTES;
     uint8_t* sb_tile = sa_tile + kATileBytes;
@@ -252,17 +308,56 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g)
 #pragma unroll
     for (int i = 0; i < kTM; ++i) acc[j][i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  issue(0, 0);
-  Scales cur = load_scales(0);
-  __builtin_amdgcn_s_waitcnt(kVmcnt0);
-  __syncthreads();
+  // Ring: k-block kb reads slots (2 kb) % 5 and (2 kb + 1) % 5.  Its
+  // iteration issues B(kb + 1), then kb + 1's scales, then A(kb + 2), into
+  // the two slots the barrier ending k-block kb - 1 released; A(kb + 1) was
+  // issued one k-block earlier.  The counter being in order, the wait that
+  // ends the k-block for everything but the last COPY_A instructions leaves
+  // only A(kb + 2) in flight.  Past the last k-block the same instructions
+  // fetch the last k-block again into slots nobody reads, so every iteration
+  // issues and waits alike: no branch for the compiler to move the products
+  // across, and the wait's count is a constant.
+  const int last = g.kblocks - 1;
+  Scales cur;
+  if constexpr (kRing) {
+    issue_a(0, 0);
+    issue_b(0, 1);
+    cur = load_scales(0);
+    issue_order_fence();
+    issue_a(last < 1 ? last : 1, 2);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(L::COPY_A));
+    ring_barrier();
+  } else {
+    issue(0, 0);
+    cur = load_scales(0);
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    __syncthreads();
+  }
 
+  int slot_a = 0;   // ring: (2 kb) % kSlots
   for (int kb = 0; kb < g.kblocks; ++kb) {
-    const int stage = kb & 1;
+    const uint8_t* ta;
+    const uint8_t* tb;
     Scales nxt = cur;
-    if (kb + 1 < g.kblocks) {
-      issue(kb + 1, stage ^ 1);
-      nxt = load_scales(kb + 1);
+    if constexpr (kRing) {
+      const int slot_b = slot_a + 1 < kSlots ? slot_a + 1 : 0;
+      const int slot_nb = slot_a + 3 < kSlots ? slot_a + 3 : slot_a + 3 - kSlots;   // B(kb + 1)
+      const int slot_na = slot_a + 4 < kSlots ? slot_a + 4 : slot_a + 4 - kSlots;   // A(kb + 2)
+      const int kb1 = kb + 1 < last ? kb + 1 : last, kb2 = kb + 2 < last ? kb + 2 : last;
+      issue_b(kb1, slot_nb);
+      nxt = load_scales(kb1);
+      issue_order_fence();
+      issue_a(kb2, slot_na);
+      ta = lds + slot_a * kSlotBytes;
+      tb = lds + slot_b * kSlotBytes;
+    } else {
+      const int stage = kb & 1;
+      if (kb + 1 < g.kblocks) {
+        issue(kb + 1, stage ^ 1);
+        nxt = load_scales(kb + 1);
+      }
+      ta = lds + stage * L::STAGE_BYTES;
+      tb = ta + kATileBytes;
     }
     constexpr int kNB = L::SPLIT ? 2 : 1;
     float smul[kNB][kTM];
@@ -274,8 +369,6 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g)
         for (int i = 0; i < kTM; ++i) smul[h][i] = to_f32(cur.a[i], ASF == SF_UE8M0) * sb;
       }
     }
-    const uint8_t* ta = lds + stage * L::STAGE_BYTES;
-    const uint8_t* tb = ta + kATileBytes;
     i32x8 af[kTM];
 #pragma unroll
     for (int i = 0; i < kTM; ++i) af[i] = lds_frag(ta, wm * 16 * kTM + 16 * i + (lane & 15), lane);
@@ -298,12 +391,31 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g)
         }
       }
     }
+    if constexpr (kRing && kHwScale) {
+      // The products are issued before the ring's wait.  (With fp32-promoted
+      // scales the compiler keeps most of them there by itself, and pinning
+      // serialises each product with its promotion: slower.)
+#pragma unroll
+      for (int j = 0; j < kTN; ++j)
+#pragma unroll
+        for (int i = 0; i < kTM; ++i) pin(acc[j][i]);
+    }
     cur = nxt;
-    // The next stage's copies have landed (each wave waits for its own) and
-    // every wave is done reading this stage before it is refilled.
-    __builtin_amdgcn_s_waitcnt(kVmcnt0);
-    __syncthreads();
+    if constexpr (kRing) {
+      // The next k-block's tiles and scales have landed (each wave waits for
+      // its own copies) and every wave is done reading this k-block's slots
+      // before the next iteration refills them.
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(L::COPY_A));
+      ring_barrier();
+      slot_a = slot_a + 2 < kSlots ? slot_a + 2 : slot_a + 2 - kSlots;
+    } else {
+      // The next stage's copies have landed (each wave waits for its own) and
+      // every wave is done reading this stage before it is refilled.
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);
+      __syncthreads();
+    }
   }
+  if constexpr (kRing) __builtin_amdgcn_s_waitcnt(kVmcnt0);   // no copy into LDS outlives the workgroup
 
   const rsrc_t rc = make_rsrc(g.c + (int64_t)m0 * g.N, (uint32_t)mrows * (uint32_t)g.N * 2u);
 #pragma unroll
