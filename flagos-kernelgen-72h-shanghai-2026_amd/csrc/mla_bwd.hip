@@ -86,6 +86,8 @@ struct MArgs {
   float scale;
   int32_t dq_bf16;    // dq is bf16 (else fp32)
   int32_t dc_bf16;
+  int32_t bsplit_sh;  // K2 workgroups per scan block = 1 << bsplit_sh, each summing
+                      // D >> bsplit_sh of its columns
 };
 
 __device__ __forceinline__ float bf16_to_f(uint32_t h) { return __uint_as_float(h << 16); }
@@ -365,9 +367,10 @@ __device__ __forceinline__ void add4(float4& a, const float4& b) {
   a.w += b.w;
 }
 
-// Thread layout of K2's block totals and K3: cpt = D / 4 column threads (16..128)
-// per part, np = kWide / cpt parts (8..64); thread t owns columns
-// 4 (t % cpt) .. + 3 of part t / cpt (threads of parts >= np idle).
+// Thread layout of K2's block totals and K3 over D columns (K2: the
+// workgroup's column slice): cpt = D / 4 column threads (16..128) per part,
+// np = kWide / cpt parts (8..64); thread t owns columns 4 (t % cpt) .. + 3 of
+// part t / cpt (threads of parts >= np idle).
 struct Parts {
   int cpt, np, p, col;
   __device__ explicit Parts(int D) : cpt(D >> 2), np(kWide / (D >> 2)), p((int)threadIdx.x / (D >> 2)),
@@ -380,12 +383,13 @@ struct Parts {
 // (planes in order) is written back over plane 0, so K3 reads one plane.
 // The parts' totals are joined in LDS, in part order.
 template <int HS>
-__device__ __forceinline__ void block_total_hs(const MArgs& g, int b, int blk, float4* part) {
+__device__ __forceinline__ void block_total_hs(const MArgs& g, int b, int blk, int cs, float4* part) {
   constexpr int R = kBatch / HS;
-  const Parts P(g.D);
+  const int cols = g.D >> g.bsplit_sh;            // this workgroup's columns: cs cols .. + cols
+  const Parts P(cols);
   const int r0 = blk * g.brows;
   const int r1 = r0 + g.brows < g.S ? r0 + g.brows : g.S;
-  float* __restrict__ hs = g.hs + (int64_t)b * g.S * g.D + 4 * P.col;
+  float* __restrict__ hs = g.hs + (int64_t)b * g.S * g.D + cs * cols + 4 * P.col;
   float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
   if (P.p < P.np) {
     for (int r = r0 + P.p; r < r1; r += R * P.np) {
@@ -414,35 +418,39 @@ __device__ __forceinline__ void block_total_hs(const MArgs& g, int b, int blk, f
   __syncthreads();
   if (P.p == 0) {
     for (int q = 1; q < P.np; ++q) add4(a, part[q * P.cpt + P.col]);
-    *reinterpret_cast<float4*>(g.tot + ((int64_t)b * g.nblk + blk) * g.D + 4 * P.col) = a;
+    *reinterpret_cast<float4*>(g.tot + ((int64_t)b * g.nblk + blk) * g.D + cs * cols + 4 * P.col) = a;
   }
 }
 
-// Totals of block blk (g.brows rows) of batch b over rows and head groups.
-__device__ __forceinline__ void block_total(const MArgs& g, int b, int blk) {
+// Totals of block blk (g.brows rows) of batch b over rows and head groups,
+// columns of slice cs (D >> bsplit_sh wide).
+__device__ __forceinline__ void block_total(const MArgs& g, int b, int blk, int cs) {
   extern __shared__ __align__(16) uint8_t smem[];
   float4* part = reinterpret_cast<float4*>(smem);
   switch (g.hsplit) {                     // 1..8 (kMaxHeadSplit)
-    case 1: block_total_hs<1>(g, b, blk, part); break;
-    case 2: block_total_hs<2>(g, b, blk, part); break;
-    case 3: block_total_hs<3>(g, b, blk, part); break;
-    case 4: block_total_hs<4>(g, b, blk, part); break;
-    case 5: block_total_hs<5>(g, b, blk, part); break;
-    case 6: block_total_hs<6>(g, b, blk, part); break;
-    case 7: block_total_hs<7>(g, b, blk, part); break;
-    default: block_total_hs<8>(g, b, blk, part); break;
+    case 1: block_total_hs<1>(g, b, blk, cs, part); break;
+    case 2: block_total_hs<2>(g, b, blk, cs, part); break;
+    case 3: block_total_hs<3>(g, b, blk, cs, part); break;
+    case 4: block_total_hs<4>(g, b, blk, cs, part); break;
+    case 5: block_total_hs<5>(g, b, blk, cs, part); break;
+    case 6: block_total_hs<6>(g, b, blk, cs, part); break;
+    case 7: block_total_hs<7>(g, b, blk, cs, part); break;
+    default: block_total_hs<8>(g, b, blk, cs, part); break;
   }
 }
 
-// grid (nexact + nblk, B): x < nexact (H in the first column slice, else 0)
-// are the exact rows of head x, the rest block totals.  Uniform per
-// workgroup, so every barrier sees all its waves.
+// grid (nexact + (nblk << bsplit_sh), B): x < nexact (H in the first column
+// slice, else 0) are the exact rows of head x, the rest block totals,
+// 1 << bsplit_sh workgroups per block.  Uniform per workgroup, so every barrier sees all its
+// waves.
 __global__ void __launch_bounds__(kWide) mla_exact_rows_block_total(const MArgs g) {
   const int x = (int)blockIdx.x, b = (int)blockIdx.y;
-  if (x < g.nexact)
+  if (x < g.nexact) {
     exact_rows(g, b, x);
-  else
-    block_total(g, b, x - g.nexact);
+  } else {
+    const int y = x - g.nexact;
+    block_total(g, b, y >> g.bsplit_sh, y & ((1 << g.bsplit_sh) - 1));
+  }
 }
 
 // ------------------------------------------------------------------ K3
@@ -522,6 +530,7 @@ bool overlap(const void* a, int64_t na, const void* b, int64_t nb) {
 }
 
 constexpr int kMinK1Groups = 1024;        // K1 workgroups wanted (4 per CU)
+constexpr int64_t kCUs = 256;             // compute units of an MI355X
 constexpr int kMaxHeadSplit = 8;
 
 // Head groups for K1 when the row grid alone is small: doubles while the grid
@@ -532,6 +541,23 @@ int64_t head_split(int64_t B, int64_t S, int64_t D, int64_t H) {
   const int64_t base = ((S + rows_per_wg - 1) / rows_per_wg) * B;
   int64_t sp = 1;
   while (base * sp < kMinK1Groups && sp < kMaxHeadSplit && sp * 2 <= H) sp *= 2;
+  return sp;
+}
+
+// Workgroups per scan block for the block totals.  A block-total workgroup
+// reads brows rows of every head-group plane; from 256 KB up (short
+// sequences, where K1 splits the heads into many planes and there are few
+// blocks) that read sets K2's length, and the block is split into up to 4
+// column slices of at least 128 dims while K2's whole grid (B (nexact + nblk
+// split) workgroups) stays within one per CU.  Below it, or past one per CU,
+// splitting measured slower.
+int32_t block_split(int64_t B, int64_t nblk, int64_t brows, int64_t hsplit, int64_t nexact,
+                    int64_t ds) {
+  if (brows * hsplit * ds * 4 < (256 << 10)) return 1;
+  int32_t sp = 1;
+  while (sp < 4 && ds % (2 * sp * 64) == 0 && ds / (2 * sp) >= 128 &&
+         B * (nexact + nblk * 2 * sp) <= kCUs)
+    sp *= 2;
   return sp;
 }
 
@@ -650,6 +676,8 @@ int launch(const void* q, const void* c_kv, const void* out, const void* dout, c
     g.D = (int32_t)ds;
     g.ld = (int32_t)D;
     g.nexact = sl == 0 ? (int32_t)H : 0;
+    const int32_t bsplit = block_split(B, g.nblk, g.brows, g.hsplit, g.nexact, ds);
+    g.bsplit_sh = bsplit == 4 ? 2 : bsplit == 2 ? 1 : 0;
     g.erows = (int32_t)(S < kE ? S : kE);
     g.scale = sm_scale;
     g.dq_bf16 = dq_dtype == FAGQ_MLA_BF16;
@@ -666,9 +694,9 @@ int launch(const void* q, const void* c_kv, const void* out, const void* dout, c
                                        : reinterpret_cast<const void*>(&mla_stream_do<2, false>));
     hipError_t e = hipLaunchKernel(k1, k1_grid, dim3(kThreads), args, 0, st);
     if (e != hipSuccess) return -(int)e;
-    // nexact + nblk < 2^17 + 2^20: nblk <= S / 16 + 1 and H S D 4 < 2^32 with D >= 64.
+    // nexact + 4 nblk < 2^17 + 2^22: nblk <= S / 16 + 1 and H S D 4 < 2^32 with D >= 64.
     e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_exact_rows_block_total),
-                        dim3((unsigned)(g.nexact + g.nblk), (unsigned)B), dim3(kWide), args,
+                        dim3((unsigned)(g.nexact + g.nblk * bsplit), (unsigned)B), dim3(kWide), args,
                         k2_lds_bytes(D), st);
     if (e != hipSuccess) return -(int)e;
     e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_suffix_scan),
