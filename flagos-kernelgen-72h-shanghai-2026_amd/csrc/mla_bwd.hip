@@ -17,22 +17,23 @@
 //                        contiguous 4 KB (D = 512) segment per workgroup.
 //                        Short sequences split the heads into up to 8 groups,
 //                        each writing a partial head-sum plane.
-//   K2 mla_exact_rows_block_total - one launch of 1024-thread workgroups, two
+//   K2 mla_block_totals - per block of 16-64 rows (or column slice of one):
+//                        fp32 totals of hs / (i + 1) over rows and head-group
+//                        planes; each row's plane sum is written back over
+//                        plane 0.
+//   K3 mla_exact_rows_suffix_scan - one launch of 1024-thread workgroups, two
 //                        kinds:
 //                        * exact rows, one per (b, h): q, do and c rows 0..E-1
 //                          in LDS, the logits and dP by bf16 MFMAs with fp32
 //                          accumulation (one wave), P and dS rounded to bf16
 //                          where the reference rounds, dq rows 0..E-1 (which
 //                          K1 does not write);
-//                        * block totals, per block of 16-64 rows: fp32 totals
-//                          of hs / (i + 1) over rows and head-group planes;
-//                          each row's plane sum is written back over plane 0.
-//                        The exact rows depend on nothing K1 writes; sharing
-//                        the launch with the few block-total workgroups runs
-//                        them in the part of the chip those leave idle.
-//   K3 mla_suffix_scan - per block: carry = totals of all later blocks, then
-//                        the reverse running sum over the block's rows (plane
-//                        0), written as dc.
+//                        * per block: carry = totals of all later blocks, then
+//                          the reverse running sum over the block's rows
+//                          (plane 0), written as dc.
+//                        The exact rows depend on nothing K1 or K2 writes;
+//                        sharing the last launch with the few scan workgroups
+//                        runs them in the part of the chip those leave idle.
 // K2 and K3 issue each thread's loads as one batch: at these sizes they are
 // latency-bound: every dependent round trip to memory adds its full latency.
 //
@@ -40,7 +41,7 @@
 // block totals and K3 are per column, so each slice runs them on its columns
 // (the tensors' row stride stays D, the workspace holds one slice), and the
 // exact rows, whose dot products span all of D, run once over all columns in
-// the first slice's K2, staging the rows in chunks of kSliceD dims.
+// the first slice's K3, staging the rows in chunks of kSliceD dims.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -347,14 +348,12 @@ __device__ __forceinline__ void exact_rows(const MArgs& g, int b, int h) {
   }
 }
 
-// Dynamic LDS of K2: the exact rows' rows and dS, at least kWide float4 for
-// the block totals' join.
-size_t k2_lds_bytes(int64_t D) {
+// Dynamic LDS of K3: the exact rows' rows and dS.
+size_t exact_lds_bytes(int64_t D) {
   const int64_t W = D < kSliceD ? D : kSliceD;
-  const size_t ex = (size_t)3 * kE * (W + kPadElems) * 2 + (size_t)(kE * kE + kE) * 4;
-  const size_t bt = (size_t)kWide * 16;
-  return ex > bt ? ex : bt;
+  return (size_t)3 * kE * (W + kPadElems) * 2 + (size_t)(kE * kE + kE) * 4;
 }
+constexpr size_t kBlockTotalLds = (size_t)kWide * 16;   // dynamic LDS of K2: the parts' join
 
 // ------------------------------------------------------------------ K2: block totals
 
@@ -439,34 +438,26 @@ __device__ __forceinline__ void block_total(const MArgs& g, int b, int blk, int 
   }
 }
 
-// grid (nexact + (nblk << bsplit_sh), B): x < nexact (H in the first column
-// slice, else 0) are the exact rows of head x, the rest block totals,
-// 1 << bsplit_sh workgroups per block.  Uniform per workgroup, so every barrier sees all its
-// waves.
-__global__ void __launch_bounds__(kWide) mla_exact_rows_block_total(const MArgs g) {
+// grid (nblk << bsplit_sh, B): 1 << bsplit_sh workgroups per block.
+__global__ void __launch_bounds__(kWide) mla_block_totals(const MArgs g) {
   const int x = (int)blockIdx.x, b = (int)blockIdx.y;
-  if (x < g.nexact) {
-    exact_rows(g, b, x);
-  } else {
-    const int y = x - g.nexact;
-    block_total(g, b, y >> g.bsplit_sh, y & ((1 << g.bsplit_sh) - 1));
-  }
+  block_total(g, b, x >> g.bsplit_sh, x & ((1 << g.bsplit_sh) - 1));
 }
 
 // ------------------------------------------------------------------ K3
 
 constexpr int kChunkRows = 8;             // >= ceil(64 / 8): rows per part of a block
 
-// grid (nblk, B).  The block's rows are np chunks of cr = ceil(brows / np)
-// rows (cr <= 8 since brows <= 64 and np >= 8); part p scans chunk p.  Part p
-// first sums (1) the totals of later blocks blk + 1 + p, blk + 1 + p + np, ...
-// and (2) the rows of its chunk (kept in registers); after one barrier its
-// carry is all parts' (1), in part order, plus the (2) of the chunks above
-// it, then the reverse running sum over the chunk is written as dc.
-__global__ void __launch_bounds__(kWide) mla_suffix_scan(const MArgs g) {
+// Block blk of batch b.  The block's rows are np chunks of cr = ceil(brows /
+// np) rows (cr <= 8 since brows <= 64 and np >= 8); part p scans chunk p.
+// Part p first sums (1) the totals of later blocks blk + 1 + p, blk + 1 + p +
+// np, ... and (2) the rows of its chunk (kept in registers); after one
+// barrier its carry is all parts' (1), in part order, plus the (2) of the
+// chunks above it, then the reverse running sum over the chunk is written as
+// dc.
+__device__ __forceinline__ void suffix_scan(const MArgs& g, int b, int blk) {
   __shared__ float4 later[kWide], chunk[kWide];
   const Parts P(g.D);
-  const int b = (int)blockIdx.y, blk = (int)blockIdx.x;
   const int r0 = blk * g.brows;
   const int r1 = r0 + g.brows < g.S ? r0 + g.brows : g.S;
   const int cr = (g.brows + P.np - 1) / P.np;
@@ -522,6 +513,17 @@ __global__ void __launch_bounds__(kWide) mla_suffix_scan(const MArgs g) {
   }
 }
 
+// grid (nexact + nblk, B): x < nexact (H in the first column slice, else 0)
+// are the exact rows of head x, the rest the scan of block x - nexact.
+// Uniform per workgroup, so every barrier sees all its waves.
+__global__ void __launch_bounds__(kWide) mla_exact_rows_suffix_scan(const MArgs g) {
+  const int x = (int)blockIdx.x, b = (int)blockIdx.y;
+  if (x < g.nexact)
+    exact_rows(g, b, x);
+  else
+    suffix_scan(g, b, x - g.nexact);
+}
+
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 bool overlap(const void* a, int64_t na, const void* b, int64_t nb) {
@@ -544,19 +546,18 @@ int64_t head_split(int64_t B, int64_t S, int64_t D, int64_t H) {
   return sp;
 }
 
-// Workgroups per scan block for the block totals.  A block-total workgroup
-// reads brows rows of every head-group plane; from 256 KB up (short
-// sequences, where K1 splits the heads into many planes and there are few
-// blocks) that read sets K2's length, and the block is split into up to 4
-// column slices of at least 128 dims while K2's whole grid (B (nexact + nblk
-// split) workgroups) stays within one per CU.  Below it, or past one per CU,
-// splitting measured slower.
-int32_t block_split(int64_t B, int64_t nblk, int64_t brows, int64_t hsplit, int64_t nexact,
-                    int64_t ds) {
-  if (brows * hsplit * ds * 4 < (256 << 10)) return 1;
+// Workgroups per scan block for the block totals.  Short sequences, where K1
+// splits the heads into several partial head-sum planes, leave few blocks
+// whose workgroups each read brows rows of every plane (and write the plane
+// sums back); from 128 KB per workgroup that read sets K2's length, and the
+// block is split into up to 4 column slices of at least 128 dims while K2's
+// grid (B nblk split workgroups) stays within one per CU.  Measured (B 2, H
+// 64, D 512): S 256 and 512 split 4 ways, 3-5 % faster per call; a split of
+// the single-plane S 4096 blocks (128 KB, 128 workgroups) 1 % slower.
+int32_t block_split(int64_t B, int64_t nblk, int64_t brows, int64_t hsplit, int64_t ds) {
+  if (hsplit < 2 || brows * hsplit * ds * 4 < (128 << 10)) return 1;
   int32_t sp = 1;
-  while (sp < 4 && ds % (2 * sp * 64) == 0 && ds / (2 * sp) >= 128 &&
-         B * (nexact + nblk * 2 * sp) <= kCUs)
+  while (sp < 4 && ds % (2 * sp * 64) == 0 && ds / (2 * sp) >= 128 && B * nblk * 2 * sp <= kCUs)
     sp *= 2;
   return sp;
 }
@@ -676,7 +677,7 @@ int launch(const void* q, const void* c_kv, const void* out, const void* dout, c
     g.D = (int32_t)ds;
     g.ld = (int32_t)D;
     g.nexact = sl == 0 ? (int32_t)H : 0;
-    const int32_t bsplit = block_split(B, g.nblk, g.brows, g.hsplit, g.nexact, ds);
+    const int32_t bsplit = block_split(B, g.nblk, g.brows, g.hsplit, ds);
     g.bsplit_sh = bsplit == 4 ? 2 : bsplit == 2 ? 1 : 0;
     g.erows = (int32_t)(S < kE ? S : kE);
     g.scale = sm_scale;
@@ -694,13 +695,15 @@ int launch(const void* q, const void* c_kv, const void* out, const void* dout, c
                                        : reinterpret_cast<const void*>(&mla_stream_do<2, false>));
     hipError_t e = hipLaunchKernel(k1, k1_grid, dim3(kThreads), args, 0, st);
     if (e != hipSuccess) return -(int)e;
-    // nexact + 4 nblk < 2^17 + 2^22: nblk <= S / 16 + 1 and H S D 4 < 2^32 with D >= 64.
-    e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_exact_rows_block_total),
-                        dim3((unsigned)(g.nexact + g.nblk * bsplit), (unsigned)B), dim3(kWide), args,
-                        k2_lds_bytes(D), st);
+    // 4 nblk < 2^22 and nexact + nblk < 2^17 + 2^20: nblk <= S / 16 + 1 and
+    // H S D 4 < 2^32 with D >= 64.
+    e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_block_totals),
+                        dim3((unsigned)(g.nblk * bsplit), (unsigned)B), dim3(kWide), args,
+                        kBlockTotalLds, st);
     if (e != hipSuccess) return -(int)e;
-    e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_suffix_scan),
-                        dim3((unsigned)g.nblk, (unsigned)B), dim3(kWide), args, 0, st);
+    e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_exact_rows_suffix_scan),
+                        dim3((unsigned)(g.nexact + g.nblk), (unsigned)B), dim3(kWide), args,
+                        g.nexact ? exact_lds_bytes(D) : 0, st);
     const int ls = launch_status(e);
     if (ls != FAGQ_OK) return ls;
   }
