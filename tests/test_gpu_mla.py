@@ -85,7 +85,8 @@ def case(pkg, dev, B, H, S, D, grad_dtype, dc_dtype=None, seed=0):
 
 
 @pytest.mark.parametrize("B,H,S,D", [(1, 4, 64, 512), (2, 3, 100, 64), (1, 2, 10, 128),
-                                     (1, 8, 257, 256), (2, 64, 256, 512), (1, 1, 1, 64)])
+                                     (1, 8, 257, 256), (2, 64, 256, 512), (2, 64, 512, 512),
+                                     (1, 1, 1, 64)])
 @pytest.mark.parametrize("grad", [torch.float32, torch.bfloat16])
 def test_mla_matches_oracle(pkg, gpu, B, H, S, D, grad):
     case(pkg, gpu, B, H, S, D, grad)
