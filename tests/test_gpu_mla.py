@@ -103,12 +103,13 @@ def test_mla_uneven_head_groups(pkg, gpu, B, H, S, D, dq_dtype):
 
 
 @pytest.mark.parametrize("B,H,S,D", [(1, 4, 40, 576), (2, 3, 10, 1024), (1, 6, 100, 640),
-                                     (1, 2, 300, 1152)])
+                                     (1, 2, 300, 1152), (2, 64, 256, 1024)])
 @pytest.mark.parametrize("dq_dtype", [torch.bfloat16, torch.float32])
 def test_mla_column_slices(pkg, gpu, B, H, S, D, dq_dtype):
-    # D above 512 runs in 512-wide column slices (the last one 64, 512, 128
-    # and 128 wide): the exact rows stage their rows in chunks and the other
-    # kernels run once per slice
+    # D above 512 runs in 512-wide column slices (the last one 64, 512, 128,
+    # 128 and 512 wide): the exact rows stage their rows in chunks and the
+    # other kernels run once per slice; the last case's slices each split the
+    # heads into 8 partial planes and the block totals into 4 column slices
     case(pkg, gpu, B, H, S, D, dq_dtype, seed=D + S)
 
 
