@@ -41,7 +41,9 @@ copy, read-only and write-only streams with the operator's cache policies
 (achievable bandwidth, counter calibration), and the GEMM's matrix instruction
 issued from registers (achievable MFMA rate).  --lds-probe times the LDS read
 patterns of fagq_diag_lds_read (run it under rocprofv3 --pmc for the bank
-conflicts of each).
+conflicts of each).  For a quantizer config, --rows-sweep times it over row
+counts and --route-sweep under each explicit launch mapping (fagq_launch_mapped)
+against the route table's choice.
 
 Usage: python bench.py [--steps K] [--warmup W] [--config NAME] [--gpus 1]
 """
@@ -180,6 +182,9 @@ def parse_args():
     p.add_argument("--rows-sweep", default="",
                    help="instead: comma-separated row counts; the config's operator at each, after "
                         "a warm-up of the device, with a least-squares line of time against bytes")
+    p.add_argument("--route-sweep", action="store_true",
+                   help="instead: the config's operator under each explicit launch mapping "
+                        "(fagq_launch_mapped), against the route table's own choice")
     return p.parse_args()
 
 
@@ -333,6 +338,8 @@ def main() -> int:
     w = CONFIGS[name]
     if args.rows_sweep:
         return rows_sweep(args, torch, pkg, w)
+    if args.route_sweep:
+        return route_sweep(args, torch, pkg, w)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     lib = pkg.load_library()
@@ -504,6 +511,97 @@ def rows_sweep(args, torch, pkg, w0) -> int:
         print(json.dumps({"fit": "t = t0 + bytes / bw", "points": n,
                           "t0_us": round(my - slope * mx, 2),
                           "bw_GBps": round(1.0 / slope / 1e3, 1)}), flush=True)
+    return 0
+
+
+def route_sweep(args, torch, pkg, w) -> int:
+    """The config's operator under explicit launch mappings (fagq_launch_mapped,
+    include/fagq_diag.h; every mapping gives the same bits), in one process: for
+    1-4 steps of 512 columns per wave, the waves per row that gives, times 1, 2
+    or 4 rows per workgroup (at most 16 waves) and each row-group mode that
+    applies, with the route's own XCD order and LDS reservation.  300 ms of
+    warm-up, then 3 interleaved rounds of K steps per mapping, one event pair
+    each; median.  One JSON line per mapping, fastest first; `route` marks the
+    route table's own choice (fagq_query_route), timed the same way."""
+    import ctypes
+    from fagq_mi355x import _lib
+    from fagq_mi355x.workloads import make_inputs
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    lib = pkg.load_library()
+    x, res, gamma = make_inputs(w)
+    nb = w.algorithmic_bytes()
+    nsets = max(2, min(64, math.ceil(ROTATE_BYTES / nb) + 1))
+    xd, rd, gd = x.to(dev), res.to(dev), gamma.to(dev)
+    sets = []
+    for i in range(nsets):
+        xs, rs = (xd, rd) if i == 0 else (xd.clone(), rd.clone())
+        sets.append((xs, rs, torch.empty_like(rs), torch.empty((w.M, w.D), dtype=w.out_dtype, device=dev),
+                     pkg.empty_scales(w.M, w.groups, ue8m0=w.scale_ue8m0, col_major=w.scale_col_major,
+                                      device=dev)))
+    qf = _lib.Q_INT8 if w.out_dtype == torch.int8 else _lib.Q_FP8_E4M3FN
+    sf = _lib.SCALE_UE8M0 if w.scale_ue8m0 else _lib.SCALE_F32
+    lay = _lib.LAYOUT_COL_MAJOR if w.scale_col_major else _lib.LAYOUT_ROW_MAJOR
+    rnd = _lib.ROUND_TRUNC if (w.out_dtype == torch.int8 and w.rounding == "trunc") else _lib.ROUND_RNE
+    route = pkg.route_for(w.M, w.D, w.group_size, scale_ue8m0=w.scale_ue8m0,
+                          scale_col_major=w.scale_col_major)
+    remap, lds = route["xcd_remap"], route["lds_bytes"]
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    st = ctypes.c_void_p(stream.cuda_stream)
+
+    def stepper(wpr, rpb, mode):
+        def step(i):
+            xs, rs, ro, q, sc = sets[i % nsets]
+            e = lib.fagq_launch_mapped(P(xs), P(rs), P(gd), P(ro), None, P(q), P(sc), w.M, w.D,
+                                       w.group_size, w.eps, qf, sf, lay, rnd, wpr, rpb, mode,
+                                       remap, lds, st)
+            if e:
+                raise RuntimeError(f"fagq_launch_mapped: status {e}")
+        return step
+
+    def route_step(i):
+        xs, rs, ro, q, sc = sets[i % nsets]
+        pkg.fused_add_rmsnorm_group_quant(xs, rs, gd, ro, None, q, sc, w.eps, w.group_size,
+                                          rounding=w.rounding if w.out_dtype == torch.int8 else None)
+
+    steps_total = -(-w.D // 512)
+    cands = [("route", route["waves_per_row"], route["rows_per_block"], route["row_group_mode"],
+              route_step)]
+    for ns in (1, 2, 3, 4):
+        wpr = -(-steps_total // ns)
+        if wpr > 16 or (ns > 1 and -(-steps_total // (ns - 1)) == wpr):
+            continue
+        for rpb in (1, 2, 4):
+            if wpr * rpb > 16:
+                continue
+            for mode in (0, 1, 2):
+                if mode >= 1 and wpr * ns > 16:
+                    continue
+                if mode == 2 and (not w.scale_col_major or rpb == 1):
+                    continue
+                step = stepper(wpr, rpb, mode)
+                try:
+                    step(0)
+                except RuntimeError:
+                    continue
+                cands.append(("mapped", wpr, rpb, mode, step))
+    torch.cuda.synchronize(dev)
+    heat(torch, dev, route_step, 300.0)
+    times = [[] for _ in cands]
+    for _ in range(3):
+        for k, c in enumerate(cands):
+            times[k].append(timed_region(torch, dev, stream, c[4], args.steps)[0])
+    rows = []
+    for (kind, wpr, rpb, mode, _), ts in zip(cands, times):
+        t = sorted(ts)[1] * 1e3
+        rows.append({"workload": w.name, "route": kind == "route", "waves_per_row": wpr,
+                     "steps_per_wave": -(-steps_total // wpr), "rows_per_block": rpb,
+                     "row_group_mode": mode, "xcd_remap": remap, "lds_bytes": lds,
+                     "us_per_call_median": round(t, 2),
+                     "pct_of_peak": round(100.0 * nb / (t * 1e-6) / 1e9 / PEAK_HBM_GBS, 2)})
+    for r in sorted(rows, key=lambda r: r["us_per_call_median"]):
+        print(json.dumps(r), flush=True)
     return 0
 
 
