@@ -311,8 +311,8 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g)
   // Ring: k-block kb reads slots (2 kb) % 5 and (2 kb + 1) % 5.  Its
   // iteration issues B(kb + 1), then kb + 1's scales, then A(kb + 2), into
   // the two slots the barrier ending k-block kb - 1 released; A(kb + 1) was
-  // issued one k-block earlier.  The counter being in order, the wait that
-  // ends the k-block for everything but the last COPY_A instructions leaves
+  // issued one k-block earlier.  The k-block ends with a wait for all but the
+  // last COPY_A memory instructions; the counter is in order, so that leaves
   // only A(kb + 2) in flight.  Past the last k-block the same instructions
   // fetch the last k-block again into slots nobody reads, so every iteration
   // issues and waits alike: no branch for the compiler to move the products

@@ -79,10 +79,10 @@ struct MArgs {
   int32_t hsplit;     // head groups K1 splits the heads into
   int32_t hps;        // heads per group
   int32_t H, S;
-  int32_t D;          // dims of this column slice (the width K1, K2's totals and K3 handle)
+  int32_t D;          // dims of this column slice (the width K1, K2 and K3's scan handle)
   int32_t ld;         // elements between rows of q, c, out, dout, dq and dc (the full D);
                       // their pointers point at the slice's first column
-  int32_t nexact;     // K2 workgroups (x < nexact) running exact rows: H in the first slice
+  int32_t nexact;     // K3 workgroups (x < nexact) running exact rows: H in the first slice
   int32_t erows;      // min(16, S)
   float scale;
   int32_t dq_bf16;    // dq is bf16 (else fp32)
@@ -217,7 +217,7 @@ __global__ void __launch_bounds__(kThreads) mla_stream_do(const MArgs g) {
   store_lane(rhs, false, wa, wb, o);
 }
 
-// ------------------------------------------------------------------ K2: exact rows
+// ------------------------------------------------------------------ K3: exact rows
 
 constexpr int kWide = 1024;               // threads of K2 and K3 (16 waves)
 
