@@ -755,10 +755,8 @@ FAGQ_API int fagq_dsa_topk_launch(const void* scores, int scores_dtype, const vo
       {FAGQ_DSA_K(true, false), FAGQ_DSA_K(true, true)}};
 #undef FAGQ_DSA_K
   void* args[] = {&g};
-  return launch_status(hipLaunchKernel(kernels[bf16][vec][kind],
-                                       dim3((unsigned)Q, (unsigned)H, (unsigned)B),
-                                       dim3((unsigned)(64 * waves)), args, 0,
-                                       static_cast<hipStream_t>(stream)));
+  return launch_kernel(kernels[bf16][vec][kind], dim3((unsigned)Q, (unsigned)H, (unsigned)B),
+                       dim3((unsigned)(64 * waves)), args, 0, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

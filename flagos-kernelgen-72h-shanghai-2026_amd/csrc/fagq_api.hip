@@ -121,19 +121,21 @@ int prefill_steps() {
 // or 32 (ue8m0) consecutive rows go to one XCD and leave its L2 as full
 // 32-byte writes (16 fp32 rows when a workgroup stores two rows' words at
 // once, measured best at 16384 x 7168); otherwise dispatch order.
-// FAGQ_XCD_REMAP overrides.
+// FAGQ_XCD_REMAP overrides with any valid remap (0, 1 or a power of two up
+// to 64); other values are ignored.
+bool valid_remap(int r) { return r == 0 || r == 1 || (r >= 2 && r <= 64 && (r & (r - 1)) == 0); }
+
 int remap_for(int scale_layout, int scale_format, int rpb, int mode) {
   static const int forced = [] {
     const char* s = std::getenv("FAGQ_XCD_REMAP");
-    return s ? std::atoi(s) : -1;
+    const int v = s ? std::atoi(s) : -1;
+    return valid_remap(v) ? v : -1;
   }();
   if (forced >= 0) return forced;
   if (scale_layout != FAGQ_LAYOUT_COL_MAJOR) return 0;
   const int rows = scale_format == FAGQ_SCALE_F32 ? (mode == RG_WIDE_SCALES ? 16 : 8) : 32;
   return rows / rpb > 1 ? rows / rpb : 0;
 }
-
-bool valid_remap(int r) { return r == 0 || r == 1 || (r >= 2 && r <= 64 && (r & (r - 1)) == 0); }
 
 int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
@@ -373,8 +375,8 @@ int launch_with(const Mapping& m, const void* x, const void* residual, const voi
             scale_format, scale_layout, remap);
   const LaunchFn fn = lookup(q_format, scale_format, rounding, lpg_index((int)G), m.ns,
                              norm_out != nullptr, m.mode);
-  return launch_status(fn(a, dim3((unsigned)m.grid), dim3((unsigned)m.block), (unsigned)m.lds,
-                          static_cast<hipStream_t>(stream)));
+  return fn(a, dim3((unsigned)m.grid), dim3((unsigned)m.block), (unsigned)m.lds,
+            static_cast<hipStream_t>(stream));
 }
 
 }  // namespace
@@ -459,8 +461,8 @@ FAGQ_API int fagq_launch_parts(const void* const* x_parts, int nparts, const voi
     a.xparts[p] = p < nparts ? static_cast<const uint16_t*>(x_parts[p]) : nullptr;
   const PartsLaunchFn fn =
       lookup_parts(q_format, scale_format, rounding, lpg_index((int)group_size), m.ns);
-  return launch_status(fn(a, dim3((unsigned)m.grid), dim3((unsigned)m.block), 0u,
-                          static_cast<hipStream_t>(stream)));
+  return fn(a, dim3((unsigned)m.grid), dim3((unsigned)m.block), 0u,
+            static_cast<hipStream_t>(stream));
 }
 
 FAGQ_API int fagq_query_route(int64_t M, int64_t D, int64_t group_size, int scale_format,
@@ -515,7 +517,7 @@ FAGQ_API int fagq_diag_encode(const float* in, void* out, int64_t n, int q_forma
        reinterpret_cast<const void*>(&fagq_encode<QF_I8_RNE, true>)},
       {reinterpret_cast<const void*>(&fagq_encode<QF_I8_TRUNC, false>),
        reinterpret_cast<const void*>(&fagq_encode<QF_I8_TRUNC, true>)}};
-  return launch_status(hipLaunchKernel(kernels[qf][clamp], grid, block, args, 0, s));
+  return launch_kernel(kernels[qf][clamp], grid, block, args, 0, s);
 }
 
 FAGQ_API int fagq_diag_stream(const void* src, void* dst, int64_t bytes, int mode,
@@ -537,8 +539,8 @@ FAGQ_API int fagq_diag_stream(const void* src, void* dst, int64_t bytes, int mod
                   : mode == FAGQ_STREAM_READ  ? reinterpret_cast<const void*>(&fagq_stream_read)
                   : mode == FAGQ_STREAM_WRITE ? reinterpret_cast<const void*>(&fagq_stream_write)
                                               : reinterpret_cast<const void*>(&fagq_stream_opmix);
-  return launch_status(hipLaunchKernel(k, dim3((unsigned)blocks), dim3(kStreamBlock), args, 0,
-                                       static_cast<hipStream_t>(stream)));
+  return launch_kernel(k, dim3((unsigned)blocks), dim3(kStreamBlock), args, 0,
+                       static_cast<hipStream_t>(stream));
 }
 
 FAGQ_API int fagq_diag_copy(const void* src, void* dst, int64_t bytes, void* stream) {

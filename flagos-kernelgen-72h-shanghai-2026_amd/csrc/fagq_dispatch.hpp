@@ -1,7 +1,7 @@
-// fagq_dispatch.hpp - launch lookups shared by the instantiation units and the
-// C ABI.  One lookup per (code format, scale format), indexed by the
-// lanes-per-group index, the steps per wave, whether norm_out is written and
-// the rows-in-sequence index.
+// fagq_dispatch.hpp - the library's one kernel-launch wrapper, and the launch
+// lookups shared by the instantiation units and the C ABI.  One lookup per
+// (code format, scale format), indexed by the lanes-per-group index, the steps
+// per wave, whether norm_out is written and the row-group mode.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -10,9 +10,9 @@
 
 namespace fagq {
 
-// (args, grid, block, dynamic LDS bytes, stream)
-using LaunchFn = hipError_t (*)(const KArgs&, dim3, dim3, unsigned, hipStream_t);
-using PartsLaunchFn = hipError_t (*)(const PArgs&, dim3, dim3, unsigned, hipStream_t);
+// (args, grid, block, dynamic LDS bytes, stream) -> launch_kernel's status
+using LaunchFn = int (*)(const KArgs&, dim3, dim3, unsigned, hipStream_t);
+using PartsLaunchFn = int (*)(const PArgs&, dim3, dim3, unsigned, hipStream_t);
 
 constexpr int kNumLpg = 3;      // lanes per group 8, 16, 32  <->  G = 64, 128, 256
 
@@ -25,15 +25,21 @@ constexpr int lpg_index(int group_size) {
 // FAGQ_E_DEVICE or -hipError_t.
 int device_check();
 
-// Status of a kernel launch: 0 (FAGQ_OK) or -hipError_t.  Built with
-// -DFAGQ_TEST_LAUNCH_FAILURE (a test build only, never the shipped library)
-// every launch reports hipErrorLaunchFailure instead, so that the CPU tests
-// can check how a launch failure propagates through the C ABI.
+// Every kernel launch of the library goes through launch_kernel; its status
+// is 0 (FAGQ_OK) or -hipError_t.  Built with -DFAGQ_TEST_LAUNCH_FAILURE (a
+// test build only, never the shipped library) it launches nothing and reports
+// hipErrorLaunchFailure, so that CPU tests can check how a launch failure
+// propagates through the C ABI without any kernel reaching a device.
+inline int launch_kernel(const void* fn, dim3 grid, dim3 block, void** args, size_t lds,
+                         hipStream_t stream) {
 #ifdef FAGQ_TEST_LAUNCH_FAILURE
-inline int launch_status(hipError_t) { return -(int)hipErrorLaunchFailure; }
+  (void)fn, (void)grid, (void)block, (void)args, (void)lds, (void)stream;
+  return -(int)hipErrorLaunchFailure;
 #else
-inline int launch_status(hipError_t e) { return e == hipSuccess ? 0 : -(int)e; }
+  const hipError_t e = hipLaunchKernel(fn, grid, block, args, lds, stream);
+  return e == hipSuccess ? 0 : -(int)e;
 #endif
+}
 
 // lookup_q<code>_s<scale>(lpg index, steps per wave in [1, 4], norm, row-group mode).
 LaunchFn lookup_q0_s0(int lpg_idx, int steps, bool norm, int mode);   // fp8, f32

@@ -517,10 +517,9 @@ int launch(const void* a_q, const void* a_scale, const void* b_q, const void* b_
   void* args[] = {&g};
   const void* kernel = bn == Layout192::BN ? kernel_for_layout<Layout192>(asf, bsf)
                                            : kernel_for_layout<Layout256>(asf, bsf);
-  const hipError_t e = hipLaunchKernel(kernel, dim3((unsigned)(g.m_tiles * g.n_tiles)),
-                                       dim3((unsigned)Layout256::THREADS), args, 0,
-                                       static_cast<hipStream_t>(stream));
-  return launch_status(e);
+  return launch_kernel(kernel, dim3((unsigned)(g.m_tiles * g.n_tiles)),
+                       dim3((unsigned)Layout256::THREADS), args, 0,
+                       static_cast<hipStream_t>(stream));
 }
 
 // Issue-rate probe of the GEMM's instruction: every wave keeps 8 independent
@@ -678,10 +677,8 @@ FAGQ_API int fagq_diag_lds_read(int32_t* out, int64_t blocks, int32_t iters, int
   if (dc != FAGQ_OK) return dc;
   int pt = pattern, it = iters;
   void* args[] = {&out, &pt, &it};
-  const hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&lds_probe_kernel),
-                                       dim3((unsigned)blocks), dim3(kLdsProbeThreads), args, 0,
-                                       static_cast<hipStream_t>(stream));
-  return launch_status(e);
+  return launch_kernel(reinterpret_cast<const void*>(&lds_probe_kernel), dim3((unsigned)blocks),
+                       dim3(kLdsProbeThreads), args, 0, static_cast<hipStream_t>(stream));
 }
 
 FAGQ_API int fagq_diag_mfma_rate(float* out, int64_t blocks, int32_t iters, int shape,
@@ -697,9 +694,8 @@ FAGQ_API int fagq_diag_mfma_rate(float* out, int64_t blocks, int32_t iters, int 
   void* args[] = {&out, &it};
   const void* k = shape == 0 ? reinterpret_cast<const void*>(&mfma_peak_kernel)
                              : reinterpret_cast<const void*>(&mfma_peak32_kernel);
-  const hipError_t e = hipLaunchKernel(k, dim3((unsigned)blocks), dim3(kPeakThreads), args, 0,
-                                       static_cast<hipStream_t>(stream));
-  return launch_status(e);
+  return launch_kernel(k, dim3((unsigned)blocks), dim3(kPeakThreads), args, 0,
+                       static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

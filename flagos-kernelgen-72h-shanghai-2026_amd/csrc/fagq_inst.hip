@@ -20,18 +20,18 @@ namespace fagq {
 namespace {
 
 template <int NS, int LPG, bool NORM, int MODE>
-hipError_t launch_rows(const KArgs& a, dim3 grid, dim3 block, unsigned lds, hipStream_t stream) {
+int launch_rows(const KArgs& a, dim3 grid, dim3 block, unsigned lds, hipStream_t stream) {
   void* args[] = {const_cast<KArgs*>(&a)};
-  return hipLaunchKernel(
+  return launch_kernel(
       reinterpret_cast<const void*>(&fagq_rows<NS, LPG, FAGQ_QF, FAGQ_SF, NORM, MODE>), grid,
       block, args, lds, stream);
 }
 
 template <int NS, int LPG>
-hipError_t launch_rows_parts(const PArgs& a, dim3 grid, dim3 block, unsigned lds,
-                             hipStream_t stream) {
+int launch_rows_parts(const PArgs& a, dim3 grid, dim3 block, unsigned lds,
+                      hipStream_t stream) {
   void* args[] = {const_cast<PArgs*>(&a)};
-  return hipLaunchKernel(
+  return launch_kernel(
       reinterpret_cast<const void*>(&fagq_rows_parts<NS, LPG, FAGQ_QF, FAGQ_SF>), grid, block,
       args, lds, stream);
 }

@@ -100,10 +100,13 @@ struct KArgs {
   __host__ __device__ int remap_shift() const { return (int)((cfg >> 17) & 7u); }
   __host__ __device__ int col_major() const { return (int)((cfg >> 20) & 1u); }
   __host__ __device__ int wide_ok() const { return (int)((cfg >> 21) & 1u); }
+  // Each field is masked to its width, so an out-of-range value cannot reach
+  // the neighbouring fields (the host passes only validated values).
   __host__ __device__ static uint32_t pack_cfg(int wpr, int rpb, int remap, int remap_shift,
                                                int col_major, int wide_ok) {
-    return (uint32_t)wpr | ((uint32_t)rpb << 5) | ((uint32_t)remap << 10) |
-           ((uint32_t)remap_shift << 17) | ((uint32_t)col_major << 20) | ((uint32_t)wide_ok << 21);
+    return ((uint32_t)wpr & 31u) | (((uint32_t)rpb & 31u) << 5) |
+           (((uint32_t)remap & 127u) << 10) | (((uint32_t)remap_shift & 7u) << 17) |
+           (((uint32_t)col_major & 1u) << 20) | (((uint32_t)wide_ok & 1u) << 21);
   }
 };
 static_assert(sizeof(KArgs) == 80, "kernel argument size");

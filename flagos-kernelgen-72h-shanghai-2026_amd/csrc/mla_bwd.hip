@@ -124,6 +124,10 @@ template <int U, bool HALVES>
 __global__ void __launch_bounds__(kThreads) mla_stream_do(const MArgs g) {
   const int lpr = g.D / 8;                        // lanes per row
   const int t = threadIdx.x;
+  // When lpr does not divide kThreads, the last kThreads % lpr threads hold
+  // no whole row of this workgroup (their t / lpr would be the next
+  // workgroup's first row), and stop here.
+  if (t / lpr >= kThreads / lpr) return;
   const int row = (int)blockIdx.x * (kThreads / lpr) + t / lpr;
   if (row >= g.S) return;
   const int b = (int)blockIdx.y;
@@ -693,18 +697,17 @@ int launch(const void* q, const void* c_kv, const void* out, const void* dout, c
                                        : reinterpret_cast<const void*>(&mla_stream_do<2, true>))
                             : (k1_wide ? reinterpret_cast<const void*>(&mla_stream_do<8, false>)
                                        : reinterpret_cast<const void*>(&mla_stream_do<2, false>));
-    hipError_t e = hipLaunchKernel(k1, k1_grid, dim3(kThreads), args, 0, st);
-    if (e != hipSuccess) return -(int)e;
+    int ls = launch_kernel(k1, k1_grid, dim3(kThreads), args, 0, st);
+    if (ls != FAGQ_OK) return ls;
     // 4 nblk < 2^22 and nexact + nblk < 2^17 + 2^20: nblk <= S / 16 + 1 and
     // H S D 4 < 2^32 with D >= 64.
-    e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_block_totals),
-                        dim3((unsigned)(g.nblk * bsplit), (unsigned)B), dim3(kWide), args,
-                        kBlockTotalLds, st);
-    if (e != hipSuccess) return -(int)e;
-    e = hipLaunchKernel(reinterpret_cast<const void*>(&mla_exact_rows_suffix_scan),
-                        dim3((unsigned)(g.nexact + g.nblk), (unsigned)B), dim3(kWide), args,
-                        g.nexact ? exact_lds_bytes(D) : 0, st);
-    const int ls = launch_status(e);
+    ls = launch_kernel(reinterpret_cast<const void*>(&mla_block_totals),
+                       dim3((unsigned)(g.nblk * bsplit), (unsigned)B), dim3(kWide), args,
+                       kBlockTotalLds, st);
+    if (ls != FAGQ_OK) return ls;
+    ls = launch_kernel(reinterpret_cast<const void*>(&mla_exact_rows_suffix_scan),
+                       dim3((unsigned)(g.nexact + g.nblk), (unsigned)B), dim3(kWide), args,
+                       g.nexact ? exact_lds_bytes(D) : 0, st);
     if (ls != FAGQ_OK) return ls;
   }
   return FAGQ_OK;

@@ -1,10 +1,14 @@
-"""A kernel launch that fails is reported, not swallowed (failure
-detection).  The library is rebuilt with -DFAGQ_TEST_LAUNCH_FAILURE, a test
-seam that makes every launch report hipErrorLaunchFailure (719) and skips the
-device check, so the whole path runs on a machine without a GPU: every entry
-point must return -719 after validation passes, keep its validation errors
-and no-op cases unchanged, and the Python layer must raise FagqError naming a
-HIP error."""
+"""A kernel launch that fails is reported, not swallowed (failure detection).
+The library is rebuilt with -DFAGQ_TEST_LAUNCH_FAILURE, a test seam in which
+the library's one launch wrapper launches nothing and reports
+hipErrorLaunchFailure (719), and the device check is skipped, so the whole
+path runs on a machine without a GPU: every entry point must return -719
+after validation passes, keep its validation errors and no-op cases
+unchanged, and the Python layer must raise FagqError naming a HIP error.
+
+The calls pass made-up device addresses.  The seam build cannot launch a
+kernel, and the module is skipped wherever a GPU is visible all the same, so
+these tests only ever run on a CPU-only host."""
 import ctypes
 import shutil
 
@@ -20,6 +24,9 @@ def fake(i):
 
 @pytest.fixture(scope="module")
 def seam(pkg):
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("made-up device addresses: CPU-only hosts run this module")
     if not shutil.which("hipcc") and not __import__("os").path.exists("/opt/rocm/bin/hipcc"):
         pytest.skip("hipcc not available")
     import __graft_entry__ as ge
@@ -54,6 +61,28 @@ def test_every_launching_entry_point_reports_it(seam):
     st = seam.fagq_gemm_launch(fake(0), fake(1), fake(2), fake(3), fake(4), 256, 256, 1024, 0, 1, 0,
                                None)
     assert st == -HIP_ERROR_LAUNCH_FAILURE
+    # MLA backward: the first of its three launches fails and the call stops there.
+    B, H, S, D = 1, 4, 256, 512
+    need = seam.fagq_mla_bwd_workspace_bytes(B, S, D)
+    assert need > 0
+    st = seam.fagq_mla_bwd_launch(fake(0), fake(1), fake(2), fake(3), fake(4), fake(5), fake(6),
+                                  fake(7), need, B, H, S, D, 0.05, 1, 1, None)
+    assert st == -HIP_ERROR_LAUNCH_FAILURE
+    # The allocation-free form looks up its array's device address first; on
+    # a host without a GPU that runtime call's error is what comes back.
+    st = seam.fagq_mla_bwd_launch_noalloc(fake(0), fake(1), fake(2), fake(3), fake(4), fake(5),
+                                          fake(6), B, H, S, D, 0.05, 1, 1, None)
+    assert st < 0
+
+
+def test_noalloc_refuses_calls_beyond_its_array(seam):
+    # The allocation-free MLA entry point refuses a call whose workspace would
+    # not fit its 32 MiB per-GPU array, before any device work.
+    B, S, D = 8, 4096, 512
+    assert seam.fagq_mla_bwd_workspace_bytes(B, S, D) > 32 << 20
+    st = seam.fagq_mla_bwd_launch_noalloc(fake(0), fake(1), fake(2), fake(3), fake(4), fake(5),
+                                          fake(6), B, 4, S, D, 0.05, 0, 0, None)
+    assert st == 7    # FAGQ_E_TOO_LARGE
 
 
 def test_python_layer_raises_on_it(seam):
