@@ -30,7 +30,8 @@
 //   2. An LDS histogram of the bins; its suffix sums above(b) (blocks in
 //      higher bins) give the boundary bin b* holding the top_k-th block.
 //      The candidates are the blocks of bins >= b*: found = above(b*) of them
-//      are certainly selected, and all of them fit in CAP = 512.
+//      are certainly selected, and all of them fit in CAP (512 for top_k
+//      <= 256, 2048 for larger top_k up to 1024; CAP >= top_k always).
 //   3. Counting sort: a candidate is stored at its bin's cursor, which starts
 //      at above(bin), so each bin owns one segment of the candidate array,
 //      bins in descending order.  A candidate's rank is above(bin) plus the
@@ -41,7 +42,8 @@
 //   If the boundary bin leaves more than CAP candidates (ties, outliers that
 //   stretch the range), a refinement finds a threshold on the composite key
 //   by 8-bit radix passes over the key range that remains, and the rank is
-//   then counted over all candidates.
+//   then counted over all candidates.  Composite keys are distinct, so the
+//   passes end with at most top_k <= CAP keys at or above the threshold.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -57,8 +59,12 @@ constexpr int kEPL = 16;                    // scores per lane
 constexpr int kChunk = 64 * kEPL;            // blocks per wave chunk
 constexpr int kMaxWaves = 16;                // waves per row (NB <= 16384 in one chunk each)
 constexpr int kBins = 256;
-constexpr uint32_t kCap = 512;               // candidates held at most
+// Candidates held at most: kCapSmall for top_k <= kSmallTopK, else kCapLarge.
+constexpr uint32_t kCapSmall = 512;
+constexpr uint32_t kCapLarge = 2048;
+constexpr int kSmallTopK = 256;
 constexpr int kMaxTopK = FAGQ_DSA_MAX_TOP_K;
+static_assert(kMaxTopK <= (int)kCapLarge && kSmallTopK <= (int)kCapSmall, "top_k fits CAP");
 constexpr int64_t kMaxGridYZ = 65535;        // H and B are grid dimensions y and z
 
 struct DArgs {
@@ -82,11 +88,12 @@ __device__ __forceinline__ uint32_t div_bs(const DArgs& g, uint32_t n) {
   return (t + ((n - t) >> g.bs_sh1)) >> g.bs_sh2;
 }
 
+template <uint32_t CAP>
 struct Lds {
   uint32_t hist[kBins + 64];        // bin counts, then one discard word per lane
   uint32_t above[kBins];            // 8 x candidates in higher bins: cand byte offsets, then
                                     // the scatter's per-bin cursors
-  uint64_t cand[kCap + 4];           // 4 spare entries: the rank loop reads in fours
+  uint64_t cand[CAP + 4];           // 4 spare entries: the rank loop reads in fours
   uint32_t kslot[kMaxWaves][2];     // per-wave max / min (ord_key)
   uint32_t uslot[2][kMaxWaves][4];  // per-wave partials of the refinement
   uint32_t ncur;                    // refinement scatter cursor
@@ -234,8 +241,8 @@ __device__ __forceinline__ int elem_off(int e) {
 struct Boundary {
   uint32_t bin, above, cnt, total;
 };
-template <bool STORE>
-__device__ __forceinline__ Boundary find_boundary(Lds& lds, uint32_t k, int lane,
+template <bool STORE, class L>
+__device__ __forceinline__ Boundary find_boundary(L& lds, uint32_t k, int lane,
                                                   bool store = false) {
   u32x4 h = reinterpret_cast<const u32x4*>(lds.hist)[lane];   // bins 4 lane .. 4 lane + 3
   if (STORE && lane == 0) h[0] = 0u;     // fp32 bins: bin 0 counts non-selectable blocks
@@ -356,12 +363,12 @@ __device__ __forceinline__ void chunk_scores(const u32x4 (&raw)[kEPL / (BF16 ? 8
 enum RowKind { kSmallRows = 0, kRows = 1, kLongRows = 2 };
 constexpr int kSmallWaves = 4;
 
-template <bool BF16, bool VECLD, int KIND>
+template <bool BF16, bool VECLD, int KIND, uint32_t CAP>
 __global__ void __launch_bounds__(KIND == kSmallRows ? 64 * kSmallWaves : 64 * kMaxWaves)
 dsa_topk_rows(const DArgs g) {
   constexpr bool MULTI = KIND == kLongRows;
   constexpr int VEC = BF16 ? 8 : 4;
-  __shared__ Lds lds;
+  __shared__ Lds<CAP> lds;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // Grid (Q, H, B): row = (b * H + h) * Q + q.
@@ -504,7 +511,7 @@ dsa_topk_rows(const DArgs g) {
 
   const Boundary bd = find_boundary<true>(lds, (uint32_t)K, lane, w == 0);
   uint32_t nc = bd.total ? bd.above + bd.cnt : 0u;
-  const bool refine = nc > kCap;
+  const bool refine = nc > CAP;
 
   if (!refine) {
     // Counting-sort scatter of the blocks in bins >= b* (b* >= 1, so bin 0,
@@ -609,7 +616,7 @@ dsa_topk_rows(const DArgs g) {
       __syncthreads();
       const Boundary r = find_boundary<false>(lds, need, lane);
       thr = (base + r.bin) << shift;
-      if (found + r.above + r.cnt <= kCap) {
+      if (found + r.above + r.cnt <= CAP) {
         nc = found + r.above + r.cnt;
         break;
       }
@@ -626,7 +633,7 @@ dsa_topk_rows(const DArgs g) {
       if (c >= thr) {
         const uint32_t p =
             __hip_atomic_fetch_add(&lds.ncur, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if (p < kCap) lds.cand[p] = c;
+        if (p < CAP) lds.cand[p] = c;
       }
     });
   }
@@ -659,7 +666,7 @@ dsa_topk_rows(const DArgs g) {
     st = st < nc ? st : nc;
     const uint32_t end = len < nc - st ? st + len : nc;
     uint32_t r = st;
-    for (uint32_t j = st; j < end; j += 4) {     // reads stay inside cand[kCap + 4]
+    for (uint32_t j = st; j < end; j += 4) {     // reads stay inside cand[CAP + 4]
       const uint64_t c0 = lds.cand[j], c1 = lds.cand[j + 1], c2 = lds.cand[j + 2], c3 = lds.cand[j + 3];
       r += (c0 > mine ? 1u : 0u) + (j + 1 < end && c1 > mine ? 1u : 0u) +
            (j + 2 < end && c2 > mine ? 1u : 0u) + (j + 3 < end && c3 > mine ? 1u : 0u);
@@ -747,15 +754,19 @@ FAGQ_API int fagq_dsa_topk_launch(const void* scores, int scores_dtype, const vo
   const int bf16 = scores_dtype == FAGQ_DSA_BF16;
   const int vec = aligned(scores, 16) && (NB * esz) % 16 == 0;
   const int kind = chunks > kMaxWaves ? kLongRows : chunks > kSmallWaves ? kRows : kSmallRows;
+  const int large = top_k > kSmallTopK;
+#define FAGQ_DSA_C(B, V, KIND) \
+  {(const void*)&dsa_topk_rows<B, V, KIND, kCapSmall>, \
+   (const void*)&dsa_topk_rows<B, V, KIND, kCapLarge>}
 #define FAGQ_DSA_K(B, V) \
-  {(const void*)&dsa_topk_rows<B, V, kSmallRows>, (const void*)&dsa_topk_rows<B, V, kRows>, \
-   (const void*)&dsa_topk_rows<B, V, kLongRows>}
-  static const void* const kernels[2][2][3] = {
+  {FAGQ_DSA_C(B, V, kSmallRows), FAGQ_DSA_C(B, V, kRows), FAGQ_DSA_C(B, V, kLongRows)}
+  static const void* const kernels[2][2][3][2] = {
       {FAGQ_DSA_K(false, false), FAGQ_DSA_K(false, true)},
       {FAGQ_DSA_K(true, false), FAGQ_DSA_K(true, true)}};
 #undef FAGQ_DSA_K
+#undef FAGQ_DSA_C
   void* args[] = {&g};
-  return launch_kernel(kernels[bf16][vec][kind], dim3((unsigned)Q, (unsigned)H, (unsigned)B),
+  return launch_kernel(kernels[bf16][vec][kind][large], dim3((unsigned)Q, (unsigned)H, (unsigned)B),
                        dim3((unsigned)(64 * waves)), args, 0, static_cast<hipStream_t>(stream));
 }
 

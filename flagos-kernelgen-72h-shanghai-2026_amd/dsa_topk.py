@@ -20,7 +20,7 @@ from . import _lib
 
 DSA_F32, DSA_BF16 = 0, 1
 DSA_I32, DSA_I64 = 0, 1
-MAX_NB, MAX_TOP_K = 1 << 28, 256
+MAX_NB, MAX_TOP_K = 1 << 28, 1024
 
 
 def dsa_topk_page_table_transform(scores: torch.Tensor, page_table: torch.Tensor,

@@ -235,7 +235,10 @@ DSA_CONFIGS = dict(_dsa(*c) for c in [
 DSA_CONFIGS.update(dict([_dsa(2, 32, 512, 4096, 128, 64, torch.bfloat16),
                          # all rows valid: the worst-case traffic R (4 NB + 12 K) bytes
                          # (reports/task02_dsa_topk_page_table_transform.md:33-36)
-                         _dsa(2, 32, 512, 4096, 128, 64, full_rows=True)]))
+                         _dsa(2, 32, 512, 4096, 128, 64, full_rows=True),
+                         # top_k past 256: the reference's power-of-two top_k up to its
+                         # 1024-block chunk (task02.py:913-945, :1712-1725)
+                         _dsa(2, 32, 512, 4096, 512, 64), _dsa(2, 32, 512, 4096, 1024, 64)]))
 DSA_HEADLINE = "dsa_f32_b2h32q512_nb4096_k128_bs64"
 
 

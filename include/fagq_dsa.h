@@ -31,7 +31,7 @@ extern "C" {
 #endif
 
 #define FAGQ_DSA_MAX_NB (1 << 28)
-#define FAGQ_DSA_MAX_TOP_K 256
+#define FAGQ_DSA_MAX_TOP_K 1024
 
 enum fagq_dsa_scores { FAGQ_DSA_F32 = 0, FAGQ_DSA_BF16 = 1 };
 enum fagq_dsa_index { FAGQ_DSA_I32 = 0, FAGQ_DSA_I64 = 1 };

@@ -359,7 +359,7 @@ def dsa_call(lib, **kw):
     (dict(ob=None), 1), (dict(op=None), 1),
     (dict(sd=2), 5), (dict(idx=-1), 5),
     (dict(B=-1), 2), (dict(NB=0), 2), (dict(bs=0), 2), (dict(k=0), 2),
-    (dict(NB=(1 << 28) + 1), 7), (dict(k=257), 7), (dict(bs=1 << 31), 7),
+    (dict(NB=(1 << 28) + 1), 7), (dict(k=1025), 7), (dict(bs=1 << 31), 7),
     (dict(H=65536), 7), (dict(B=65536), 7),
     (dict(Q=1 << 26), 7),                          # Q x 64 work-items (1 wave) reach 2^32
     (dict(Q=1 << 22, NB=16384, B=1, H=1), 7),      # Q x 64 x 16 waves reach 2^32

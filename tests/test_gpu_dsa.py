@@ -184,3 +184,34 @@ def test_dsa_scores_not_16_byte_aligned(pkg, gpu, dtype, offset):
     s_np = s.view(torch.uint16).numpy() if dtype == torch.bfloat16 else s.numpy()
     rb, rp = oracle.dsa_topk(s_np, pt.numpy(), pos.numpy(), kv.numpy(), 16, 64)
     assert np.array_equal(ob.cpu().numpy(), rb) and np.array_equal(op.cpu().numpy(), rp)
+
+
+# top_k past 256 (the reference's power-of-two top_k up to its 1024-block chunk width,
+# task02.py:913-945 and :1712-1725) takes the kernel with the larger candidate array;
+# 257 is the first such top_k, 256 the last of the smaller one.
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("NB,k", [(1024, 512), (1024, 1024), (4096, 512), (4096, 1024),
+                                  (8192, 512), (8192, 1024), (4096, 256), (4096, 257),
+                                  (2000, 1000)])
+def test_dsa_large_top_k(pkg, gpu, dtype, NB, k):
+    s, pt, pos, kv = case(NB + k, B=2, H=2, Q=16, NB=NB, bs=16, dtype=dtype)
+    check(pkg, gpu, s, pt, pos, kv, 16, k, f"large_k NB={NB} k={k}")
+
+
+@pytest.mark.parametrize("ties", ["round", "heavy", "equal", "outlier", "cluster"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("NB,k", [(4096, 1024), (8192, 512)])
+def test_dsa_large_top_k_ties(pkg, gpu, ties, dtype, NB, k):
+    s, pt, pos, kv = case(7 * NB + k, B=1, H=2, Q=12, NB=NB, bs=16, dtype=dtype, ties=ties)
+    check(pkg, gpu, s, pt, pos, kv, 16, k, f"large_k ties={ties} NB={NB} k={k}")
+
+
+def test_dsa_large_top_k_all_rows_valid(pkg, gpu):
+    # Every row sees the whole NB-block prefix: exactly top_k of NB selected.
+    g = torch.Generator().manual_seed(11)
+    B, H, Q, NB, bs, k = 1, 4, 32, 4096, 64, 1024
+    s = torch.randn(B, H, Q, NB, generator=g)
+    pt = torch.randint(0, 1 << 24, (B, NB), generator=g).to(torch.int32)
+    pos = torch.full((B, Q), NB * bs - 1, dtype=torch.int32)
+    kv = torch.full((B,), NB * bs, dtype=torch.int32)
+    check(pkg, gpu, s, pt, pos, kv, bs, k, "large_k all rows valid")
