@@ -74,12 +74,13 @@ enum fagq_rounding {
 enum fagq_status {
   FAGQ_OK = 0,
   FAGQ_E_NULL = 1,          /* a required pointer is NULL */
-  FAGQ_E_SHAPE = 2,         /* M < 0, D <= 0, D % group_size != 0, D % 8 != 0 */
+  FAGQ_E_SHAPE = 2,         /* M < 0, D <= 0 or D % group_size != 0 (so D % 64 == 0) */
   FAGQ_E_GROUP = 3,         /* group_size not in {64, 128, 256} */
   FAGQ_E_ALIGN = 4,         /* a pointer is not aligned as required */
   FAGQ_E_FORMAT = 5,        /* unknown enum value or unsupported combination */
   FAGQ_E_EPS = 6,           /* eps negative or not finite */
-  FAGQ_E_TOO_LARGE = 7,     /* D > FAGQ_MAX_D or M * D overflows int64 */
+  FAGQ_E_TOO_LARGE = 7,     /* D > FAGQ_MAX_D, M > INT32_MAX, or column-major scales
+                               past 2^32 - 16 bytes */
   FAGQ_E_DEVICE = 8,        /* current device is not gfx950 */
   FAGQ_E_ALIAS = 9          /* an output overlaps an input it must not overlap */
 };
