@@ -335,7 +335,8 @@ def main() -> int:
         return gemm_bench(args, torch, pkg, GEMM_CONFIGS[name])
     if name in PARTS_CONFIGS:
         return parts_bench(args, torch, pkg, PARTS_CONFIGS[name])
-    w = CONFIGS[name]
+    from fagq_mi355x.workloads import TYPED_CONFIGS
+    w = CONFIGS[name] if name in CONFIGS else TYPED_CONFIGS[name]
     if args.rows_sweep:
         return rows_sweep(args, torch, pkg, w)
     if args.route_sweep:
@@ -428,7 +429,9 @@ def main() -> int:
                    "q": str(w.out_dtype).replace("torch.", ""),
                    "scale": ("ue8m0" if w.scale_ue8m0 else "f32") +
                             (" col-major" if w.scale_col_major else " row-major"),
-                   "inputs": w.dist, "algorithmic_bytes": set_bytes, "buffer_sets": nsets,
+                   "inputs": w.dist, "x_dtype": str(w.act).replace("torch.", ""),
+                   "residual_dtype": str(w.res).replace("torch.", ""),
+                   "algorithmic_bytes": set_bytes, "buffer_sets": nsets,
                    "route": route},
         "us_per_call": round(kern_ms * 1e3, 2),
         "us_per_call_host_wall": round(wall_ms * 1e3, 2),

@@ -22,6 +22,7 @@ Q_INT8, Q_FP8_E4M3FN = 0, 1
 SCALE_F32, SCALE_UE8M0 = 0, 1
 LAYOUT_ROW_MAJOR, LAYOUT_COL_MAJOR = 0, 1
 ROUND_RNE, ROUND_TRUNC = 0, 1
+DT_BF16, DT_F16, DT_F32 = 0, 1, 2
 MAX_D = 32768
 MAX_PARTS, MAX_D_PARTS = 8, 16384
 MODE_INDEPENDENT, MODE_SHARED_GAMMA, MODE_WIDE_SCALES = 0, 1, 2
@@ -53,6 +54,7 @@ class GemmRoute(ctypes.Structure):
 
 SIGNATURES = {
     "fagq_launch": ([_P] * 7 + [_I64, _I64, _I64, _F, _I, _I, _I, _I, _P], _I),
+    "fagq_launch_typed": ([_P] * 7 + [_I64, _I64, _I64, _F, _I, _I, _I, _I, _I, _I, _P], _I),
     "fagq_launch_parts": ([_P, _I] + [_P] * 5 + [_I64, _I64, _I64, _F, _I, _I, _I, _I, _P], _I),
     "fagq_launch_mapped": ([_P] * 7 + [_I64, _I64, _I64, _F] + [_I] * 9 + [_P], _I),
     "fagq_query_route": ([_I64, _I64, _I64, _I, _I, ctypes.POINTER(Route)], _I),
@@ -127,7 +129,8 @@ def fast_launch():
         if not _fast_tried:
             try:
                 from . import _fagq_py
-                _fagq_py.bind(ctypes.cast(lib.fagq_launch, ctypes.c_void_p).value)
+                _fagq_py.bind(ctypes.cast(lib.fagq_launch, ctypes.c_void_p).value,
+                              ctypes.cast(lib.fagq_launch_typed, ctypes.c_void_p).value)
                 _fast = _fagq_py.launch
             except ImportError:
                 _fast = None

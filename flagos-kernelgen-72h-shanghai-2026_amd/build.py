@@ -98,6 +98,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     for q, s in INST_COMBOS:
         units.append((CSRC / "fagq_inst.hip", OBJ_DIR / f"fagq_inst_q{q}_s{s}.o",
                       [f"-DFAGQ_QF={q}", f"-DFAGQ_SF={s}"]))
+        units.append((CSRC / "fagq_inst_typed.hip", OBJ_DIR / f"fagq_inst_typed_q{q}_s{s}.o",
+                      [f"-DFAGQ_QF={q}", f"-DFAGQ_SF={s}"]))
     units.append((CSRC / "fagq_api.hip", OBJ_DIR / "fagq_api.o", []))
     units.append((CSRC / "fagq_gemm.hip", OBJ_DIR / "fagq_gemm.o", []))
     units.append((CSRC / "dsa_topk.hip", OBJ_DIR / "dsa_topk.o", []))
@@ -144,6 +146,8 @@ def build_variant(name: str, *, defines: tuple[str, ...] = (), sanitize: bool = 
     units: list[tuple[Path, Path, list[str]]] = []
     for q, sf in INST_COMBOS:
         units.append((CSRC / "fagq_inst.hip", out_dir / f"fagq_inst_q{q}_s{sf}.o",
+                      [f"-DFAGQ_QF={q}", f"-DFAGQ_SF={sf}"]))
+        units.append((CSRC / "fagq_inst_typed.hip", out_dir / f"fagq_inst_typed_q{q}_s{sf}.o",
                       [f"-DFAGQ_QF={q}", f"-DFAGQ_SF={sf}"]))
     for unit in ("fagq_api", "fagq_gemm", "dsa_topk", "mla_bwd"):
         units.append((CSRC / f"{unit}.hip", out_dir / f"{unit}.o", []))

@@ -188,17 +188,12 @@ bool finish_mapping(int64_t M, int D, int wpr, int rpb, int mode, int lds, Mappi
 // * decode: 1 step per wave, one row per workgroup, as many waves as the row
 //   has steps (<= 16).
 // Rows of more than 16 steps use up to 4 steps per wave.
-void choose_mapping(int64_t M, int D, int scale_format, int scale_layout, Mapping* m) {
+// Rows split into waves of 1 step (decode, and prefill rows of 5..8 steps)
+// or FAGQ_PREFILL_STEPS steps, independent row groups: the route for every
+// shape the cases of choose_mapping below leave, and for the typed form.
+void default_mapping(int64_t M, int D, Mapping* m) {
   const int steps = ceil_div(D, kStepCols);
   const bool prefill = M >= prefill_rows();
-  const bool col = scale_layout == FAGQ_LAYOUT_COL_MAJOR;
-  (void)scale_format;
-  if (prefill && steps >= 12 && steps <= kMaxSharedSteps) {
-    const int wpr4 = ceil_div(steps, kMaxStepsPerWave);
-    if (col && finish_mapping(M, D, wpr4, 2, RG_WIDE_SCALES, 0, m)) return;
-    if (!col && steps >= 15 && finish_mapping(M, D, wpr4, 2, RG_SHARED_GAMMA, 0, m)) return;
-    if (!col && finish_mapping(M, D, ceil_div(steps, 2), 1, RG_INDEPENDENT, 48 * 1024, m)) return;
-  }
   int ns = prefill ? (steps >= 5 && steps <= 8 ? 1 : prefill_steps()) : 1;
   if (ns > kMaxStepsPerWave) ns = kMaxStepsPerWave;
   const int min_ns = ceil_div(steps, kMaxWavesPerBlock);
@@ -212,6 +207,20 @@ void choose_mapping(int64_t M, int D, int scale_format, int scale_layout, Mappin
   finish_mapping(M, D, wpr, rpb, RG_INDEPENDENT, lds, m);
 }
 
+void choose_mapping(int64_t M, int D, int scale_format, int scale_layout, Mapping* m) {
+  const int steps = ceil_div(D, kStepCols);
+  const bool prefill = M >= prefill_rows();
+  const bool col = scale_layout == FAGQ_LAYOUT_COL_MAJOR;
+  (void)scale_format;
+  if (prefill && steps >= 12 && steps <= kMaxSharedSteps) {
+    const int wpr4 = ceil_div(steps, kMaxStepsPerWave);
+    if (col && finish_mapping(M, D, wpr4, 2, RG_WIDE_SCALES, 0, m)) return;
+    if (!col && steps >= 15 && finish_mapping(M, D, wpr4, 2, RG_SHARED_GAMMA, 0, m)) return;
+    if (!col && finish_mapping(M, D, ceil_div(steps, 2), 1, RG_INDEPENDENT, 48 * 1024, m)) return;
+  }
+  default_mapping(M, D, m);
+}
+
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 struct Range {
@@ -220,10 +229,13 @@ struct Range {
 
 bool overlap(Range a, Range b) { return a.lo < b.hi && b.lo < a.hi; }
 
+// Argument checks of the operator; ba and br are the element sizes of the
+// activation tensors (x, gamma, norm_out) and of the residual stream
+// (residual, residual_out): 2 for bf16 / fp16, 4 for fp32.
 int validate(const void* x, const void* residual, const void* gamma, const void* residual_out,
              const void* norm_out, const void* q, const void* scale, int64_t M, int64_t D,
              int64_t G, float eps, int q_format, int scale_format, int scale_layout,
-             int rounding) {
+             int rounding, uintptr_t ba = 2, uintptr_t br = 2) {
   if (!x || !residual || !gamma || !residual_out || !q || !scale) return FAGQ_E_NULL;
   if (q_format != FAGQ_Q_INT8 && q_format != FAGQ_Q_FP8_E4M3FN) return FAGQ_E_FORMAT;
   if (scale_format != FAGQ_SCALE_F32 && scale_format != FAGQ_SCALE_UE8M0) return FAGQ_E_FORMAT;
@@ -246,18 +258,19 @@ int validate(const void* x, const void* residual, const void* gamma, const void*
     return FAGQ_E_ALIGN;
   if (M == 0) return FAGQ_OK;
 
-  // Byte ranges.  residual_out may be exactly x or residual (each element is
-  // read by the lane that later writes it); everything else is disjoint.
-  const uintptr_t nb = (uintptr_t)(M * D * 2);
+  // Byte ranges.  residual_out may be exactly residual, or x when x has the
+  // residual stream's element type (each element is read by the lane that
+  // later writes it); everything else is disjoint.
+  const uintptr_t ne = (uintptr_t)(M * D);
   const uintptr_t sb = (uintptr_t)(M * (D / G) * (scale_format == FAGQ_SCALE_F32 ? 4 : 1));
   auto rng = [](const void* p, uintptr_t n) {
     return Range{reinterpret_cast<uintptr_t>(p), reinterpret_cast<uintptr_t>(p) + n};
   };
-  const Range in[3] = {rng(x, nb), rng(residual, nb), rng(gamma, (uintptr_t)D * 2)};
-  const Range ro = rng(residual_out, nb), qo = rng(q, nb / 2), so = rng(scale, sb);
-  const Range no = norm_out ? rng(norm_out, nb) : Range{0, 0};
+  const Range in[3] = {rng(x, ne * ba), rng(residual, ne * br), rng(gamma, (uintptr_t)D * ba)};
+  const Range ro = rng(residual_out, ne * br), qo = rng(q, ne), so = rng(scale, sb);
+  const Range no = norm_out ? rng(norm_out, ne * ba) : Range{0, 0};
   for (int i = 0; i < 3; ++i) {
-    const bool exact_ok = (i < 2) && ro.lo == in[i].lo;
+    const bool exact_ok = ((i == 0 && ba == br) || i == 1) && ro.lo == in[i].lo;
     if (overlap(ro, in[i]) && !exact_ok) return FAGQ_E_ALIAS;
     if (overlap(qo, in[i]) || overlap(so, in[i]) || (norm_out && overlap(no, in[i])))
       return FAGQ_E_ALIAS;
@@ -308,6 +321,35 @@ LaunchFn lookup(int q_format, int scale_format, int rounding, int lpg_idx, int s
     default:
       return ue ? lookup_q2_s1(lpg_idx, steps, norm, ri) : lookup_q2_s0(lpg_idx, steps, norm, ri);
   }
+}
+
+LaunchFn lookup_typed(int q_format, int scale_format, int rounding, int lpg_idx, int steps,
+                      bool norm, int family) {
+  const int qf = q_format == FAGQ_Q_FP8_E4M3FN ? QF_FP8
+                 : rounding == FAGQ_ROUND_RNE  ? QF_I8_RNE
+                                               : QF_I8_TRUNC;
+  const bool ue = scale_format == FAGQ_SCALE_UE8M0;
+  switch (qf) {
+    case QF_FP8:
+      return ue ? lookup_typed_q0_s1(lpg_idx, steps, norm, family)
+                : lookup_typed_q0_s0(lpg_idx, steps, norm, family);
+    case QF_I8_RNE:
+      return ue ? lookup_typed_q1_s1(lpg_idx, steps, norm, family)
+                : lookup_typed_q1_s0(lpg_idx, steps, norm, family);
+    default:
+      return ue ? lookup_typed_q2_s1(lpg_idx, steps, norm, family)
+                : lookup_typed_q2_s0(lpg_idx, steps, norm, family);
+  }
+}
+
+// Type family of an (activation, residual-stream) element-type pair; -1 if
+// the pair is not supported (or is the bf16 pair, which fagq_launch serves).
+int type_family(int act_dtype, int res_dtype) {
+  if (act_dtype == FAGQ_DT_F16 && res_dtype == FAGQ_DT_F16) return TF_F16;
+  if (act_dtype == FAGQ_DT_BF16 && res_dtype == FAGQ_DT_F32) return TF_BF16_R32;
+  if (act_dtype == FAGQ_DT_F16 && res_dtype == FAGQ_DT_F32) return TF_F16_R32;
+  if (act_dtype == FAGQ_DT_F32 && res_dtype == FAGQ_DT_F32) return TF_F32;
+  return -1;
 }
 
 PartsLaunchFn lookup_parts(int q_format, int scale_format, int rounding, int lpg_idx, int steps) {
@@ -398,6 +440,33 @@ FAGQ_API int fagq_launch(const void* x, const void* residual, const void* gamma,
   return launch_with(m, x, residual, gamma, residual_out, norm_out, q, scale, M, D, group_size,
                      eps, q_format, scale_format, scale_layout, rounding,
                      remap_for(scale_layout, scale_format, m.rpb, m.mode), stream);
+}
+
+FAGQ_API int fagq_launch_typed(const void* x, const void* residual, const void* gamma,
+                               void* residual_out, void* norm_out, void* q, void* scale,
+                               int64_t M, int64_t D, int64_t group_size, float eps,
+                               int q_format, int scale_format, int scale_layout, int rounding,
+                               int act_dtype, int res_dtype, void* stream) {
+  if (act_dtype == FAGQ_DT_BF16 && res_dtype == FAGQ_DT_BF16)
+    return fagq_launch(x, residual, gamma, residual_out, norm_out, q, scale, M, D, group_size, eps,
+                       q_format, scale_format, scale_layout, rounding, stream);
+  const int tf = type_family(act_dtype, res_dtype);
+  if (tf < 0) return FAGQ_E_FORMAT;
+  const uintptr_t ba = act_dtype == FAGQ_DT_F32 ? 4 : 2, br = res_dtype == FAGQ_DT_F32 ? 4 : 2;
+  const int v = validate(x, residual, gamma, residual_out, norm_out, q, scale, M, D, group_size,
+                         eps, q_format, scale_format, scale_layout, rounding, ba, br);
+  if (v != FAGQ_OK || M == 0) return v;
+  const int dc = device_check();
+  if (dc != FAGQ_OK) return dc;
+  Mapping m;
+  default_mapping(M, (int)D, &m);
+  KArgs a;
+  fill_args(&a, m, x, residual, gamma, residual_out, norm_out, q, scale, M, D, group_size, eps,
+            scale_format, scale_layout, remap_for(scale_layout, scale_format, m.rpb, m.mode));
+  const LaunchFn fn = lookup_typed(q_format, scale_format, rounding, lpg_index((int)group_size),
+                                   m.ns, norm_out != nullptr, tf);
+  return fn(a, dim3((unsigned)m.grid), dim3((unsigned)m.block), (unsigned)m.lds,
+            static_cast<hipStream_t>(stream));
 }
 
 FAGQ_API int fagq_launch_mapped(const void* x, const void* residual, const void* gamma,

@@ -49,6 +49,15 @@ LaunchFn lookup_q1_s1(int lpg_idx, int steps, bool norm, int mode);   // int8 rn
 LaunchFn lookup_q2_s0(int lpg_idx, int steps, bool norm, int mode);   // int8 trunc, f32
 LaunchFn lookup_q2_s1(int lpg_idx, int steps, bool norm, int mode);   // int8 trunc, ue8m0
 
+// Typed form (fagq_rows_typed): lookup_typed_q<code>_s<scale>(lpg index, steps
+// per wave in [1, 4], norm, type family).
+LaunchFn lookup_typed_q0_s0(int lpg_idx, int steps, bool norm, int family);
+LaunchFn lookup_typed_q0_s1(int lpg_idx, int steps, bool norm, int family);
+LaunchFn lookup_typed_q1_s0(int lpg_idx, int steps, bool norm, int family);
+LaunchFn lookup_typed_q1_s1(int lpg_idx, int steps, bool norm, int family);
+LaunchFn lookup_typed_q2_s0(int lpg_idx, int steps, bool norm, int family);
+LaunchFn lookup_typed_q2_s1(int lpg_idx, int steps, bool norm, int family);
+
 // Multi-input form (fagq_rows_parts): lookup_parts_q<code>_s<scale>(lpg index,
 // steps per wave in [1, kMaxStepsParts]).
 PartsLaunchFn lookup_parts_q0_s0(int lpg_idx, int steps);

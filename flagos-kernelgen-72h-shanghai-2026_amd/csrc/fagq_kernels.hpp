@@ -507,14 +507,153 @@ __device__ __forceinline__ float group_scale(uint32_t gmax_bits, float inv_q, in
   return s;
 }
 
+// ---------------------------------------------------------------- element types
+
+// Element types of the tensors around the operator.  The bf16 kernel
+// (fagq_rows) reads and writes bf16 only; the typed kernel (fagq_rows_typed)
+// takes one element type for the activation tensors (x, gamma, norm_out) and
+// one for the residual stream (residual, residual_out), and converts every
+// load to fp32 and every store from fp32 (round to nearest even), as the
+// reference's kernels do (task01.py:88-89, :93-94 loads; :91, :118 stores).
+enum ElemType { ET_BF16 = 0, ET_F16 = 1, ET_F32 = 2 };
+
+// Type families of the typed kernel: (activation type, residual-stream type).
+enum TypeFamily { TF_F16 = 0, TF_BF16_R32 = 1, TF_F16_R32 = 2, TF_F32 = 3 };
+constexpr int kNumTypeFamilies = 4;
+
+template <int TF>
+struct Family {
+  static constexpr int A = TF == TF_F16 || TF == TF_F16_R32 ? ET_F16
+                           : TF == TF_BF16_R32            ? ET_BF16
+                                                          : ET_F32;
+  static constexpr int R = TF == TF_F16 ? ET_F16 : ET_F32;
+};
+
+template <int ET>
+constexpr uint32_t elem_bytes() {
+  return ET == ET_F32 ? 4u : 2u;
+}
+
+// A lane's 8 elements of one step: one 16-byte word for 2-byte types, two for
+// fp32.  2-byte types: lane l loads elements 8l..8l+7 of the step (bytes 16l..,
+// the wave's 64 loads one contiguous 1 KB).  fp32: the wave reads the step's
+// 2 KB as two contiguous 1 KB loads (lane l: 16-byte chunks l and 64 + l), and
+// lane_order() hands each lane its own chunks 2l and 2l + 1 through the wave's
+// LDS stage.  A lane-ordered fp32 load would stride 32 bytes per lane and
+// touch every 32-byte sector in two halves; on stores that means partial-sector
+// writes to HBM.
+template <int ET>
+struct Vec8 {
+  u32x4 v[ET == ET_F32 ? 2 : 1];
+};
+
+// 2 KB of LDS per wave: fp32 chunks on their way between wave order and lane
+// order.  A wave's LDS accesses execute in program order, so the hardware
+// needs no barrier between its transposes; the compiler, which reasons about
+// one lane, must not move a lane's read of another lane's slot across the
+// write of that slot (stage_sync between the two halves of each exchange).
+typedef u32x4 Stage[128];
+
+__device__ __forceinline__ void stage_sync() {
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int ET, int AUX>
+__device__ __forceinline__ Vec8<ET> load_elems8(const rsrc_t& rs, int lane, int k) {
+  Vec8<ET> r;
+  if constexpr (ET == ET_F32) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      r.v[h] = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16 + h * 1024 + k * kStepCols * 4,
+                                                     0, AUX);
+  } else {
+    r.v[0] = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16 + k * kStepCols * 2, 0, AUX);
+  }
+  return r;
+}
+
+// fp32 step as loaded (chunks l, 64 + l) -> lane order (chunks 2l, 2l + 1).
+template <int ET>
+__device__ __forceinline__ void lane_order(Vec8<ET>& p, int lane, Stage& st) {
+  if constexpr (ET == ET_F32) {
+    st[lane] = p.v[0];
+    st[64 + lane] = p.v[1];
+    stage_sync();
+    p.v[0] = st[2 * lane];
+    p.v[1] = st[2 * lane + 1];
+    stage_sync();
+  }
+}
+
+__device__ __forceinline__ float f16_lo(uint32_t v) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xffffu));
+}
+__device__ __forceinline__ float f16_hi(uint32_t v) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+}
+
+template <int ET>
+__device__ __forceinline__ void unpack_elems8(const Vec8<ET>& p, float (&f)[8]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if constexpr (ET == ET_BF16) {
+      f[2 * j] = bf16_lo(p.v[0][j]);
+      f[2 * j + 1] = bf16_hi(p.v[0][j]);
+    } else if constexpr (ET == ET_F16) {
+      f[2 * j] = f16_lo(p.v[0][j]);
+      f[2 * j + 1] = f16_hi(p.v[0][j]);
+    } else {
+      f[j] = __uint_as_float(p.v[0][j]);
+      f[4 + j] = __uint_as_float(p.v[1][j]);
+    }
+  }
+}
+
+// Two fp32 -> packed fp16x2, round to nearest even.
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+  f32x2 v = {lo, hi};
+  f16x2 h = __builtin_convertvector(v, f16x2);
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+// Stores a lane's 8 fp32 values of step k as ET (streaming stores); fp32
+// passes through the wave's LDS stage to leave as two contiguous 1 KB stores
+// (st is used for fp32 only).
+template <int ET>
+__device__ __forceinline__ void store_elems8(const rsrc_t& rs, int lane, int k,
+                                             const float (&f)[8], Stage* st = nullptr) {
+  if constexpr (ET == ET_F32) {
+    (*st)[2 * lane] = u32x4{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]),
+                            __float_as_uint(f[3])};
+    (*st)[2 * lane + 1] = u32x4{__float_as_uint(f[4]), __float_as_uint(f[5]),
+                                __float_as_uint(f[6]), __float_as_uint(f[7])};
+    stage_sync();
+    const u32x4 c0 = (*st)[lane], c1 = (*st)[64 + lane];
+    stage_sync();
+    __builtin_amdgcn_raw_buffer_store_b128(c0, rs, lane * 16 + k * kStepCols * 4, 0, kStoreAux);
+    __builtin_amdgcn_raw_buffer_store_b128(c1, rs, lane * 16 + 1024 + k * kStepCols * 4, 0,
+                                           kStoreAux);
+  } else {
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = ET == ET_BF16 ? pack_bf16x2(f[2 * j], f[2 * j + 1]) : pack_f16x2(f[2 * j], f[2 * j + 1]);
+    __builtin_amdgcn_raw_buffer_store_b128(o, rs, lane * 16 + k * kStepCols * 2, 0, kStoreAux);
+  }
+}
+
 // Phase 4 for one row: codes, optional norm_out and, with STORE_SCALES, the
 // scales (every lane of a group stores the group's scale to the same
 // address, one write after coalescing; groups past the row end get an
 // offset outside the descriptor and are dropped).
-template <int NS, int LPG, int QF, int SF, bool NORM, bool STORE_SCALES = true>
+template <int NS, int LPG, int QF, int SF, bool NORM, bool STORE_SCALES = true,
+          int NET = ET_BF16>
 __device__ __forceinline__ void row_out(const RowRsrc& rr, int lane, uint32_t gl,
                                         const float (&w)[NS][8], const uint32_t (&gmax)[NS],
-                                        float inv, float inv_q) {
+                                        float inv, float inv_q, Stage* st = nullptr) {
   constexpr uint32_t GPS = kStepCols / (LPG * 8);
 #pragma unroll
   for (int k = 0; k < NS; ++k) {
@@ -533,12 +672,7 @@ __device__ __forceinline__ void row_out(const RowRsrc& rr, int lane, uint32_t gl
       n[j] = w[k][j] * inv;
       t[j] = (SF == SF_F32) ? n[j] * mul : __builtin_ldexpf(n[j], -e);
     }
-    if constexpr (NORM) {
-      u32x4 no;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) no[j] = pack_bf16x2(n[2 * j], n[2 * j + 1]);
-      __builtin_amdgcn_raw_buffer_store_b128(no, rr.norm, lane * 16 + k * 1024, 0, kStoreAux);
-    }
+    if constexpr (NORM) store_elems8<NET>(rr.norm, lane, k, n, st);   // norm_out's element type
     const u32x2 codes = encode8<QF>(t);
     __builtin_amdgcn_raw_buffer_store_b64(codes, rr.q, lane * 8 + k * 512, 0, kStoreAux);
     if constexpr (STORE_SCALES) {
@@ -794,6 +928,105 @@ fagq_rows_parts(const PArgs pa) {
   float inv, inv_q;
   row_scale<QF>(ss, a, wave, rib, part, wpr, lane, s_part, s_inv, inv, inv_q);
   row_out<NS, LPG, QF, SF, false>(rr, lane, (uint32_t)wc.gl, w, gmax, inv, inv_q);
+}
+
+// Typed form (fagq_launch_typed): the operator with activation tensors (x,
+// gamma, norm_out) of element type Family<TF>::A and a residual stream
+// (residual, residual_out) of type Family<TF>::R, each converted to fp32 on
+// load and rounded to nearest even on store; the arithmetic from r = x +
+// residual on is the bf16 kernel's, operation for operation.  Row groups are
+// independent (each wave loads its own gamma slice, each row stores its own
+// scales); the element sizes set the descriptors and offsets.
+template <int NS, int LPG, int QF, int SF, bool NORM, int TF>
+__global__ void __launch_bounds__(1024)
+fagq_rows_typed(const KArgs a) {
+  static_assert(NS >= 1 && NS <= kMaxStepsPerWave, "steps per wave");
+  static_assert(TF >= 0 && TF < kNumTypeFamilies, "type family");
+  constexpr int EA = Family<TF>::A, ER = Family<TF>::R;
+  constexpr uint32_t ba = elem_bytes<EA>(), br = elem_bytes<ER>();
+  constexpr int G = LPG * 8;
+  constexpr uint32_t sb = SF == SF_F32 ? 4u : 1u;
+  constexpr bool F32IO = EA == ET_F32 || ER == ET_F32;
+  __shared__ double s_part[kMaxWavesPerBlock];
+  __shared__ float s_inv[kMaxWavesPerBlock][2];
+  __shared__ Stage s_stage[F32IO ? kMaxWavesPerBlock : 1];   // fp32 transposes, per wave
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  Stage& st = s_stage[F32IO ? wave : 0];
+  const int wpr = a.wpr();
+  const int blk = tile_of_block((int)blockIdx.x, (int)gridDim.x, a.remap(), a.remap_shift());
+  const int rib = (wave * a.wpr_magic) >> 16;
+  const int part = wave - rib * wpr;
+  const int64_t row = (int64_t)blk * a.rpb() + rib;
+  const int c0 = part * (NS * kStepCols);
+  const uint32_t wcols = a.D > c0 ? (uint32_t)(a.D - c0) : 0u;
+  const bool ok = row < a.M;
+  const int64_t e = (ok ? row : 0) * (int64_t)a.D + c0;
+  const uint32_t cols = ok ? wcols : 0u;
+
+  RowRsrc rr;
+  const uint8_t* xb = reinterpret_cast<const uint8_t*>(a.x);
+  const uint8_t* rb = reinterpret_cast<const uint8_t*>(a.res);
+  rr.x = make_rsrc(xb + e * ba, cols * ba);
+  rr.res = make_rsrc(rb + e * br, cols * br);
+  Vec8<EA> xv[NS];
+  Vec8<ER> rv[NS];
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    xv[k] = load_elems8<EA, kNonTemporal>(rr.x, lane, k);
+    rv[k] = load_elems8<ER, kNonTemporal>(rr.res, lane, k);
+  }
+  const rsrc_t rg = make_rsrc(reinterpret_cast<const uint8_t*>(a.gamma) + c0 * ba, wcols * ba);
+  Vec8<EA> gv[NS];
+#pragma unroll
+  for (int k = 0; k < NS; ++k) gv[k] = load_elems8<EA, 0>(rg, lane, k);
+  rr.res_out = make_rsrc(reinterpret_cast<uint8_t*>(a.res_out) + e * br, cols * br);
+  if constexpr (NORM) rr.norm = make_rsrc(reinterpret_cast<uint8_t*>(a.norm_out) + e * ba, cols * ba);
+  rr.q = make_rsrc(a.q + e, cols);
+  const ScaleSpan sp = scale_span(a.M, a.groups, a.col_major(), sb, row, ok, c0 / G, wcols != 0);
+  rr.scale = make_rsrc(a.scale + sp.base * sb, sp.bytes);
+  rr.ngroups = sp.ngroups;
+  rr.gstride = sp.gstride;
+
+  // r = x + residual, residual_out, the fp64 sum of squares, w = r * gamma and
+  // the group maxima, in the bf16 kernel's order.
+  float w[NS][8];
+  uint32_t gmax[NS];
+  double ss = 0.0;
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    float xs[8], rs[8];
+    lane_order<EA>(xv[k], lane, st);
+    lane_order<ER>(rv[k], lane, st);
+    unpack_elems8<EA>(xv[k], xs);
+    unpack_elems8<ER>(rv[k], rs);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w[k][j] = xs[j] + rs[j];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const double rd = (double)w[k][j];
+      ss = __builtin_fma(rd, rd, ss);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NS; ++k) store_elems8<ER>(rr.res_out, lane, k, w[k], &st);
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    float gs[8];
+    lane_order<EA>(gv[k], lane, st);
+    unpack_elems8<EA>(gv[k], gs);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w[k][j] = w[k][j] * gs[j];
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = __builtin_fmaxf(m, __builtin_fabsf(w[k][j]));
+    gmax[k] = group_max_bits<LPG>(__float_as_uint(m));
+  }
+  float inv, inv_q;
+  row_scale<QF>(ss, a, wave, rib, part, wpr, lane, s_part, s_inv, inv, inv_q);
+  row_out<NS, LPG, QF, SF, NORM, true, EA>(rr, lane, (uint32_t)(lane / LPG), w, gmax, inv, inv_q,
+                                           &st);
 }
 
 // ---------------------------------------------------------------- diagnostics

@@ -5,8 +5,10 @@
 // decode-sized call on the host: some 30 tensor attribute reads in Python and
 // a 16-argument ctypes call cost about 5 us against a 3 us kernel.  This
 // module does the same checks on the tensors' C++ metadata and calls
-// fagq_launch (include/fagq.h) through a function pointer handed over from
-// the ctypes binding at import, so both bindings reach the one library.
+// fagq_launch (bf16 tensors) or fagq_launch_typed (fp16 activations or an
+// fp32 residual stream; include/fagq.h) through function pointers handed
+// over from the ctypes binding at import, so both bindings reach the one
+// library.
 //
 //   launch(x, residual, gamma, residual_out, norm_out, x_q, x_scale, eps,
 //          group_size, rounding, stream) -> int
@@ -33,14 +35,29 @@ constexpr int kArgError = 1000;
 
 using LaunchFn = int (*)(const void*, const void*, const void*, void*, void*, void*, void*, int64_t,
                          int64_t, int64_t, float, int, int, int, int, void*);
+using TypedLaunchFn = int (*)(const void*, const void*, const void*, void*, void*, void*, void*,
+                              int64_t, int64_t, int64_t, float, int, int, int, int, int, int,
+                              void*);
 LaunchFn g_launch = nullptr;
+TypedLaunchFn g_launch_typed = nullptr;
 
 bool is_tensor(PyObject* o) { return THPVariable_Check(o); }
 
-// A contiguous bf16 tensor of `shape` on CUDA device `dev`.
-bool rows_ok(const at::Tensor& t, at::IntArrayRef shape, c10::DeviceIndex dev) {
-  return t.scalar_type() == at::kBFloat16 && t.sizes() == shape && t.is_cuda() &&
-         t.get_device() == dev && t.is_contiguous();
+// A contiguous tensor of element type `st` and `shape` on CUDA device `dev`.
+bool rows_ok(const at::Tensor& t, at::IntArrayRef shape, c10::DeviceIndex dev,
+             at::ScalarType st) {
+  return t.scalar_type() == st && t.sizes() == shape && t.is_cuda() && t.get_device() == dev &&
+         t.is_contiguous();
+}
+
+// fagq_dtype code of an element type, -1 for others.
+int dtype_code(at::ScalarType st) {
+  switch (st) {
+    case at::kBFloat16: return FAGQ_DT_BF16;
+    case at::kHalf: return FAGQ_DT_F16;
+    case at::kFloat: return FAGQ_DT_F32;
+    default: return -1;
+  }
 }
 
 PyObject* launch(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
@@ -80,10 +97,16 @@ PyObject* launch(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
   const auto shape = x.sizes();
   const int64_t M = shape[0], D = shape[1];
   const int64_t dshape[1] = {D};
-  if (!rows_ok(x, shape, dev) || !rows_ok(residual, shape, dev) ||
-      !rows_ok(residual_out, shape, dev) || !rows_ok(gamma, at::IntArrayRef(dshape, 1), dev))
+  // x, gamma and norm_out share the activation type, residual and
+  // residual_out the residual stream's; the library checks the pair.
+  const at::ScalarType at_ = x.scalar_type(), rt = residual.scalar_type();
+  const int act = dtype_code(at_), res = dtype_code(rt);
+  if (act < 0 || res < 0) return PyLong_FromLong(kArgError);
+  if (!rows_ok(x, shape, dev, at_) || !rows_ok(residual, shape, dev, rt) ||
+      !rows_ok(residual_out, shape, dev, rt) ||
+      !rows_ok(gamma, at::IntArrayRef(dshape, 1), dev, at_))
     return PyLong_FromLong(kArgError);
-  if (has_norm && !rows_ok(THPVariable_Unpack(args[4]), shape, dev))
+  if (has_norm && !rows_ok(THPVariable_Unpack(args[4]), shape, dev, at_))
     return PyLong_FromLong(kArgError);
   if (G <= 0 || D % G != 0) return PyLong_FromLong(kArgError);
 
@@ -127,30 +150,44 @@ PyObject* launch(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     return PyLong_FromLong(kArgError);
   if (M == 0) return PyLong_FromLong(FAGQ_OK);
 
-  const int st = g_launch(x.data_ptr(), residual.data_ptr(), gamma.data_ptr(),
-                          residual_out.data_ptr(),
-                          has_norm ? THPVariable_Unpack(args[4]).data_ptr() : nullptr,
-                          x_q.data_ptr(), x_scale.data_ptr(), M, D, G, (float)eps, qf, sf, layout,
-                          rnd, stream);
-  return PyLong_FromLong(st);
+  void* norm = has_norm ? THPVariable_Unpack(args[4]).data_ptr() : nullptr;
+  if (act == FAGQ_DT_BF16 && res == FAGQ_DT_BF16)
+    return PyLong_FromLong(g_launch(x.data_ptr(), residual.data_ptr(), gamma.data_ptr(),
+                                    residual_out.data_ptr(), norm, x_q.data_ptr(),
+                                    x_scale.data_ptr(), M, D, G, (float)eps, qf, sf, layout, rnd,
+                                    stream));
+  if (!g_launch_typed) return PyLong_FromLong(kArgError);
+  const int st = g_launch_typed(x.data_ptr(), residual.data_ptr(), gamma.data_ptr(),
+                                residual_out.data_ptr(), norm, x_q.data_ptr(), x_scale.data_ptr(),
+                                M, D, G, (float)eps, qf, sf, layout, rnd, act, res, stream);
+  // An unsupported type pair goes to the Python checks, which word the error.
+  return PyLong_FromLong(st == FAGQ_E_FORMAT ? kArgError : st);
 }
 
-// bind(address of fagq_launch in the loaded libfagq.so)
-PyObject* bind(PyObject*, PyObject* arg) {
-  void* p = PyLong_AsVoidPtr(arg);
+// bind(address of fagq_launch, address of fagq_launch_typed) in the loaded
+// libfagq.so.
+PyObject* bind(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+  if (nargs != 2) {
+    PyErr_SetString(PyExc_TypeError, "bind() takes 2 arguments");
+    return nullptr;
+  }
+  void* p = PyLong_AsVoidPtr(args[0]);
+  void* pt = PyLong_AsVoidPtr(args[1]);
   if (PyErr_Occurred()) return nullptr;
-  if (!p) {
+  if (!p || !pt) {
     PyErr_SetString(PyExc_ValueError, "bind(): null function address");
     return nullptr;
   }
   g_launch = reinterpret_cast<LaunchFn>(p);
+  g_launch_typed = reinterpret_cast<TypedLaunchFn>(pt);
   Py_RETURN_NONE;
 }
 
 PyMethodDef kMethods[] = {
     {"launch", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(&launch)),
      METH_FASTCALL, "Checks the operator's tensors and calls fagq_launch; returns its status."},
-    {"bind", &bind, METH_O, "Sets the address of fagq_launch."},
+    {"bind", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(&bind)),
+     METH_FASTCALL, "Sets the addresses of fagq_launch and fagq_launch_typed."},
     {nullptr, nullptr, 0, nullptr}};
 
 PyModuleDef kModule = {PyModuleDef_HEAD_INIT, "_fagq_py", "Per-call binding of fagq_launch.", -1,

@@ -14,6 +14,12 @@ returned.  The output formats are read from the destination tensors:
   :121); a [M, D/G] view with strides (1, M), e.g.
   ``torch.empty(D // G, M).t()``, -> column-major.
 * ``norm_out`` may be None: the 3-output form, which skips 2 bytes/element.
+* Element types, as the reference's kernels convert them (loads to fp32,
+  stores rounded to the destination's type, task01.py:88-94, :91, :118):
+  ``x``, ``gamma`` and ``norm_out`` share one type and ``residual``,
+  ``residual_out`` another, with (x, residual) in (bf16, bf16), (fp16, fp16),
+  (bf16, fp32), (fp16, fp32) or (fp32, fp32).  bf16 runs through
+  ``fagq_launch``, the others through ``fagq_launch_typed``.
 
 The reference validates nothing; here shapes, dtypes, devices and layouts
 are checked in Python (TypeError / ValueError) and everything else by the
@@ -28,7 +34,13 @@ import torch
 from . import _lib
 
 _BF16 = torch.bfloat16
+_F16 = torch.float16
 _FP8 = torch.float8_e4m3fn
+_DT_CODE = {torch.bfloat16: _lib.DT_BF16, torch.float16: _lib.DT_F16,
+            torch.float32: _lib.DT_F32}
+# (x dtype, residual dtype) pairs the library takes.
+_PAIRS = {(_lib.DT_BF16, _lib.DT_BF16), (_lib.DT_F16, _lib.DT_F16), (_lib.DT_BF16, _lib.DT_F32),
+          (_lib.DT_F16, _lib.DT_F32), (_lib.DT_F32, _lib.DT_F32)}
 
 
 def _q_format(x_q: torch.Tensor) -> int:
@@ -70,11 +82,12 @@ def _rounding(rounding: str | None, q_format: int) -> int:
     raise ValueError(f"rounding must be 'rne' or 'trunc', got {rounding!r}")
 
 
-def _check_rows(name: str, t: torch.Tensor, shape: tuple, device: torch.device) -> None:
+def _check_rows(name: str, t: torch.Tensor, shape: tuple, device: torch.device,
+                dtype: torch.dtype = _BF16) -> None:
     if t.device != device:
         raise ValueError(f"{name} is on {t.device}, expected {device}")
-    if t.dtype != _BF16:
-        raise TypeError(f"{name} must be bfloat16, got {t.dtype}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {str(dtype).replace('torch.', '')}, got {t.dtype}")
     if tuple(t.shape) != shape:
         raise ValueError(f"{name} must have shape {shape}, got {tuple(t.shape)}")
     if not t.is_contiguous():
@@ -114,8 +127,8 @@ def _is_current(dev: int) -> bool:
     return (_raw_device() if _raw_device is not None else torch.cuda.current_device()) == dev
 
 
-def _rows_ok(t, shape, dev: int) -> bool:
-    return (t.dtype is _BF16 and t.shape == shape and t.get_device() == dev
+def _rows_ok(t, shape, dev: int, dtype=_BF16) -> bool:
+    return (t.dtype is dtype and t.shape == shape and t.get_device() == dev
             and t.is_contiguous())
 
 
@@ -130,12 +143,19 @@ def _explain(x, residual, gamma, residual_out, norm_out, x_q, x_scale, group_siz
     """Raises the detailed error for arguments the fast checks rejected."""
     M, D = (int(v) for v in x.shape)
     device = x.device
-    _check_rows("x", x, (M, D), device)
-    _check_rows("residual", residual, (M, D), device)
-    _check_rows("gamma", gamma, (D,), device)
-    _check_rows("residual_out", residual_out, (M, D), device)
+    if x.dtype not in _DT_CODE:
+        raise TypeError(f"x must be bfloat16, float16 or float32, got {x.dtype}")
+    if residual.dtype not in _DT_CODE:
+        raise TypeError(f"residual must be bfloat16, float16 or float32, got {residual.dtype}")
+    if (_DT_CODE[x.dtype], _DT_CODE[residual.dtype]) not in _PAIRS:
+        raise TypeError(f"unsupported (x, residual) dtypes ({x.dtype}, {residual.dtype}): "
+                        "residual must have x's dtype or be float32")
+    _check_rows("x", x, (M, D), device, x.dtype)
+    _check_rows("residual", residual, (M, D), device, residual.dtype)
+    _check_rows("gamma", gamma, (D,), device, x.dtype)
+    _check_rows("residual_out", residual_out, (M, D), device, residual.dtype)
     if norm_out is not None:
-        _check_rows("norm_out", norm_out, (M, D), device)
+        _check_rows("norm_out", norm_out, (M, D), device, x.dtype)
     if group_size <= 0 or D % group_size != 0:
         raise ValueError(f"group_size {group_size} must divide D = {D}")
     qf = _q_format(x_q)
@@ -192,13 +212,15 @@ def fused_add_rmsnorm_group_quant(
     qf = _Q_CODE.get(x_q.dtype)
     sf = _S_CODE.get(x_scale.dtype)
     ss = x_scale.shape
-    if not (x.dtype is _BF16 and x.is_contiguous()
-            and residual.dtype is _BF16 and residual.shape == shape
+    xt, rt = x.dtype, residual.dtype
+    act, res = _DT_CODE.get(xt), _DT_CODE.get(rt)
+    if not ((act, res) in _PAIRS and x.is_contiguous()
+            and residual.shape == shape
             and residual.get_device() == dev and residual.is_contiguous()
-            and residual_out.dtype is _BF16 and residual_out.shape == shape
+            and residual_out.dtype is rt and residual_out.shape == shape
             and residual_out.get_device() == dev and residual_out.is_contiguous()
-            and (norm_out is None or _rows_ok(norm_out, shape, dev))
-            and gamma.dtype is _BF16 and gamma.shape == (D,) and gamma.get_device() == dev
+            and (norm_out is None or _rows_ok(norm_out, shape, dev, xt))
+            and gamma.dtype is xt and gamma.shape == (D,) and gamma.get_device() == dev
             and gamma.is_contiguous()
             and G > 0 and D % G == 0
             and qf is not None and x_q.shape == shape and x_q.get_device() == dev
@@ -216,10 +238,15 @@ def fused_add_rmsnorm_group_quant(
         rnd = _rounding(rounding, qf)
     if M == 0:
         return residual_out, norm_out, x_q, x_scale
-    fn = (_lib._lib or _lib.load()).fagq_launch
+    L = _lib._lib or _lib.load()
     args = (x.data_ptr(), residual.data_ptr(), gamma.data_ptr(), residual_out.data_ptr(),
             None if norm_out is None else norm_out.data_ptr(), x_q.data_ptr(), x_scale.data_ptr(),
             M, D, G, float(eps), qf, sf, layout, rnd)
+    if act == _lib.DT_BF16 and res == _lib.DT_BF16:
+        fn = L.fagq_launch
+    else:
+        fn = L.fagq_launch_typed
+        args = args + (act, res)
     if _raw_device is not None and _raw_stream is not None and _raw_device() == dev:
         st = fn(*args, _raw_stream(dev))
     else:

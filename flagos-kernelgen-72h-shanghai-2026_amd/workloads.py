@@ -24,6 +24,8 @@ class Workload:
     dist: str = "normal"             # "normal" | "outliers" | "student_t"
     eps: float = 1e-6
     seed: int = 0
+    act: torch.dtype = torch.bfloat16     # x and weight (the typed form: fp16 or fp32 too)
+    res: torch.dtype = torch.bfloat16     # residual and residual_out
 
     @property
     def groups(self) -> int:
@@ -34,11 +36,12 @@ class Workload:
         return 1 if self.scale_ue8m0 else 4
 
     def algorithmic_bytes(self, with_norm: bool = False) -> int:
-        """HBM bytes one call must move: read x, residual (2 B each per element)
-        and gamma once; write residual_out (2 B), codes (1 B) and scales."""
+        """HBM bytes one call must move: read x, residual (2 B each per bf16
+        element) and gamma once; write residual_out, codes (1 B) and scales."""
         N = self.M * self.D
-        b = 4 * N + 2 * self.D + 2 * N + N + self.scale_bytes * self.M * self.groups
-        return b + (2 * N if with_norm else 0)
+        ba, br = self.act.itemsize, self.res.itemsize
+        b = (ba + br) * N + ba * self.D + br * N + N + self.scale_bytes * self.M * self.groups
+        return b + (ba * N if with_norm else 0)
 
 
 # The benchmark configurations (BASELINE.json "configs", in order).
@@ -57,6 +60,15 @@ CONFIGS = {
 
 HEADLINE = "dsv3_16384x7168"
 
+# The headline shape through the typed form (fagq_launch_typed): fp16 tensors,
+# and bf16 activations with an fp32 residual stream.  Not BASELINE configs.
+TYPED_CONFIGS = {
+    "f16_16384x7168": Workload("f16_16384x7168", 16384, 7168, scale_col_major=True,
+                               dist="outliers", act=torch.float16, res=torch.float16),
+    "bf16_r32_16384x7168": Workload("bf16_r32_16384x7168", 16384, 7168, scale_col_major=True,
+                                    dist="outliers", res=torch.float32),
+}
+
 
 def outlier_channels(D: int, seed: int) -> torch.Tensor:
     """The fixed 1 % of hidden channels (round(0.01 * D)) scaled by 50."""
@@ -66,7 +78,8 @@ def outlier_channels(D: int, seed: int) -> torch.Tensor:
 
 
 def make_inputs(w: Workload, M: int | None = None):
-    """(x, residual, weight) bf16 CPU tensors for workload ``w``.  ``M``
+    """(x, residual, weight) CPU tensors for workload ``w`` (bf16, or the
+    workload's typed-form element types).  ``M``
     overrides the row count: same distributions and seed, but a different
     draw (weight is drawn after x and residual)."""
     M = w.M if M is None else M
@@ -86,7 +99,7 @@ def make_inputs(w: Workload, M: int | None = None):
         ch = outlier_channels(w.D, w.seed)
         x[:, ch] *= 50.0
         res[:, ch] *= 50.0
-    return x.to(torch.bfloat16), res.to(torch.bfloat16), weight.to(torch.bfloat16)
+    return x.to(w.act), res.to(w.res), weight.to(w.act)
 
 
 # ------------------------------------------------------------- GEMM consumer

@@ -111,6 +111,34 @@ FAGQ_API int fagq_launch(const void* x, const void* residual, const void* gamma,
                          int q_format, int scale_format, int scale_layout,
                          int rounding, void* stream);
 
+/* Element types of the typed form. */
+enum fagq_dtype { FAGQ_DT_BF16 = 0, FAGQ_DT_F16 = 1, FAGQ_DT_F32 = 2 };
+
+/*
+ * fagq_launch_typed - fagq_launch for other element types, as the reference
+ * accepts them: its kernels convert every load to fp32 (task01.py:88-89,
+ * :93-94) and every store to the destination's type (:91, :118), so fp16
+ * activations or an fp32 residual stream run through the same operator
+ * (src/task01_fused_add_rmsnorm_group_quant.py:1731-1741).
+ *
+ *   act_dtype        element type of x, gamma and norm_out
+ *   res_dtype        element type of residual and residual_out
+ *   (act_dtype, res_dtype) in {(BF16, BF16) (= fagq_launch), (F16, F16),
+ *   (BF16, F32), (F16, F32), (F32, F32)}; other pairs FAGQ_E_FORMAT.
+ *
+ * Loads convert to fp32 exactly; residual_out and norm_out are rounded to
+ * their type to nearest even (fp16 overflows to +-inf).  From r = x +
+ * residual on, the definition is fagq_launch's.  Every x / residual /
+ * gamma / residual_out / norm_out pointer is 16-byte aligned; residual_out
+ * may be exactly residual (or x when both have the same element type).
+ * Other arguments, limits and statuses as for fagq_launch.
+ */
+FAGQ_API int fagq_launch_typed(const void* x, const void* residual, const void* gamma,
+                               void* residual_out, void* norm_out, void* q, void* scale,
+                               int64_t M, int64_t D, int64_t group_size, float eps,
+                               int q_format, int scale_format, int scale_layout, int rounding,
+                               int act_dtype, int res_dtype, void* stream);
+
 /* Multi-input form: the epilogue of a tensor-parallel reduction.  x is the
  * sum of nparts partial tensors (one per rank of a row-parallel layer, e.g.
  * the contributions a reduce-scatter gathers for this rank's rows), added in

@@ -62,6 +62,12 @@ def lib() -> ctypes.CDLL:
         L.orc_fagq.restype = I
         L.orc_fagq_parts.argtypes = [P, I] + [P] * 6 + [I64, I64, I64, F, I, I, I, I, I]
         L.orc_fagq_parts.restype = I
+        L.orc_fagq_typed.argtypes = [P] * 7 + [I64, I64, I64, F, I, I, I, I, I, I, I]
+        L.orc_fagq_typed.restype = I
+        L.orc_f16_from_f32.argtypes = [P, P, I64]
+        L.orc_f16_from_f32.restype = None
+        L.orc_f32_from_f16.argtypes = [P, P, I64]
+        L.orc_f32_from_f16.restype = None
         L.orc_e4m3fn_to_f64.argtypes = [P, P, I64]
         L.orc_e4m3fn_to_f64.restype = None
         L.orc_gemm.argtypes = [P, P, P, P, P, P, I64, I64, I64, I, I, I, I]
@@ -82,6 +88,22 @@ def bf16_from_f32(v: np.ndarray) -> np.ndarray:
     v = np.ascontiguousarray(v, dtype=np.float32)
     out = np.empty(v.shape, np.uint16)
     lib().orc_bf16_from_f32(_ptr(v), _ptr(out), v.size)
+    return out
+
+
+def f16_from_f32(v: np.ndarray) -> np.ndarray:
+    """fp32 -> IEEE binary16 bits, round to nearest even (the oracle's encoder)."""
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    out = np.empty(v.shape, np.uint16)
+    lib().orc_f16_from_f32(_ptr(v), _ptr(out), v.size)
+    return out
+
+
+def f32_from_f16(h: np.ndarray) -> np.ndarray:
+    """IEEE binary16 bits -> fp32 (the oracle's decoder)."""
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().orc_f32_from_f16(_ptr(h), _ptr(out), h.size)
     return out
 
 
@@ -133,6 +155,43 @@ def fagq(x: np.ndarray, residual: np.ndarray, gamma: np.ndarray, eps: float, gro
     st = lib().orc_fagq(_ptr(x), _ptr(residual), _ptr(gamma), _ptr(res_out), _ptr(norm_out),
                         _ptr(q), _ptr(scale), M, D, group_size, float(eps), q_format,
                         scale_format, scale_layout, rounding, nthreads)
+    if st != 0:
+        raise ValueError(f"oracle rejected the arguments (status {st})")
+    out = {"residual_out": res_out, "q": q, "scale": scale}
+    if with_norm:
+        out["norm_out"] = norm_out
+    return out
+
+
+DT_BF16, DT_F16, DT_F32 = 0, 1, 2
+_DT_NP = {DT_BF16: np.uint16, DT_F16: np.uint16, DT_F32: np.float32}
+
+
+def fagq_typed(x: np.ndarray, residual: np.ndarray, gamma: np.ndarray, eps: float,
+               group_size: int, act_dtype: int, res_dtype: int, q_format: int = Q_FP8,
+               scale_format: int = S_F32, scale_layout: int = L_ROW, rounding: int = R_RNE,
+               with_norm: bool = False, nthreads: int = 0) -> dict:
+    """The typed form (orc_fagq_typed): x and gamma hold act_dtype elements,
+    residual res_dtype elements (bf16 and fp16 as uint16 bit patterns, fp32 as
+    float32).  Returns residual_out (res_dtype storage), q, scale and, when
+    with_norm, norm_out (act_dtype storage)."""
+    ta, tr = _DT_NP[act_dtype], _DT_NP[res_dtype]
+    x = np.ascontiguousarray(x).view(ta) if x.dtype.itemsize == np.dtype(ta).itemsize else None
+    residual = np.ascontiguousarray(residual).view(tr)
+    gamma = np.ascontiguousarray(gamma).view(ta)
+    assert x is not None
+    M, D = x.shape
+    assert residual.shape == (M, D) and gamma.shape == (D,)
+    groups = D // group_size
+    res_out = np.empty((M, D), tr)
+    norm_out = np.empty((M, D), ta) if with_norm else None
+    q = np.empty((M, D), np.uint8)
+    sdt = np.float32 if scale_format == S_F32 else np.uint8
+    scale = np.empty((groups, M) if scale_layout == L_COL else (M, groups), sdt)
+    st = lib().orc_fagq_typed(_ptr(x), _ptr(residual), _ptr(gamma), _ptr(res_out),
+                              _ptr(norm_out), _ptr(q), _ptr(scale), M, D, group_size, float(eps),
+                              q_format, scale_format, scale_layout, rounding, act_dtype,
+                              res_dtype, nthreads)
     if st != 0:
         raise ValueError(f"oracle rejected the arguments (status {st})")
     out = {"residual_out": res_out, "q": q, "scale": scale}

@@ -48,6 +48,33 @@ static inline uint16_t f32_to_bf16(float f) {
   return (uint16_t)(u >> 16);
 }
 
+/* IEEE binary16 -> fp32, exactly (subnormals, infinities, NaN payloads). */
+static inline float f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  if (e == 0) {                                    /* zero or subnormal: m * 2^-24 */
+    const float v = ldexpf((float)m, -24);
+    return sign ? -v : v;
+  }
+  if (e == 31) return u2f(sign | 0x7f800000u | (m << 13));
+  return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+/* fp32 -> IEEE binary16, round to nearest even: |v| >= 65520 (the tie above
+ * the largest finite 65504) becomes +-inf; below 2^-14 the result is the
+ * subnormal rint(|v| * 2^24) * 2^-24 (1024 there is 2^-14, the smallest
+ * normal); NaN stays NaN (quiet). */
+static inline uint16_t f32_to_f16(float f) {
+  const uint32_t u = f2u(f);
+  const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
+  if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
+  if (a < 0x38800000u) return (uint16_t)(sign | (uint16_t)rintf(u2f(a) * 16777216.0f));
+  /* rebias the exponent (127 -> 15) and round the 23-bit mantissa to 10 bits */
+  return (uint16_t)(sign | ((a - 0x38000000u + 0x0fffu + ((a >> 13) & 1u)) >> 13));
+}
+
 /* fp32 -> OCP fp8 e4m3fn (bias 7, 3 mantissa bits, no infinities, max 448,
  * S.1111.111 = NaN), round to nearest even.  |v| >= 464 rounds past 448 and
  * gives NaN (no saturation), as a plain IEEE-style conversion does. */
@@ -94,6 +121,14 @@ static inline uint8_t encode(float t, int q_format, int rounding) {
 
 ORC_API void orc_bf16_from_f32(const float* in, uint16_t* out, int64_t n) {
   for (int64_t i = 0; i < n; ++i) out[i] = f32_to_bf16(in[i]);
+}
+
+ORC_API void orc_f16_from_f32(const float* in, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = f32_to_f16(in[i]);
+}
+
+ORC_API void orc_f32_from_f16(const uint16_t* in, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = f16_to_f32(in[i]);
 }
 
 /* Codes for already-scaled values, after the operator's clamp. */
@@ -199,4 +234,90 @@ ORC_API int orc_fagq(const uint16_t* x, const uint16_t* residual, const uint16_t
   const uint16_t* parts[1] = {x};
   return orc_fagq_parts(parts, 1, residual, gamma, residual_out, norm_out, q, scale, M, D, G,
                         eps, q_format, scale_format, scale_layout, rounding, nthreads);
+}
+
+/* ---- the typed form (fagq_launch_typed, include/fagq.h) ---- */
+
+enum { DT_BF16 = 0, DT_F16 = 1, DT_F32 = 2 };
+
+static inline float load_elem(const void* p, int64_t i, int dt) {
+  if (dt == DT_F32) return ((const float*)p)[i];
+  const uint16_t h = ((const uint16_t*)p)[i];
+  return dt == DT_F16 ? f16_to_f32(h) : bf16_to_f32(h);
+}
+
+static inline void store_elem(void* p, int64_t i, int dt, float v) {
+  if (dt == DT_F32) ((float*)p)[i] = v;
+  else ((uint16_t*)p)[i] = dt == DT_F16 ? f32_to_f16(v) : f32_to_bf16(v);
+}
+
+/*
+ * The operator with x, gamma and norm_out of element type act_dtype and
+ * residual, residual_out of res_dtype (DT_BF16, DT_F16 or DT_F32): every
+ * load is converted to fp32 and every store rounded to its type, as the
+ * reference's kernels do (task01.py:88-89, :93-94, :91, :118); the
+ * arithmetic is orc_fagq_parts' with one part.  Host pointers; norm_out may
+ * be NULL.  Returns 0, or 1 on an argument this restatement does not accept.
+ */
+ORC_API int orc_fagq_typed(const void* x, const void* residual, const void* gamma,
+                           void* residual_out, void* norm_out, uint8_t* q, void* scale,
+                           int64_t M, int64_t D, int64_t G, float eps, int q_format,
+                           int scale_format, int scale_layout, int rounding, int act_dtype,
+                           int res_dtype, int nthreads) {
+  if (M < 0 || D <= 0 || G <= 0 || D % G != 0) return 1;
+  if (q_format == Q_FP8 && rounding != R_RNE) return 1;
+  if (act_dtype < DT_BF16 || act_dtype > DT_F32 || res_dtype < DT_BF16 || res_dtype > DT_F32)
+    return 1;
+  const float qmax = q_format == Q_FP8 ? 448.0f : 127.0f;
+  const int64_t groups = D / G;
+  int ok = 0;
+#pragma omp parallel num_threads(nthreads > 0 ? nthreads : omp_get_max_threads()) if (M > 1)
+  {
+    float* w = (float*)malloc((size_t)D * sizeof(float));
+    if (!w) {
+#pragma omp atomic write
+      ok = 1;
+    } else {
+#pragma omp for schedule(static)
+      for (int64_t m = 0; m < M; ++m) {
+        double ss = 0.0;
+        for (int64_t j = 0; j < D; ++j) {
+          const int64_t i = m * D + j;
+          const float r = load_elem(x, i, act_dtype) + load_elem(residual, i, res_dtype);
+          store_elem(residual_out, i, res_dtype, r);
+          ss += (double)r * (double)r;
+          w[j] = r * load_elem(gamma, j, act_dtype);
+        }
+        const float sumsq = (float)ss;
+        const float mean = sumsq / (float)D;
+        const float inv = (float)(1.0 / sqrt((double)(mean + eps)));
+        const float inv_q = inv / qmax;
+        for (int64_t g = 0; g < groups; ++g) {
+          float gmax = 0.0f;
+          for (int64_t j = g * G; j < (g + 1) * G; ++j) gmax = fmaxf(gmax, fabsf(w[j]));
+          const float s = fmaxf(gmax * inv_q, 1.0e-12f);
+          const int64_t si = scale_layout == L_COL ? g * M + m : m * groups + g;
+          float mul = 0.0f;
+          int e = 0;
+          if (scale_format == S_F32) {
+            mul = 1.0f / s;
+            ((float*)scale)[si] = s;
+          } else {
+            e = ceil_log2_bits(s);
+            if (e > 127) e = 127;
+            ((uint8_t*)scale)[si] = (uint8_t)(e + 127);
+          }
+          for (int64_t j = g * G; j < (g + 1) * G; ++j) {
+            const float n = w[j] * inv;
+            if (norm_out) store_elem(norm_out, m * D + j, act_dtype, n);
+            const float u = scale_format == S_F32 ? n * mul : ldexpf(n, -e);
+            const float t = fminf(fmaxf(u, -qmax), qmax);
+            q[m * D + j] = encode(t, q_format, rounding);
+          }
+        }
+      }
+      free(w);
+    }
+  }
+  return ok;
 }

@@ -16,17 +16,18 @@ def fagq_torch(x: torch.Tensor, residual: torch.Tensor, gamma: torch.Tensor, eps
                group_size: int, out_dtype: torch.dtype = torch.float8_e4m3fn,
                scale_ue8m0: bool = False, col_major: bool = False, rounding: str = "rne",
                with_norm: bool = False):
-    """x, residual: bf16 [M, D]; gamma: bf16 [D] (CPU tensors).
+    """x, residual: [M, D]; gamma: [D] (CPU tensors; bf16, or the typed form's
+    element types: x and gamma one type, residual another).
 
-    Returns (residual_out bf16, q, scale[, norm_out]) with scale in its
-    physical layout ([M, groups] or [groups, M]).
+    Returns (residual_out in residual's type, q, scale[, norm_out in x's type])
+    with scale in its physical layout ([M, groups] or [groups, M]).
     """
     M, D = x.shape
     G = group_size
     groups = D // G
     qmax = 448.0 if out_dtype == torch.float8_e4m3fn else 127.0
     r = x.float() + residual.float()                                # :88-89
-    residual_out = r.to(torch.bfloat16)                             # :91
+    residual_out = r.to(residual.dtype)                             # :91
     rd = r.double()
     sumsq = (rd * rd).sum(dim=1).float()                            # :90, exact-rounded
     mean = sumsq / torch.tensor(float(D), dtype=torch.float32)
@@ -59,5 +60,5 @@ def fagq_torch(x: torch.Tensor, residual: torch.Tensor, gamma: torch.Tensor, eps
         scale = scale.t().contiguous()
     outs = (residual_out, q, scale)
     if with_norm:
-        outs = outs + (n.to(torch.bfloat16),)
+        outs = outs + (n.to(x.dtype),)
     return outs

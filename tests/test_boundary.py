@@ -139,6 +139,66 @@ def test_launch_validation(lib, kw, status):
     assert call(lib, **kw) == status
 
 
+def call_typed(lib, act, res, **kw):
+    a = dict(x=fake(0), residual=fake(1), gamma=fake(2), residual_out=fake(3), norm_out=None,
+             q=fake(4), scale=fake(5), M=8, D=4096, G=128, eps=1e-6, qf=1, sf=0, layout=0,
+             rounding=0, stream=None)
+    a.update(kw)
+    return lib.fagq_launch_typed(a["x"], a["residual"], a["gamma"], a["residual_out"],
+                                 a["norm_out"], a["q"], a["scale"], a["M"], a["D"], a["G"],
+                                 a["eps"], a["qf"], a["sf"], a["layout"], a["rounding"], act, res,
+                                 a["stream"])
+
+
+BF16, F16, F32 = 0, 1, 2
+
+
+@pytest.mark.parametrize("act,res,kw,status", [
+    (BF16, F16, {}, 5), (F32, BF16, {}, 5), (F32, F16, {}, 5), (F16, BF16, {}, 5),
+    (3, F32, {}, 5), (F16, -1, {}, 5),
+    (F16, F16, dict(x=None), 1), (BF16, F32, dict(gamma=None), 1),
+    (BF16, BF16, dict(x=None), 1), (BF16, BF16, dict(G=32), 3),   # the bf16 pair is fagq_launch
+    (F16, F32, dict(D=4000), 2), (F32, F32, dict(eps=-1.0), 6),
+    (F16, F32, dict(residual=ctypes.c_void_p(BASE + 0x1_0000_0008)), 4),
+    (F32, F32, dict(gamma=ctypes.c_void_p(BASE + 0x2_0000_0004)), 4),
+    # residual_out may be exactly residual, or x only when x has the residual's size
+    (F16, F32, dict(residual_out=fake(0)), 9),
+    (BF16, F32, dict(residual_out=ctypes.c_void_p(BASE + 0x1_0000_0000 + 0x100)), 9),
+    # fp32 x spans M * D * 4 = 128 KiB: codes 64 KiB past it overlap (bf16 x would not)
+    (F32, F32, dict(q=ctypes.c_void_p(BASE + 0x10000)), 9),
+    (F16, F32, dict(norm_out=ctypes.c_void_p(BASE + 0x1_0000_0000 + 0x10000)), 9),
+    (F16, F16, dict(M=0), 0), (F32, F32, dict(M=0), 0), (BF16, F32, dict(M=0), 0),
+])
+def test_typed_launch_validation(lib, act, res, kw, status):
+    assert call_typed(lib, act, res, **kw) == status
+
+
+def test_typed_dtype_errors_are_worded(pkg):
+    # The Python checks (reached for every argument the fast path rejects)
+    # name the tensor and the type it must have.
+    from fagq_mi355x import ops
+    M, D = 2, 256
+    kw = dict(x_q=torch.empty(M, D, dtype=torch.int8), x_scale=torch.empty(M, 2), group_size=128,
+              rounding=None)
+    h, f, b = torch.float16, torch.float32, torch.bfloat16
+    def explain(x, r, g, ro, norm=None):
+        ops._explain(torch.empty(M, D, dtype=x), torch.empty(M, D, dtype=r),
+                     torch.empty(D, dtype=g), torch.empty(M, D, dtype=ro),
+                     None if norm is None else torch.empty(M, D, dtype=norm), **kw)
+    with pytest.raises(TypeError, match="unsupported"):
+        explain(h, b, h, b)
+    with pytest.raises(TypeError, match="unsupported"):
+        explain(f, h, f, h)
+    with pytest.raises(TypeError, match="gamma must be float16"):
+        explain(h, f, f, f)
+    with pytest.raises(TypeError, match="residual_out must be float32"):
+        explain(b, f, b, b)
+    with pytest.raises(TypeError, match="norm_out must be bfloat16"):
+        explain(b, f, b, f, norm=f)
+    with pytest.raises(TypeError, match="x must be"):
+        explain(torch.int32, f, f, f)
+
+
 def test_in_place_residual_is_accepted_by_validation(lib):
     # residual_out == residual passes validation; with M = 0 nothing is launched.
     assert call(lib, residual_out=fake(1), M=0) == 0
@@ -231,6 +291,8 @@ def test_cpython_binding_is_built_and_bound(pkg):
     with pytest.raises(TypeError):
         fast(*args[:10])
     with pytest.raises(ValueError):
+        _fagq_py.bind(0, 0)
+    with pytest.raises(TypeError):
         _fagq_py.bind(0)
 
 
@@ -332,7 +394,7 @@ def test_gemm_mapped_validation(lib):
     assert mapped(192, K=1000) == 2
 
 
-def test_gemm_workloads():
+def test_gemm_workloads(pkg):
     from fagq_mi355x.workloads import GEMM_CONFIGS, GemmWorkload, make_gemm_inputs
     w = GemmWorkload("t", 300, 272, 512, "f32", "ue8m0", seed=3)
     a_q, a_s, b_q, b_s = make_gemm_inputs(w)
@@ -413,7 +475,7 @@ def test_mla_workspace_size(lib):
     assert lib.fagq_mla_bwd_workspace_bytes(2, 4096, 576) == 2 * (4096 + 64) * 512 * 4
 
 
-def test_mla_workloads():
+def test_mla_workloads(pkg):
     from fagq_mi355x.workloads import MLA_CONFIGS, MLA_HEADLINE
     w = MLA_CONFIGS[MLA_HEADLINE]
     assert (w.B, w.H, w.S, w.D) == (2, 64, 4096, 512)

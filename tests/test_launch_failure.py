@@ -53,6 +53,10 @@ def test_every_launching_entry_point_reports_it(seam):
     st = seam.fagq_launch_parts(ctypes.cast(parts, ctypes.c_void_p), 2, fake(1), fake(2), fake(3),
                                 fake(4), fake(5), 8, 4096, 128, 1e-6, 1, 0, 0, 0, None)
     assert st == -HIP_ERROR_LAUNCH_FAILURE
+    for act, res in ((1, 1), (0, 2), (1, 2), (2, 2)):      # the typed form's type pairs
+        st = seam.fagq_launch_typed(fake(0), fake(1), fake(2), fake(3), fake(6), fake(4), fake(5),
+                                    8, 4096, 128, 1e-6, 1, 0, 0, 0, act, res, None)
+        assert st == -HIP_ERROR_LAUNCH_FAILURE, (act, res)
     assert seam.fagq_diag_stream(fake(0), fake(1), 4096, 0, None) == -HIP_ERROR_LAUNCH_FAILURE
     assert seam.fagq_diag_encode(fake(0), fake(1), 64, 1, 0, 0, None) == -HIP_ERROR_LAUNCH_FAILURE
     st = seam.fagq_dsa_topk_launch(fake(0), 0, fake(1), fake(2), fake(3), 0, fake(4), fake(5), 1, 2,

@@ -323,3 +323,108 @@ def test_thread_count_does_not_change_results():
     b = oracle.fagq(x, r, g, 1e-6, 128, nthreads=8)
     for k in a:
         assert np.array_equal(a[k], b[k])
+
+
+# ----------------------------------------------------------------- typed form
+
+def test_f16_decoder_matches_torch_exhaustively():
+    """All 65536 fp16 bit patterns (subnormals, infinities, NaNs) against torch."""
+    h = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    ours = oracle.f32_from_f16(h)
+    ref = torch.from_numpy(h.view(np.int16)).view(torch.float16).float().numpy()
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(ours), nan)
+    assert np.array_equal(ours.view(np.uint32)[~nan], ref.view(np.uint32)[~nan])
+
+
+def test_f16_encoder_matches_torch_cast():
+    """fp32 -> fp16 round to nearest even against torch's cast: every fp32 in
+    the binades around the subnormal range, the subnormal/normal boundary and
+    the overflow edge (65504 .. 65520 .. inf), every tie between fp16
+    neighbours in [1, 2), and 4 M random bit patterns."""
+    parts = [binade(e) for e in (-26, -25, -24, -15, -14, 15, 16)]
+    ties = (np.arange(1 << 10, dtype=np.uint32) << 13 | np.uint32(0x1000)) | np.uint32(127 << 23)
+    rng = np.random.default_rng(8)
+    u = rng.integers(0, 1 << 32, size=1 << 22, dtype=np.uint64).astype(np.uint32)
+    parts += [bits_to_f32(ties), -bits_to_f32(ties), bits_to_f32(u),
+              np.float32([65504.0, 65519.996, 65520.0, 70000.0, np.inf, -np.inf, 0.0, -0.0])]
+    f = np.concatenate(parts)
+    f = f[~np.isnan(f)]
+    ours = oracle.f16_from_f32(f)
+    ref = torch.from_numpy(f).to(torch.float16).view(torch.int16).numpy().view(np.uint16)
+    bad = ours != ref
+    assert not bad.any(), (f[bad][:4], ours[bad][:4], ref[bad][:4])
+    nan = oracle.f16_from_f32(np.float32([np.nan]))
+    assert (int(nan[0]) & 0x7C00) == 0x7C00 and (int(nan[0]) & 0x3FF) != 0
+
+
+def run_typed(x, r, g, act, res, G=128, fmt="fp8", ue8m0=False, col=False, eps=1e-6,
+              with_norm=False):
+    qf, rnd, _ = FMT[fmt]
+    return oracle.fagq_typed(x, r, g, eps, G, act, res, qf,
+                             oracle.S_UE8M0 if ue8m0 else oracle.S_F32,
+                             oracle.L_COL if col else oracle.L_ROW, rnd, with_norm)
+
+
+@pytest.mark.parametrize("fmt", list(FMT))
+@pytest.mark.parametrize("ue8m0,col", [(False, False), (True, True)])
+def test_typed_bf16_pair_is_the_bf16_oracle(fmt, ue8m0, col):
+    x, r, g = random_inputs(9, 3072, 11, scale=3.0)
+    a = run(x, r, g, 128, fmt, ue8m0, col, with_norm=True)
+    b = run_typed(x, r, g, oracle.DT_BF16, oracle.DT_BF16, 128, fmt, ue8m0, col, with_norm=True)
+    for k in a:
+        assert np.array_equal(a[k], b[k]), k
+
+
+@pytest.mark.parametrize("act", [oracle.DT_BF16, oracle.DT_F16])
+def test_f32_residual_stream_widens_exactly(act):
+    """An fp32 residual stream holding exactly the widened 16-bit residual gives
+    the same r, so the same codes, scales and norm_out as the 16-bit stream;
+    residual_out is then r itself, which rounds to the 16-bit residual_out.
+    Catches a residual loaded or stored with the wrong width or type."""
+    rng = np.random.default_rng(12)
+    M, D = 6, 2048
+    enc = oracle.bf16_from_f32 if act == oracle.DT_BF16 else oracle.f16_from_f32
+    dec = oracle.f32_from_bf16 if act == oracle.DT_BF16 else oracle.f32_from_f16
+    x = enc(rng.standard_normal((M, D)).astype(np.float32))
+    r16 = enc(rng.standard_normal((M, D)).astype(np.float32))
+    g = enc((1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32))
+    a = run_typed(x, r16, g, act, act, with_norm=True)
+    b = run_typed(x, dec(r16), g, act, oracle.DT_F32, with_norm=True)
+    assert np.array_equal(a["q"], b["q"]) and np.array_equal(a["scale"], b["scale"])
+    assert np.array_equal(a["norm_out"], b["norm_out"])
+    r = dec(x) + dec(r16)
+    assert np.array_equal(b["residual_out"].view(np.uint32), r.view(np.uint32))
+    assert np.array_equal(enc(b["residual_out"]), a["residual_out"])
+
+
+def test_f32_activations_match_f64_mathematics():
+    """All-fp32 tensors: dequantized codes against the float64 mathematics of
+    (x + r) * g / rms, within half a code step (catches a dropped /D, a wrong
+    eps or a gamma applied after the maximum, without any 16-bit rounding)."""
+    rng = np.random.default_rng(13)
+    M, D, G, eps = 8, 1024, 128, 1e-6
+    x = rng.standard_normal((M, D)).astype(np.float32)
+    r = rng.standard_normal((M, D)).astype(np.float32)
+    g = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    out = run_typed(x, r, g, oracle.DT_F32, oracle.DT_F32, G, "int8_rne", eps=eps, with_norm=True)
+    rr = x.astype(np.float64) + r.astype(np.float64)
+    n = rr * g.astype(np.float64) / np.sqrt((rr * rr).mean(axis=1, keepdims=True) + eps)
+    s = out["scale"].astype(np.float64)
+    assert np.allclose(s, np.abs(n.reshape(M, D // G, G)).max(axis=2) / 127.0, rtol=2e-6)
+    deq = decode_codes(out["q"], "int8_rne").reshape(M, D // G, G) * s[..., None]
+    assert np.all(np.abs(deq - n.reshape(M, D // G, G)) <= 0.5 * s[..., None] * (1 + 1e-5))
+    assert np.allclose(out["norm_out"].astype(np.float64), n, rtol=1e-6, atol=1e-30)
+    assert np.array_equal(out["residual_out"], (x + r).astype(np.float32))
+
+
+def test_f16_constant_row_closed_form():
+    """fp16 x = c, residual = 0, gamma = 1: every scale |c| / sqrt(c^2 + eps) / 448."""
+    eps, D = 1e-6, 4096
+    for c in (0.001, 0.5, 3.0, 250.0):
+        cf = float(oracle.f32_from_f16(oracle.f16_from_f32(np.float32([c])))[0])
+        x = np.full((1, D), oracle.f16_from_f32(np.float32([c]))[0], np.uint16)
+        out = run_typed(x, np.zeros_like(x), oracle.f16_from_f32(np.ones(D, np.float32)),
+                        oracle.DT_F16, oracle.DT_F16, eps=eps)
+        expect = cf / math.sqrt(cf * cf + eps) / 448.0
+        assert np.abs(out["scale"].astype(np.float64) - expect).max() / expect < 1e-6
