@@ -84,9 +84,12 @@ def case(pkg, dev, B, H, S, D, grad_dtype, dc_dtype=None, seed=0):
         f"{label}: dc off by {float((err - tol).max())} over tolerance"
 
 
+# S <= 1024 runs the single-launch sequence scan (up to 4 rows per part at 1024),
+# longer sequences the block totals and block scan (1025, 2048).
 @pytest.mark.parametrize("B,H,S,D", [(1, 4, 64, 512), (2, 3, 100, 64), (1, 2, 10, 128),
                                      (1, 8, 257, 256), (2, 64, 256, 512), (2, 64, 512, 512),
-                                     (1, 1, 1, 64)])
+                                     (1, 1, 1, 64), (1, 4, 1024, 128), (1, 4, 1025, 128),
+                                     (2, 16, 2048, 64), (2, 8, 769, 512)])
 @pytest.mark.parametrize("grad", [torch.float32, torch.bfloat16])
 def test_mla_matches_oracle(pkg, gpu, B, H, S, D, grad):
     case(pkg, gpu, B, H, S, D, grad)
