@@ -84,8 +84,9 @@ def case(pkg, dev, B, H, S, D, grad_dtype, dc_dtype=None, seed=0):
         f"{label}: dc off by {float((err - tol).max())} over tolerance"
 
 
-# S <= 1024 runs the single-launch sequence scan (up to 4 rows per part at 1024),
-# longer sequences the block totals and block scan (1025, 2048).
+# Short sequences split the heads into several partial head-sum planes and
+# their scan blocks into column slices (S = 256, 512); 769, 1024, 1025 and 2048
+# cover block counts that do not divide the rows evenly and fewer planes.
 @pytest.mark.parametrize("B,H,S,D", [(1, 4, 64, 512), (2, 3, 100, 64), (1, 2, 10, 128),
                                      (1, 8, 257, 256), (2, 64, 256, 512), (2, 64, 512, 512),
                                      (1, 1, 1, 64), (1, 4, 1024, 128), (1, 4, 1025, 128),
