@@ -36,7 +36,8 @@ output (fagq_gemm_launch); value and roofline in TFLOP/s against MI355X's
 5.0 PFLOP/s dense fp8 peak, cpu_baseline = the C oracle (oracle/gemm_oracle.c)
 on a row sample.
 
---copy BYTES and --mfma-peak time the library's ceiling probes instead: HBM
+--copy BYTES and --mfma-peak time the ceiling probes instead (libfagq_probe.so,
+include/fagq_probe.h, not part of the drop-in library): HBM
 copy, read-only and write-only streams with the operator's cache policies
 (achievable bandwidth, counter calibration), and the GEMM's matrix instruction
 issued from registers (achievable MFMA rate).  --lds-probe times the LDS read
@@ -198,7 +199,7 @@ def copy_bench(args, torch, pkg) -> int:
     import ctypes
     from fagq_mi355x import _lib
     dev = torch.device("cuda:0")
-    lib = pkg.load_library()
+    lib = pkg.load_probe_library()
     n = args.copy // 16 * 16
     nsets = max(2, math.ceil(ROTATE_BYTES / (2 * n)) + 1)
     bufs = [(torch.empty(n, dtype=torch.uint8, device=dev).fill_(1),
@@ -236,7 +237,7 @@ def mfma_peak_bench(args, torch, pkg) -> int:
     register operands, the same flops per launch.  One JSON line per shape."""
     import ctypes
     dev = torch.device("cuda:0")
-    lib = pkg.load_library()
+    lib = pkg.load_probe_library()
     blocks, iters = 2048, 1000
     out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream(dev)
@@ -272,7 +273,7 @@ def lds_probe_bench(args, torch, pkg) -> int:
     line per pattern."""
     import ctypes
     dev = torch.device("cuda:0")
-    lib = pkg.load_library()
+    lib = pkg.load_probe_library()
     blocks, iters = 1024, 256
     out = torch.empty(blocks * 256 * 4, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream(dev)

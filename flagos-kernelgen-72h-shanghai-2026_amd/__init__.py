@@ -7,7 +7,7 @@ Python identifier; load it with ``__graft_entry__.load_package()``, which
 registers it as ``fagq_mi355x``.
 """
 from . import _lib
-from ._lib import FagqError, load as load_library
+from ._lib import FagqError, load as load_library, load_probe as load_probe_library
 from .dsa_topk import dsa_topk_page_table_transform
 from .gemm import fp8_block_scaled_gemm, gemm_route
 from .mla_bwd import mla_bwd_nope_dkdv
@@ -24,6 +24,7 @@ __all__ = [
     "fused_reduce_add_rmsnorm_group_quant",
     "gemm_route",
     "load_library",
+    "load_probe_library",
     "mla_bwd_nope_dkdv",
     "route_for",
 ]

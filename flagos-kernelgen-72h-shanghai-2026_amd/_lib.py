@@ -1,5 +1,7 @@
 """ctypes binding of libfagq.so (the C ABI declared in include/fagq.h,
-include/fagq_gemm.h, include/fagq_dsa.h and include/fagq_diag.h).
+include/fagq_gemm.h, include/fagq_dsa.h, include/fagq_mla.h and
+include/fagq_diag.h) and of libfagq_probe.so (include/fagq_probe.h, the
+measurement probes, loaded only when asked for).
 
 The library is loaded after ``import torch`` so that its libamdhip64.so.7
 dependency resolves to the HIP runtime torch already loaded (same soname);
@@ -16,6 +18,7 @@ import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = PKG_DIR / "libfagq.so"
+PROBE_LIB_PATH = PKG_DIR / "libfagq_probe.so"
 
 # Enums of include/fagq.h and include/fagq_diag.h.
 Q_INT8, Q_FP8_E4M3FN = 0, 1
@@ -61,12 +64,7 @@ SIGNATURES = {
     "fagq_status_string": ([_I], ctypes.c_char_p),
     "fagq_version": ([], _I),
     "fagq_diag_encode": ([_P, _P, _I64, _I, _I, _I, _P], _I),
-    "fagq_diag_copy": ([_P, _P, _I64, _P], _I),
-    "fagq_diag_stream": ([_P, _P, _I64, _I, _P], _I),
     "fagq_diag_scale_offsets": ([_I64, _I64, _I64, _I, _I, _I, _I64, _P, _I64], _I),
-    "fagq_diag_mfma_peak": ([_P, _I64, _I, _P], _I),
-    "fagq_diag_mfma_rate": ([_P, _I64, _I, _I, _P], _I),
-    "fagq_diag_lds_read": ([_P, _I64, _I, _I, _P], _I),
     "fagq_dsa_topk_launch": ([_P, _I, _P, _P, _P, _I, _P, _P] + [_I64] * 6 + [_P], _I),
     "fagq_gemm_launch": ([_P] * 5 + [_I64, _I64, _I64, _I, _I, _I, _P], _I),
     "fagq_gemm_launch_mapped": ([_P] * 5 + [_I64, _I64, _I64, _I, _I, _I, _I, _P], _I),
@@ -74,6 +72,16 @@ SIGNATURES = {
     "fagq_mla_bwd_workspace_bytes": ([_I64, _I64, _I64], _I64),
     "fagq_mla_bwd_launch": ([_P] * 8 + [_I64] * 5 + [_F, _I, _I, _P], _I),
     "fagq_mla_bwd_launch_noalloc": ([_P] * 7 + [_I64] * 4 + [_F, _I, _I, _P], _I),
+}
+
+
+# libfagq_probe.so (include/fagq_probe.h).
+PROBE_SIGNATURES = {
+    "fagq_diag_copy": ([_P, _P, _I64, _P], _I),
+    "fagq_diag_stream": ([_P, _P, _I64, _I, _P], _I),
+    "fagq_diag_mfma_peak": ([_P, _I64, _I, _P], _I),
+    "fagq_diag_mfma_rate": ([_P, _I64, _I, _I, _P], _I),
+    "fagq_diag_lds_read": ([_P, _I64, _I, _I, _P], _I),
 }
 
 
@@ -88,6 +96,20 @@ class FagqError(RuntimeError):
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
+_probe: ctypes.CDLL | None = None
+
+
+def _open(p: Path, signatures: dict) -> ctypes.CDLL:
+    if not p.exists():
+        raise ImportError(
+            f"{p} is missing: build the HIP libraries first "
+            "(python __graft_entry__.py build, or build.build())")
+    lib = ctypes.CDLL(str(p))
+    for name, (args, res) in signatures.items():
+        fn = getattr(lib, name)   # AttributeError if an export is missing
+        fn.argtypes = args
+        fn.restype = res
+    return lib
 
 
 def load(path: str | Path | None = None) -> ctypes.CDLL:
@@ -98,18 +120,24 @@ def load(path: str | Path | None = None) -> ctypes.CDLL:
     with _lock:
         if _lib is not None and path is None:
             return _lib
-        p = Path(path) if path is not None else LIB_PATH
-        if not p.exists():
-            raise ImportError(
-                f"{p} is missing: build the HIP library first "
-                "(python __graft_entry__.py build, or build.build())")
-        lib = ctypes.CDLL(str(p))
-        for name, (args, res) in SIGNATURES.items():
-            fn = getattr(lib, name)   # AttributeError if an export is missing
-            fn.argtypes = args
-            fn.restype = res
+        lib = _open(Path(path) if path is not None else LIB_PATH, SIGNATURES)
         if path is None:
             _lib = lib
+        return lib
+
+
+def load_probe(path: str | Path | None = None) -> ctypes.CDLL:
+    """Loads libfagq_probe.so (the measurement probes) once; raises if it is
+    absent or incomplete."""
+    global _probe
+    if _probe is not None and path is None:
+        return _probe
+    with _lock:
+        if _probe is not None and path is None:
+            return _probe
+        lib = _open(Path(path) if path is not None else PROBE_LIB_PATH, PROBE_SIGNATURES)
+        if path is None:
+            _probe = lib
         return lib
 
 

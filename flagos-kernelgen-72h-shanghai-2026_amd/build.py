@@ -1,8 +1,10 @@
-"""Builds libfagq.so, the gfx950 HIP library behind the operator.
+"""Builds libfagq.so, the gfx950 HIP library behind the operators, and
+libfagq_probe.so, the measurement probes (HBM streams, matrix-instruction
+rate, LDS reads) that are not part of the drop-in library.
 
 Every HIP translation unit is compiled by hipcc for gfx950 only, in
-parallel, into ``_build/``; the objects are linked into ``libfagq.so`` next
-to this file, which is what the Python layer loads.  Runs on a machine
+parallel, into ``_build/``; the objects are linked into the two libraries
+next to this file, which is what the Python layer loads.  Runs on a machine
 without a GPU (hipcc cross-compiles).
 """
 from __future__ import annotations
@@ -19,6 +21,9 @@ CSRC = PKG_DIR / "csrc"
 INCLUDE = REPO_DIR / "include"
 OBJ_DIR = PKG_DIR / "_build"
 LIB_PATH = PKG_DIR / "libfagq.so"
+PROBE_LIB_PATH = PKG_DIR / "libfagq_probe.so"
+LIB_UNITS = ("fagq_api", "fagq_device", "fagq_gemm", "dsa_topk", "mla_bwd")
+PROBE_UNITS = ("fagq_probe", "fagq_device")
 
 ARCH = "gfx950"
 # (code format, scale format) pairs compiled from fagq_inst.hip:
@@ -100,10 +105,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
                       [f"-DFAGQ_QF={q}", f"-DFAGQ_SF={s}"]))
         units.append((CSRC / "fagq_inst_typed.hip", OBJ_DIR / f"fagq_inst_typed_q{q}_s{s}.o",
                       [f"-DFAGQ_QF={q}", f"-DFAGQ_SF={s}"]))
-    units.append((CSRC / "fagq_api.hip", OBJ_DIR / "fagq_api.o", []))
-    units.append((CSRC / "fagq_gemm.hip", OBJ_DIR / "fagq_gemm.o", []))
-    units.append((CSRC / "dsa_topk.hip", OBJ_DIR / "dsa_topk.o", []))
-    units.append((CSRC / "mla_bwd.hip", OBJ_DIR / "mla_bwd.o", []))
+    for unit in sorted(set(LIB_UNITS) | set(PROBE_UNITS)):
+        units.append((CSRC / f"{unit}.hip", OBJ_DIR / f"{unit}.o", []))
     jobs = jobs or min(len(units) + 1, max(1, min(16, os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         futs = [ex.submit(_run, [cc, *flags, *defs, "-c", str(src), "-o", str(obj)], verbose)
@@ -112,11 +115,22 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
         for f in futs:
             f.result()
     os.replace(pyext_path().with_suffix(".so.tmp"), pyext_path())
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
-          *[str(o) for _, o, _ in units]], verbose)
-    os.replace(tmp, LIB_PATH)
+    _link(cc, units, LIB_PATH, probe=False, verbose=verbose)
+    _link(cc, units, PROBE_LIB_PATH, probe=True, verbose=verbose)
     return LIB_PATH
+
+
+def _link(cc: str, units, lib: Path, *, probe: bool, verbose: bool, extra=()) -> None:
+    """Links libfagq.so (every unit but the probes) or libfagq_probe.so (the
+    probes and the device check) from the compiled units."""
+    if probe:
+        objs = [str(o) for src, o, _ in units if src.stem in PROBE_UNITS]
+    else:
+        objs = [str(o) for src, o, _ in units if src.stem != "fagq_probe"]
+    tmp = lib.with_suffix(".so.tmp")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *extra, "-o", str(tmp), *objs],
+         verbose)
+    os.replace(tmp, lib)
 
 
 def sanitizer_runtime() -> Path:
@@ -131,7 +145,8 @@ def sanitizer_runtime() -> Path:
 
 def build_variant(name: str, *, defines: tuple[str, ...] = (), sanitize: bool = False,
                   verbose: bool = False) -> Path:
-    """A test-only build of the same sources into _build/<name>/libfagq.so, with
+    """A test-only build of the same sources into _build/<name>/libfagq.so (and
+    libfagq_probe.so beside it), with
     extra -D defines (e.g. FAGQ_TEST_LAUNCH_FAILURE) and, with `sanitize`,
     AddressSanitizer and UndefinedBehaviorSanitizer on every host function
     (the argument validation, route table and host-side diagnostics; the
@@ -149,7 +164,7 @@ def build_variant(name: str, *, defines: tuple[str, ...] = (), sanitize: bool = 
                       [f"-DFAGQ_QF={q}", f"-DFAGQ_SF={sf}"]))
         units.append((CSRC / "fagq_inst_typed.hip", out_dir / f"fagq_inst_typed_q{q}_s{sf}.o",
                       [f"-DFAGQ_QF={q}", f"-DFAGQ_SF={sf}"]))
-    for unit in ("fagq_api", "fagq_gemm", "dsa_topk", "mla_bwd"):
+    for unit in sorted(set(LIB_UNITS) | set(PROBE_UNITS)):
         units.append((CSRC / f"{unit}.hip", out_dir / f"{unit}.o", []))
     with ThreadPoolExecutor(max_workers=min(len(units), max(1, min(16, os.cpu_count() or 1)))) as ex:
         futs = [ex.submit(_run, [cc, *flags, *san, *defs, "-c", str(src), "-o", str(obj)], verbose)
@@ -158,8 +173,8 @@ def build_variant(name: str, *, defines: tuple[str, ...] = (), sanitize: bool = 
             f.result()
     lib = out_dir / "libfagq.so"
     link_san = ["-fsanitize=address", "-fsanitize=undefined", "-shared-libsan"] if sanitize else []
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *link_san,
-          "-o", str(lib), *[str(o) for _, o, _ in units]], verbose)
+    _link(cc, units, lib, probe=False, verbose=verbose, extra=link_san)
+    _link(cc, units, out_dir / "libfagq_probe.so", probe=True, verbose=verbose, extra=link_san)
     return lib
 
 

@@ -1,13 +1,12 @@
 // fagq_api.hip - C ABI of the fused residual-add + RMSNorm + group-quant
-// operator: argument validation, the route table, the per-device gfx950
-// check, and launches on the caller's stream.
+// operator: argument validation, the route table and launches on the
+// caller's stream (the per-device gfx950 check is fagq_device.hip's).
 //
 // Replaces the reference's Python entry and routers
 // (src/task01_fused_add_rmsnorm_group_quant.py:1731-1851 and :1548-1728) and
 // its per-call backend tagging (:13-62): the route is a pure function of
 // (M, D), the device check is done once per device, and nothing here
 // allocates, synchronizes or throws.
-#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -19,71 +18,7 @@
 namespace fagq {
 namespace {
 
-// HBM ceiling probes (and byte-counter calibration): every thread moves one
-// 16-byte chunk through buffer descriptors, with the operator's cache
-// policies (non-temporal loads, sc1 | nt stores).  kStreamBlock threads per
-// workgroup, one workgroup per kStreamBlock * 16 bytes.
-constexpr int kStreamBlock = 512;
-
-__device__ __forceinline__ uint32_t chunk_bytes(int64_t bytes) {
-  const int64_t rem = bytes - (int64_t)blockIdx.x * kStreamBlock * 16;
-  return rem > kStreamBlock * 16 ? kStreamBlock * 16u : (uint32_t)rem;
-}
-
-__global__ void __launch_bounds__(kStreamBlock) fagq_stream_copy(const uint8_t* src, uint8_t* dst,
-                                                                 int64_t bytes) {
-  const int64_t base = (int64_t)blockIdx.x * kStreamBlock * 16;
-  const uint32_t n = chunk_bytes(bytes);
-  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(src + base, n), threadIdx.x * 16,
-                                                        0, kNonTemporal);
-  __builtin_amdgcn_raw_buffer_store_b128(v, make_rsrc(dst + base, n), threadIdx.x * 16, 0,
-                                         kStoreAux);
-}
-
-// Read-only: the loaded data is kept live by a store to dst[0..15] that runs
-// only when a chunk's four words XOR to 0x9e3779b9.
-__global__ void __launch_bounds__(kStreamBlock) fagq_stream_read(const uint8_t* src, uint8_t* dst,
-                                                                 int64_t bytes) {
-  const int64_t base = (int64_t)blockIdx.x * kStreamBlock * 16;
-  const uint32_t n = chunk_bytes(bytes);
-  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(src + base, n), threadIdx.x * 16,
-                                                        0, kNonTemporal);
-  if ((v[0] ^ v[1] ^ v[2] ^ v[3]) == 0x9e3779b9u)
-    __builtin_amdgcn_raw_buffer_store_b128(v, make_rsrc(dst, 16), 0, 0, 0);
-}
-
-// Write-only: each chunk gets (its byte offset, thread, 2, 3).
-__global__ void __launch_bounds__(kStreamBlock) fagq_stream_write(const uint8_t*, uint8_t* dst,
-                                                                  int64_t bytes) {
-  const int64_t base = (int64_t)blockIdx.x * kStreamBlock * 16;
-  const uint32_t n = chunk_bytes(bytes);
-  const u32x4 v = {(uint32_t)base, threadIdx.x, 2u, 3u};
-  __builtin_amdgcn_raw_buffer_store_b128(v, make_rsrc(dst + base, n), threadIdx.x * 16, 0,
-                                         kStoreAux);
-}
-
-// The operator's byte mix without its arithmetic: every thread reads 16
-// bytes of x and of residual (8 bf16 each) and writes 16 bytes of
-// residual_out and 8 bytes of codes.  x, residual = src, src + bytes;
-// residual_out, codes = dst, dst + bytes.
-__global__ void __launch_bounds__(kStreamBlock) fagq_stream_opmix(const uint8_t* src, uint8_t* dst,
-                                                                  int64_t bytes) {
-  const int64_t base = (int64_t)blockIdx.x * kStreamBlock * 16;
-  const uint32_t n = chunk_bytes(bytes);
-  const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(src + base, n), threadIdx.x * 16,
-                                                        0, kNonTemporal);
-  const u32x4 r = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(src + bytes + base, n),
-                                                        threadIdx.x * 16, 0, kNonTemporal);
-  const u32x4 s = x ^ r;
-  __builtin_amdgcn_raw_buffer_store_b128(s, make_rsrc(dst + base, n), threadIdx.x * 16, 0,
-                                         kStoreAux);
-  __builtin_amdgcn_raw_buffer_store_b64(u32x2{s[0] ^ s[1], s[2] ^ s[3]},
-                                        make_rsrc(dst + bytes + base / 2, n / 2), threadIdx.x * 8,
-                                        0, kStoreAux);
-}
-
 constexpr int kVersion = 1 * 10000 + 0 * 100 + 0;
-constexpr int kMaxDevices = 64;
 
 struct Mapping {
   int wpr;        // waves per row
@@ -279,32 +214,6 @@ int validate(const void* x, const void* residual, const void* gamma, const void*
   if (norm_out && (overlap(no, ro) || overlap(no, qo) || overlap(no, so))) return FAGQ_E_ALIAS;
   return FAGQ_OK;
 }
-
-}  // namespace
-
-// gfx950 check, done once per device.  The launch-failure test build has no
-// device to check.
-int device_check() {
-#ifdef FAGQ_TEST_LAUNCH_FAILURE
-  return FAGQ_OK;
-#endif
-  static std::atomic<int> cache[kMaxDevices];   // 0 unknown, 1 gfx950, 2 other
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return -(int)e;
-  if (dev < 0 || dev >= kMaxDevices) return FAGQ_E_DEVICE;
-  int c = cache[dev].load(std::memory_order_relaxed);
-  if (c == 0) {
-    hipDeviceProp_t prop;
-    e = hipGetDeviceProperties(&prop, dev);
-    if (e != hipSuccess) return -(int)e;
-    c = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 2;
-    cache[dev].store(c, std::memory_order_relaxed);
-  }
-  return c == 1 ? FAGQ_OK : FAGQ_E_DEVICE;
-}
-
-namespace {
 
 LaunchFn lookup(int q_format, int scale_format, int rounding, int lpg_idx, int steps, bool norm,
                 int mode) {
@@ -587,33 +496,6 @@ FAGQ_API int fagq_diag_encode(const float* in, void* out, int64_t n, int q_forma
       {reinterpret_cast<const void*>(&fagq_encode<QF_I8_TRUNC, false>),
        reinterpret_cast<const void*>(&fagq_encode<QF_I8_TRUNC, true>)}};
   return launch_kernel(kernels[qf][clamp], grid, block, args, 0, s);
-}
-
-FAGQ_API int fagq_diag_stream(const void* src, void* dst, int64_t bytes, int mode,
-                              void* stream) {
-  if (mode < FAGQ_STREAM_COPY || mode > FAGQ_STREAM_OPMIX) return FAGQ_E_FORMAT;
-  if ((mode != FAGQ_STREAM_WRITE && !src) || !dst) return FAGQ_E_NULL;
-  if (bytes < 0 || bytes % (mode == FAGQ_STREAM_OPMIX ? 32 : 16) != 0) return FAGQ_E_SHAPE;
-  if ((src && !aligned(src, 16)) || !aligned(dst, 16)) return FAGQ_E_ALIGN;
-  if (bytes == 0) return FAGQ_OK;
-  const int64_t blocks = (bytes + kStreamBlock * 16 - 1) / (kStreamBlock * 16);
-  if (blocks > INT32_MAX) return FAGQ_E_TOO_LARGE;
-  const int dc = device_check();
-  if (dc != FAGQ_OK) return dc;
-  const uint8_t* s8 = static_cast<const uint8_t*>(src);
-  uint8_t* d8 = static_cast<uint8_t*>(dst);
-  int64_t n = bytes;
-  void* args[] = {&s8, &d8, &n};
-  const void* k = mode == FAGQ_STREAM_COPY    ? reinterpret_cast<const void*>(&fagq_stream_copy)
-                  : mode == FAGQ_STREAM_READ  ? reinterpret_cast<const void*>(&fagq_stream_read)
-                  : mode == FAGQ_STREAM_WRITE ? reinterpret_cast<const void*>(&fagq_stream_write)
-                                              : reinterpret_cast<const void*>(&fagq_stream_opmix);
-  return launch_kernel(k, dim3((unsigned)blocks), dim3(kStreamBlock), args, 0,
-                       static_cast<hipStream_t>(stream));
-}
-
-FAGQ_API int fagq_diag_copy(const void* src, void* dst, int64_t bytes, void* stream) {
-  return fagq_diag_stream(src, dst, bytes, FAGQ_STREAM_COPY, stream);
 }
 
 FAGQ_API int fagq_diag_scale_offsets(int64_t M, int64_t D, int64_t group_size, int scale_format,

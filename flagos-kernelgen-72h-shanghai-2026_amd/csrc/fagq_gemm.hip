@@ -55,6 +55,7 @@
 #include "fagq_diag.h"
 #include "fagq_dispatch.hpp"
 #include "fagq_gemm.h"
+#include "fagq_gemm_lds.hpp"
 
 namespace fagq {
 namespace gemm {
@@ -67,7 +68,6 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 
 constexpr int kBM = 256;                 // rows of C per workgroup
 constexpr int kMaxBN = 256;              // columns of C per workgroup, at most
-constexpr int kBK = 128;                 // k per block (one MFMA deep, one scale block)
 constexpr int kATileBytes = kBM * kBK;   // the activation tile of one stage in LDS
 constexpr int kGroupM = 4;               // row tiles per group of the tile order
 constexpr int kCUs = 256;                // compute units of a gfx950 MI355X / MI350X
@@ -145,9 +145,6 @@ __device__ __forceinline__ void tile_coords(int b, int m_tiles, int n_tiles, int
   nt = w / gm;
 }
 
-// Position of logical 16-byte chunk c of LDS row r (only r % 8 matters).
-__device__ __forceinline__ int swz_of(int r) { return ((r >> 1) & 1) | (r & 4); }
-__device__ __forceinline__ int swz(int c, int r) { return c ^ swz_of(r); }
 
 // One 16 x 128-byte MFMA operand: lane l gets row (r0 + l % 16), k bytes
 // 32 (l / 16) .. +32, from a swizzled LDS tile.
@@ -522,108 +519,6 @@ int launch(const void* a_q, const void* a_scale, const void* b_q, const void* b_
                        static_cast<hipStream_t>(stream));
 }
 
-// Issue-rate probe of the GEMM's instruction: every wave keeps 8 independent
-// 16 x 16 accumulators and issues iters x 8 v_mfma_scale_f32_16x16x128_f8f6f4
-// (E8M0 scales 2^-7 and 2^3) on register operands, with no memory access in
-// the loop; each thread then writes the sum of its accumulators.
-constexpr int kPeakThreads = 256;
-constexpr int kPeakChain = 8;
-__global__ void __launch_bounds__(kPeakThreads) mfma_peak_kernel(float* out, int iters) {
-  const int t = threadIdx.x;
-  i32x8 a, b;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {   // fp8 e4m3 values near 1.0 (0x38) and 0.5 (0x30)
-    a[i] = 0x38383838 ^ (t * 7 + i);
-    b[i] = 0x30303030 ^ (t * 3 + i);
-  }
-  f32x4 c[kPeakChain] = {};
-  for (int it = 0; it < iters; ++it) {
-#pragma unroll
-    for (int j = 0; j < kPeakChain; ++j)
-      c[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c[j], 0, 0, 0, 120, 0, 130);
-  }
-  float r = 0.0f;
-#pragma unroll
-  for (int j = 0; j < kPeakChain; ++j) r += c[j][0] + c[j][1] + c[j][2] + c[j][3];
-  out[(int64_t)blockIdx.x * kPeakThreads + t] = r;
-}
-
-// The 32 x 32 x 64 shape: every wave keeps 4 independent 32 x 32
-// accumulators (16 floats per lane each) and issues iters x 4 instructions,
-// each twice the flops of one 16 x 16 x 128.
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-constexpr int kPeakChain32 = 4;
-__global__ void __launch_bounds__(kPeakThreads) mfma_peak32_kernel(float* out, int iters) {
-  const int t = threadIdx.x;
-  i32x8 a, b;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    a[i] = 0x38383838 ^ (t * 7 + i);
-    b[i] = 0x30303030 ^ (t * 3 + i);
-  }
-  f32x16 c[kPeakChain32] = {};
-  for (int it = 0; it < iters; ++it) {
-#pragma unroll
-    for (int j = 0; j < kPeakChain32; ++j)
-      c[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c[j], 0, 0, 0, 120, 0, 130);
-  }
-  float r = 0.0f;
-#pragma unroll
-  for (int j = 0; j < kPeakChain32; ++j)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) r += c[j][i];
-  out[(int64_t)blockIdx.x * kPeakThreads + t] = r;
-}
-
-// LDS bank probe.  Every lane of 4 waves reads the 16 bytes at
-// lds_probe_addr(pattern, lane % 64) with ds_read_b128, 8 x iters times, from 16
-// KB of LDS holding word i = i * 0x9E3779B1, then writes the 4 words it read.
-// Patterns 1-5 are one MFMA operand fragment of a 16-row tile of 128-byte
-// rows: lane l reads row l % 16 at logical chunk 2 (l / 16) (pattern 2: the
-// chunk after it).
-constexpr int kLdsProbeThreads = 256;
-constexpr int kLdsProbeWords = 4096;
-__device__ __forceinline__ int lds_probe_addr(int pattern, int lane) {
-  const int r = lane & 15, c = (lane >> 4) * 2 + (pattern == 2 ? 1 : 0);
-  switch (pattern) {
-    case 0: return lane * 16;                                 // 1 KB in lane order
-    case 1:
-    case 2: return r * kBK + (swz(c, r) << 4);                // the GEMM's swizzle
-    case 3: return r * kBK + ((c ^ ((r >> 1) & 7)) << 4);     // chunk c ^ ((r / 2) % 8)
-    case 4: return r * kBK + ((c ^ (r & 7)) << 4);            // chunk c ^ (r % 8)
-    default: return r * kBK + (c << 4);                       // no swizzle
-  }
-}
-
-__global__ void __launch_bounds__(kLdsProbeThreads) lds_probe_kernel(int32_t* out, int pattern,
-                                                                     int iters) {
-  __shared__ __attribute__((aligned(1024))) int32_t words[kLdsProbeWords];
-  for (int i = threadIdx.x; i < kLdsProbeWords; i += kLdsProbeThreads)
-    words[i] = (int32_t)((uint32_t)i * 0x9E3779B1u);
-  __syncthreads();
-  const uint32_t a = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int32_t*)words +
-                     (uint32_t)lds_probe_addr(pattern, threadIdx.x & 63);
-  i32x4 v = {0, 0, 0, 0};
-  for (int it = 0; it < iters; ++it) {
-    i32x4 v0, v1, v2, v3, v4, v5, v6, v7;
-    asm volatile(
-        "ds_read_b128 %0, %8\n\t"
-        "ds_read_b128 %1, %8\n\t"
-        "ds_read_b128 %2, %8\n\t"
-        "ds_read_b128 %3, %8\n\t"
-        "ds_read_b128 %4, %8\n\t"
-        "ds_read_b128 %5, %8\n\t"
-        "ds_read_b128 %6, %8\n\t"
-        "ds_read_b128 %7, %8\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=v"(v0), "=v"(v1), "=v"(v2), "=v"(v3), "=v"(v4), "=v"(v5), "=v"(v6), "=v"(v7)
-        : "v"(a));
-    v = v0 & v1 & v2 & v3 & v4 & v5 & v6 & v7;   // all eight read the same bytes
-  }
-  i32x4* o = reinterpret_cast<i32x4*>(out) + (int64_t)blockIdx.x * kLdsProbeThreads + threadIdx.x;
-  *o = v;
-}
-
 }  // namespace
 }  // namespace gemm
 }  // namespace fagq
@@ -660,42 +555,6 @@ FAGQ_API int fagq_gemm_query_route(int64_t M, int64_t N, int64_t K, fagq_gemm_ro
   route->group_m = kGroupM;
   route->grid_blocks = ceil_div(M, kBM) * ceil_div(N, bn);
   return FAGQ_OK;
-}
-
-FAGQ_API int fagq_diag_mfma_peak(float* out, int64_t blocks, int32_t iters, void* stream) {
-  return fagq_diag_mfma_rate(out, blocks, iters, 0, stream);
-}
-
-FAGQ_API int fagq_diag_lds_read(int32_t* out, int64_t blocks, int32_t iters, int pattern,
-                                void* stream) {
-  if (!out) return FAGQ_E_NULL;
-  if (pattern < 0 || pattern > 5) return FAGQ_E_FORMAT;
-  if (blocks < 1 || iters < 1) return FAGQ_E_SHAPE;
-  if (blocks > (1 << 20) || iters > (1 << 20)) return FAGQ_E_TOO_LARGE;
-  if (!aligned(out, 16)) return FAGQ_E_ALIGN;
-  const int dc = device_check();
-  if (dc != FAGQ_OK) return dc;
-  int pt = pattern, it = iters;
-  void* args[] = {&out, &pt, &it};
-  return launch_kernel(reinterpret_cast<const void*>(&lds_probe_kernel), dim3((unsigned)blocks),
-                       dim3(kLdsProbeThreads), args, 0, static_cast<hipStream_t>(stream));
-}
-
-FAGQ_API int fagq_diag_mfma_rate(float* out, int64_t blocks, int32_t iters, int shape,
-                                 void* stream) {
-  if (!out) return FAGQ_E_NULL;
-  if (shape != 0 && shape != 1) return FAGQ_E_FORMAT;
-  if (blocks < 1 || iters < 1) return FAGQ_E_SHAPE;
-  if (blocks > (1 << 20) || iters > (1 << 20)) return FAGQ_E_TOO_LARGE;
-  if (!aligned(out, 4)) return FAGQ_E_ALIGN;
-  const int dc = device_check();
-  if (dc != FAGQ_OK) return dc;
-  int it = iters;
-  void* args[] = {&out, &it};
-  const void* k = shape == 0 ? reinterpret_cast<const void*>(&mfma_peak_kernel)
-                             : reinterpret_cast<const void*>(&mfma_peak32_kernel);
-  return launch_kernel(k, dim3((unsigned)blocks), dim3(kPeakThreads), args, 0,
-                       static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -40,3 +40,13 @@ def gpu(pkg):
     torch.cuda.set_device(dev)
     pkg.load_library()
     return dev
+
+
+@pytest.fixture(scope="session")
+def probe_lib(pkg):
+    # FAGQ_TEST_PROBE_LIBRARY: the sanitizer run's build of the probe library.
+    alt = os.environ.get("FAGQ_TEST_PROBE_LIBRARY")
+    if alt:
+        from fagq_mi355x import _lib
+        _lib._probe = _lib.load_probe(alt)
+    return pkg.load_probe_library()

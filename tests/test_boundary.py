@@ -1,6 +1,8 @@
-"""The C ABI boundary and the Python host layer, without a GPU: the library
-loads and exports everything include/*.h declares, the route table keeps its
-invariants, and every argument error is reported before any device work."""
+"""The C ABI boundary and the Python host layer, without a GPU: the libraries
+load and export everything include/*.h declares (libfagq_probe.so the
+measurement probes of fagq_probe.h, libfagq.so the rest), the route table
+keeps its invariants, and every argument error is reported before any device
+work."""
 import ctypes
 import math
 import re
@@ -13,9 +15,16 @@ REPO = Path(__file__).resolve().parents[1]
 HEADERS = sorted((REPO / "include").glob("*.h"))
 
 
-def declared_functions():
+PROBE_HEADER = "fagq_probe.h"
+
+
+def declared_functions(probe=None):
+    """FAGQ_API functions of every header; probe=True: fagq_probe.h only,
+    probe=False: every other header."""
     names = []
     for h in HEADERS:
+        if probe is not None and (h.name == PROBE_HEADER) != probe:
+            continue
         text = h.read_text()
         names += re.findall(r"FAGQ_API\s+[\w\s\*]+?\b(\w+)\s*\(", text)
     return names
@@ -27,12 +36,22 @@ def test_headers_declare_the_abi():
     assert len(names) == len(set(names))
 
 
-def test_library_exports_every_declared_symbol(pkg, lib):
+def test_library_exports_every_declared_symbol(pkg, lib, probe_lib):
     from fagq_mi355x import _lib
-    for name in declared_functions():
+    for name in declared_functions(probe=False):
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, name
-    assert set(_lib.SIGNATURES) == set(declared_functions())
+    assert set(_lib.SIGNATURES) == set(declared_functions(probe=False))
+    for name in declared_functions(probe=True):
+        assert hasattr(probe_lib, name), name
+        assert name in _lib.PROBE_SIGNATURES, name
+    assert set(_lib.PROBE_SIGNATURES) == set(declared_functions(probe=True))
+
+
+def test_probes_are_not_in_the_drop_in_library(lib):
+    # The measurement probes live in libfagq_probe.so only.
+    for name in declared_functions(probe=True):
+        assert not hasattr(lib, name), name
 
 
 def test_version_and_status_strings(lib):
@@ -226,35 +245,35 @@ def test_mapped_launch_rejects_bad_mappings(lib):
     assert mapped(7, 1, lds=65537) == 5
 
 
-def test_diag_validation(lib):
+def test_diag_validation(lib, probe_lib):
     assert lib.fagq_diag_encode(None, fake(1), 8, 1, 0, 1, None) == 1
     assert lib.fagq_diag_encode(fake(0), fake(1), 9, 1, 0, 1, None) == 2
     assert lib.fagq_diag_encode(fake(0), fake(1), 8, 1, 1, 1, None) == 5
     assert lib.fagq_diag_encode(fake(0), fake(1), 8, 1, 0, 2, None) == 5
     assert lib.fagq_diag_encode(fake(0), fake(1), 0, 1, 0, 0, None) == 0
-    assert lib.fagq_diag_copy(fake(0), fake(1), 15, None) == 2
-    assert lib.fagq_diag_copy(None, fake(1), 16, None) == 1
-    assert lib.fagq_diag_copy(fake(0), fake(1), 0, None) == 0
-    assert lib.fagq_diag_stream(fake(0), fake(1), 16, 4, None) == 5
-    assert lib.fagq_diag_stream(fake(0), fake(1), 16, 3, None) == 2   # opmix: bytes % 32
-    assert lib.fagq_diag_stream(None, fake(1), 16, 1, None) == 1     # read needs src
-    assert lib.fagq_diag_stream(fake(0), None, 16, 2, None) == 1
-    assert lib.fagq_diag_stream(None, fake(1), 0, 2, None) == 0      # write: src may be NULL
-    assert lib.fagq_diag_stream(fake(0), ctypes.c_void_p(BASE + 8), 16, 0, None) == 4
-    assert lib.fagq_diag_mfma_peak(None, 1, 1, None) == 1
-    assert lib.fagq_diag_mfma_peak(fake(0), 0, 1, None) == 2
-    assert lib.fagq_diag_mfma_peak(fake(0), 1, 0, None) == 2
-    assert lib.fagq_diag_mfma_rate(fake(0), 1, 1, 2, None) == 5
-    assert lib.fagq_diag_mfma_rate(None, 1, 1, 1, None) == 1
-    assert lib.fagq_diag_mfma_peak(fake(0), (1 << 20) + 1, 1, None) == 7
-    assert lib.fagq_diag_mfma_peak(ctypes.c_void_p(BASE + 2), 1, 1, None) == 4
-    assert lib.fagq_diag_lds_read(None, 1, 1, 0, None) == 1
-    assert lib.fagq_diag_lds_read(fake(0), 1, 1, 6, None) == 5
-    assert lib.fagq_diag_lds_read(fake(0), 1, 1, -1, None) == 5
-    assert lib.fagq_diag_lds_read(fake(0), 0, 1, 0, None) == 2
-    assert lib.fagq_diag_lds_read(fake(0), 1, 0, 0, None) == 2
-    assert lib.fagq_diag_lds_read(fake(0), 1, (1 << 20) + 1, 0, None) == 7
-    assert lib.fagq_diag_lds_read(ctypes.c_void_p(BASE + 8), 1, 1, 0, None) == 4
+    assert probe_lib.fagq_diag_copy(fake(0), fake(1), 15, None) == 2
+    assert probe_lib.fagq_diag_copy(None, fake(1), 16, None) == 1
+    assert probe_lib.fagq_diag_copy(fake(0), fake(1), 0, None) == 0
+    assert probe_lib.fagq_diag_stream(fake(0), fake(1), 16, 4, None) == 5
+    assert probe_lib.fagq_diag_stream(fake(0), fake(1), 16, 3, None) == 2   # opmix: bytes % 32
+    assert probe_lib.fagq_diag_stream(None, fake(1), 16, 1, None) == 1     # read needs src
+    assert probe_lib.fagq_diag_stream(fake(0), None, 16, 2, None) == 1
+    assert probe_lib.fagq_diag_stream(None, fake(1), 0, 2, None) == 0      # write: src may be NULL
+    assert probe_lib.fagq_diag_stream(fake(0), ctypes.c_void_p(BASE + 8), 16, 0, None) == 4
+    assert probe_lib.fagq_diag_mfma_peak(None, 1, 1, None) == 1
+    assert probe_lib.fagq_diag_mfma_peak(fake(0), 0, 1, None) == 2
+    assert probe_lib.fagq_diag_mfma_peak(fake(0), 1, 0, None) == 2
+    assert probe_lib.fagq_diag_mfma_rate(fake(0), 1, 1, 2, None) == 5
+    assert probe_lib.fagq_diag_mfma_rate(None, 1, 1, 1, None) == 1
+    assert probe_lib.fagq_diag_mfma_peak(fake(0), (1 << 20) + 1, 1, None) == 7
+    assert probe_lib.fagq_diag_mfma_peak(ctypes.c_void_p(BASE + 2), 1, 1, None) == 4
+    assert probe_lib.fagq_diag_lds_read(None, 1, 1, 0, None) == 1
+    assert probe_lib.fagq_diag_lds_read(fake(0), 1, 1, 6, None) == 5
+    assert probe_lib.fagq_diag_lds_read(fake(0), 1, 1, -1, None) == 5
+    assert probe_lib.fagq_diag_lds_read(fake(0), 0, 1, 0, None) == 2
+    assert probe_lib.fagq_diag_lds_read(fake(0), 1, 0, 0, None) == 2
+    assert probe_lib.fagq_diag_lds_read(fake(0), 1, (1 << 20) + 1, 0, None) == 7
+    assert probe_lib.fagq_diag_lds_read(ctypes.c_void_p(BASE + 8), 1, 1, 0, None) == 4
 
 
 # ----------------------------------------------------------------- Python layer

@@ -1,4 +1,4 @@
-"""The library's ceiling probes (include/fagq_diag.h) move and compute what
+"""The ceiling probes (libfagq_probe.so, include/fagq_probe.h) move and compute what
 their descriptions say, so the bandwidth and issue-rate figures bench.py prints
 for them are figures of that work: copy, write and the operator-mix stream on
 ragged sizes (a partial last workgroup), and both shapes of the MFMA probe."""
@@ -17,7 +17,7 @@ CHUNK = 512 * 16          # bytes one probe workgroup moves per stream
 
 def _stream(pkg, gpu, src, dst, nbytes, mode):
     from fagq_mi355x import _lib
-    lib = _lib.load()
+    lib = _lib.load_probe()
     st = lib.fagq_diag_stream(ctypes.c_void_p(src.data_ptr()) if src is not None else None,
                               ctypes.c_void_p(dst.data_ptr()), nbytes, mode,
                               ctypes.c_void_p(torch.cuda.current_stream(gpu).cuda_stream))
@@ -73,7 +73,7 @@ def test_mfma_rate_probe_shapes(pkg, gpu):
     bit from launch to launch (the operand bytes are arbitrary fp8 codes, NaN
     included: the probe measures issue rate, not values)."""
     from fagq_mi355x import _lib
-    lib = _lib.load()
+    lib = _lib.load_probe()
     note("case mfma rate probe, both shapes")
     outs = []
     for shape in (0, 1):
@@ -101,7 +101,7 @@ def _lds_probe_addr(pattern: int, lane: int) -> int:
 def test_lds_read_probe_addresses(pkg, gpu, pattern):
     """Every thread returns the four 32-bit words at its documented address."""
     from fagq_mi355x import _lib
-    lib = _lib.load()
+    lib = _lib.load_probe()
     note(f"case lds read probe pattern={pattern}")
     blocks = 3
     out = torch.full((blocks * 256 * 4,), -1, dtype=torch.int32, device=gpu)

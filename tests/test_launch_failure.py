@@ -32,7 +32,10 @@ def seam(pkg):
     import __graft_entry__ as ge
     from fagq_mi355x import _lib
     build = ge._load_module("fagq_mi355x_build", ge.PKG_DIR / "build.py")
-    return _lib.load(build.build_variant("launch_failure", defines=("FAGQ_TEST_LAUNCH_FAILURE",)))
+    lib = build.build_variant("launch_failure", defines=("FAGQ_TEST_LAUNCH_FAILURE",))
+    seam_lib = _lib.load(lib)
+    seam_lib.probe = _lib.load_probe(lib.parent / "libfagq_probe.so")
+    return seam_lib
 
 
 def test_operator_launch_failure_is_returned(seam):
@@ -57,7 +60,9 @@ def test_every_launching_entry_point_reports_it(seam):
         st = seam.fagq_launch_typed(fake(0), fake(1), fake(2), fake(3), fake(6), fake(4), fake(5),
                                     8, 4096, 128, 1e-6, 1, 0, 0, 0, act, res, None)
         assert st == -HIP_ERROR_LAUNCH_FAILURE, (act, res)
-    assert seam.fagq_diag_stream(fake(0), fake(1), 4096, 0, None) == -HIP_ERROR_LAUNCH_FAILURE
+    assert seam.probe.fagq_diag_stream(fake(0), fake(1), 4096, 0, None) == -HIP_ERROR_LAUNCH_FAILURE
+    assert seam.probe.fagq_diag_mfma_rate(fake(0), 1, 1, 0, None) == -HIP_ERROR_LAUNCH_FAILURE
+    assert seam.probe.fagq_diag_lds_read(fake(0), 1, 1, 0, None) == -HIP_ERROR_LAUNCH_FAILURE
     assert seam.fagq_diag_encode(fake(0), fake(1), 64, 1, 0, 0, None) == -HIP_ERROR_LAUNCH_FAILURE
     st = seam.fagq_dsa_topk_launch(fake(0), 0, fake(1), fake(2), fake(3), 0, fake(4), fake(5), 1, 2,
                                    4, 1024, 64, 32, None)

@@ -37,7 +37,7 @@ def test_cpu_tests_pass_under_asan_and_ubsan(pkg):
     orc = oracle_build.build_sanitized()
     runtime = build.sanitizer_runtime()
     # Both builds are instrumented (they call the sanitizers' report hooks).
-    for so in (lib, orc):
+    for so in (lib, lib.parent / "libfagq_probe.so", orc):
         syms = subprocess.run(["nm", "-D", str(so)], capture_output=True, text=True).stdout
         assert "__asan_report" in syms and "__ubsan_handle" in syms, so
     env = dict(os.environ)
@@ -49,6 +49,7 @@ def test_cpu_tests_pass_under_asan_and_ubsan(pkg):
                         "alloc_dealloc_mismatch=0",
         "UBSAN_OPTIONS": "halt_on_error=1:print_stacktrace=1",
         "FAGQ_TEST_LIBRARY": str(lib),
+        "FAGQ_TEST_PROBE_LIBRARY": str(lib.parent / "libfagq_probe.so"),
         "FAGQ_TEST_ORACLE_LIBRARY": str(orc),
     })
     r = subprocess.run([sys.executable, "-m", "pytest", "-x", "-q", "-p", "no:cacheprovider",
