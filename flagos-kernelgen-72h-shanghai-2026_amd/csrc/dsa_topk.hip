@@ -97,6 +97,7 @@ struct Lds {
   uint32_t kslot[kMaxWaves][2];     // per-wave max / min (ord_key)
   uint32_t uslot[2][kMaxWaves][4];  // per-wave partials of the refinement
   uint32_t ncur;                    // refinement scatter cursor
+  uint32_t bnd[2];                  // candidate count and boundary bin, from wave 0
 };
 constexpr int kZeroWords = kBins + 64;   // hist, cleared per row
 static_assert(kZeroWords % 4 == 0, "cleared with 16-byte stores");
@@ -509,8 +510,23 @@ dsa_topk_rows(const DArgs g) {
   }
   __syncthreads();
 
-  const Boundary bd = find_boundary<true>(lds, (uint32_t)K, lane, w == 0);
-  uint32_t nc = bd.total ? bd.above + bd.cnt : 0u;
+  // Wave 0 finds the boundary, stores above(b) and hands the candidate count
+  // and the boundary bin to the other waves.
+  uint32_t nc = 0, bstar = 1;
+  if (w == 0) {
+    const Boundary bd = find_boundary<true>(lds, (uint32_t)K, lane, true);
+    nc = bd.total ? bd.above + bd.cnt : 0u;
+    bstar = bd.bin > 1u ? bd.bin : 1u;
+    if (lane == 0) {
+      lds.bnd[0] = nc;
+      lds.bnd[1] = bstar;
+    }
+  }
+  __syncthreads();
+  if (w != 0) {
+    nc = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds.bnd[0]);
+    bstar = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds.bnd[1]);
+  }
   const bool refine = nc > CAP;
 
   if (!refine) {
@@ -518,8 +534,6 @@ dsa_topk_rows(const DArgs g) {
     // the non-selectable blocks, never qualifies); p < nc <= CAP.  The entry
     // holds the raw score bits and 0xffffffff - id; the scores become ordered
     // keys in one pass over the candidates below.
-    const uint32_t bstar = bd.bin > 1u ? bd.bin : 1u;
-    __syncthreads();                      // above(b) stored by wave 0
     auto scatter = [&](int wbase) {
       const uint32_t nid = 0xffffffffu - (uint32_t)(wbase + lbase);
 #pragma unroll
