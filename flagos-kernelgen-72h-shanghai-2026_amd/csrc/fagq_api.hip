@@ -215,13 +215,27 @@ int validate(const void* x, const void* residual, const void* gamma, const void*
   return FAGQ_OK;
 }
 
+// fagq_rows for bf16 tensors, or (f16) for the typed form's fp16 tensors.
 LaunchFn lookup(int q_format, int scale_format, int rounding, int lpg_idx, int steps, bool norm,
-                int mode) {
+                int mode, bool f16 = false) {
   const int qf = q_format == FAGQ_Q_FP8_E4M3FN ? QF_FP8
                  : rounding == FAGQ_ROUND_RNE  ? QF_I8_RNE
                                                : QF_I8_TRUNC;
   const bool ue = scale_format == FAGQ_SCALE_UE8M0;
   const int ri = mode;
+  if (f16) {
+    switch (qf) {
+      case QF_FP8:
+        return ue ? lookup_f16_q0_s1(lpg_idx, steps, norm, ri)
+                  : lookup_f16_q0_s0(lpg_idx, steps, norm, ri);
+      case QF_I8_RNE:
+        return ue ? lookup_f16_q1_s1(lpg_idx, steps, norm, ri)
+                  : lookup_f16_q1_s0(lpg_idx, steps, norm, ri);
+      default:
+        return ue ? lookup_f16_q2_s1(lpg_idx, steps, norm, ri)
+                  : lookup_f16_q2_s0(lpg_idx, steps, norm, ri);
+    }
+  }
   switch (qf) {
     case QF_FP8:
       return ue ? lookup_q0_s1(lpg_idx, steps, norm, ri) : lookup_q0_s0(lpg_idx, steps, norm, ri);
@@ -232,6 +246,7 @@ LaunchFn lookup(int q_format, int scale_format, int rounding, int lpg_idx, int s
   }
 }
 
+// fagq_rows_typed, family in [TF_BF16_R32, TF_F32] (fp16 tensors alone run fagq_rows).
 LaunchFn lookup_typed(int q_format, int scale_format, int rounding, int lpg_idx, int steps,
                       bool norm, int family) {
   const int qf = q_format == FAGQ_Q_FP8_E4M3FN ? QF_FP8
@@ -318,14 +333,14 @@ void fill_args(KArgs* a, const Mapping& m, const void* x, const void* residual, 
 int launch_with(const Mapping& m, const void* x, const void* residual, const void* gamma,
                 void* residual_out, void* norm_out, void* q, void* scale, int64_t M, int64_t D,
                 int64_t G, float eps, int q_format, int scale_format, int scale_layout,
-                int rounding, int remap, void* stream) {
+                int rounding, int remap, void* stream, bool f16 = false) {
   const int dc = device_check();
   if (dc != FAGQ_OK) return dc;
   KArgs a;
   fill_args(&a, m, x, residual, gamma, residual_out, norm_out, q, scale, M, D, G, eps,
             scale_format, scale_layout, remap);
   const LaunchFn fn = lookup(q_format, scale_format, rounding, lpg_index((int)G), m.ns,
-                             norm_out != nullptr, m.mode);
+                             norm_out != nullptr, m.mode, f16);
   return fn(a, dim3((unsigned)m.grid), dim3((unsigned)m.block), (unsigned)m.lds,
             static_cast<hipStream_t>(stream));
 }
@@ -361,6 +376,17 @@ FAGQ_API int fagq_launch_typed(const void* x, const void* residual, const void* 
                        q_format, scale_format, scale_layout, rounding, stream);
   const int tf = type_family(act_dtype, res_dtype);
   if (tf < 0) return FAGQ_E_FORMAT;
+  if (tf == TF_F16) {
+    // fp16 tensors: the bf16 operator's kernels and route, with fp16 elements.
+    const int v = validate(x, residual, gamma, residual_out, norm_out, q, scale, M, D, group_size,
+                           eps, q_format, scale_format, scale_layout, rounding);
+    if (v != FAGQ_OK || M == 0) return v;
+    Mapping m;
+    choose_mapping(M, (int)D, scale_format, scale_layout, &m);
+    return launch_with(m, x, residual, gamma, residual_out, norm_out, q, scale, M, D, group_size,
+                       eps, q_format, scale_format, scale_layout, rounding,
+                       remap_for(scale_layout, scale_format, m.rpb, m.mode), stream, true);
+  }
   const uintptr_t ba = act_dtype == FAGQ_DT_F32 ? 4 : 2, br = res_dtype == FAGQ_DT_F32 ? 4 : 2;
   const int v = validate(x, residual, gamma, residual_out, norm_out, q, scale, M, D, group_size,
                          eps, q_format, scale_format, scale_layout, rounding, ba, br);

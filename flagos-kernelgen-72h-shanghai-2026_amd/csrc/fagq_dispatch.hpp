@@ -49,8 +49,18 @@ LaunchFn lookup_q1_s1(int lpg_idx, int steps, bool norm, int mode);   // int8 rn
 LaunchFn lookup_q2_s0(int lpg_idx, int steps, bool norm, int mode);   // int8 trunc, f32
 LaunchFn lookup_q2_s1(int lpg_idx, int steps, bool norm, int mode);   // int8 trunc, ue8m0
 
-// Typed form (fagq_rows_typed): lookup_typed_q<code>_s<scale>(lpg index, steps
-// per wave in [1, 4], norm, type family).
+// Typed form, fp16 tensors (fagq_rows with ET_F16): lookup_f16_q<code>_s<scale>(lpg
+// index, steps per wave in [1, 4], norm, row-group mode).
+LaunchFn lookup_f16_q0_s0(int lpg_idx, int steps, bool norm, int mode);
+LaunchFn lookup_f16_q0_s1(int lpg_idx, int steps, bool norm, int mode);
+LaunchFn lookup_f16_q1_s0(int lpg_idx, int steps, bool norm, int mode);
+LaunchFn lookup_f16_q1_s1(int lpg_idx, int steps, bool norm, int mode);
+LaunchFn lookup_f16_q2_s0(int lpg_idx, int steps, bool norm, int mode);
+LaunchFn lookup_f16_q2_s1(int lpg_idx, int steps, bool norm, int mode);
+
+// Typed form, families with an fp32 tensor (fagq_rows_typed):
+// lookup_typed_q<code>_s<scale>(lpg index, steps per wave in [1, 4], norm, type
+// family in [TF_BF16_R32, TF_F32]).
 LaunchFn lookup_typed_q0_s0(int lpg_idx, int steps, bool norm, int family);
 LaunchFn lookup_typed_q0_s1(int lpg_idx, int steps, bool norm, int family);
 LaunchFn lookup_typed_q1_s0(int lpg_idx, int steps, bool norm, int family);

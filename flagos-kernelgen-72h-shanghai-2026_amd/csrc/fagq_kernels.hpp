@@ -143,6 +143,46 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, b);
 }
 
+// Element types of the operator's tensors.
+enum ElemType { ET_BF16 = 0, ET_F16 = 1, ET_F32 = 2 };
+
+__device__ __forceinline__ float f16_lo(uint32_t v) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xffffu));
+}
+__device__ __forceinline__ float f16_hi(uint32_t v) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+}
+
+// Two fp32 -> packed fp16x2, round to nearest even (v_cvt_pk_f16_f32).
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+  f32x2 v = {lo, hi};
+  f16x2 h = __builtin_convertvector(v, f16x2);
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+// The low / high element of a word holding two 16-bit elements of type E
+// (ET_BF16 or ET_F16) as fp32, and two fp32 values packed as E.
+template <int E>
+__device__ __forceinline__ float lo16(uint32_t v) {
+  static_assert(E == ET_BF16 || E == ET_F16, "16-bit element type");
+  if constexpr (E == ET_F16) return f16_lo(v);
+  else return bf16_lo(v);
+}
+template <int E>
+__device__ __forceinline__ float hi16(uint32_t v) {
+  static_assert(E == ET_BF16 || E == ET_F16, "16-bit element type");
+  if constexpr (E == ET_F16) return f16_hi(v);
+  else return bf16_hi(v);
+}
+template <int E>
+__device__ __forceinline__ uint32_t pack16(float lo, float hi) {
+  static_assert(E == ET_BF16 || E == ET_F16, "16-bit element type");
+  if constexpr (E == ET_F16) return pack_f16x2(lo, hi);
+  else return pack_bf16x2(lo, hi);
+}
+
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
@@ -385,9 +425,9 @@ __device__ __forceinline__ void load_gamma(const KArgs& a, const WaveCtx& w, int
 
 // Phase 2a for one row: r = x + residual into rw, the fp64 sum of squares, and
 // the residual_out stores (after every use of the loaded data).  xs holds x in
-// fp32 (one bf16 tensor, or the fp32 sum of the partial tensors in the
-// multi-input form).
-template <int NS>
+// fp32 (one 16-bit tensor, or the fp32 sum of the partial tensors in the
+// multi-input form); residual and residual_out have element type E16.
+template <int NS, int E16 = ET_BF16>
 __device__ __forceinline__ double row_sum(const RowRsrc& rr, int lane, const float (&xs)[NS][8],
                                           const u32x4 (&rv)[NS], float (&rw)[NS][8]) {
   double ss = 0.0;
@@ -396,8 +436,8 @@ __device__ __forceinline__ double row_sum(const RowRsrc& rr, int lane, const flo
   for (int k = 0; k < NS; ++k) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      rw[k][2 * j] = xs[k][2 * j] + bf16_lo(rv[k][j]);
-      rw[k][2 * j + 1] = xs[k][2 * j + 1] + bf16_hi(rv[k][j]);
+      rw[k][2 * j] = xs[k][2 * j] + lo16<E16>(rv[k][j]);
+      rw[k][2 * j + 1] = xs[k][2 * j + 1] + hi16<E16>(rv[k][j]);
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -405,7 +445,7 @@ __device__ __forceinline__ double row_sum(const RowRsrc& rr, int lane, const flo
       ss = __builtin_fma(rd, rd, ss);   // r^2 is exact in fp64
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) ro[k][j] = pack_bf16x2(rw[k][2 * j], rw[k][2 * j + 1]);
+    for (int j = 0; j < 4; ++j) ro[k][j] = pack16<E16>(rw[k][2 * j], rw[k][2 * j + 1]);
   }
 #pragma unroll
   for (int k = 0; k < NS; ++k)
@@ -415,15 +455,15 @@ __device__ __forceinline__ double row_sum(const RowRsrc& rr, int lane, const flo
 
 // Phase 2b: w = r * gamma in place (rw holds r on entry, w on exit) and the
 // group maxima of |w|.
-template <int NS, int LPG>
+template <int NS, int LPG, int E16 = ET_BF16>
 __device__ __forceinline__ void row_weight(float (&rw)[NS][8], const u32x4 (&gv)[NS],
                                            uint32_t (&gmax)[NS]) {
 #pragma unroll
   for (int k = 0; k < NS; ++k) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      rw[k][2 * j] = rw[k][2 * j] * bf16_lo(gv[k][j]);
-      rw[k][2 * j + 1] = rw[k][2 * j + 1] * bf16_hi(gv[k][j]);
+      rw[k][2 * j] = rw[k][2 * j] * lo16<E16>(gv[k][j]);
+      rw[k][2 * j + 1] = rw[k][2 * j + 1] * hi16<E16>(gv[k][j]);
     }
     float m = 0.0f;
 #pragma unroll
@@ -432,14 +472,14 @@ __device__ __forceinline__ void row_weight(float (&rw)[NS][8], const u32x4 (&gv)
   }
 }
 
-template <int NS>
+template <int NS, int E16 = ET_BF16>
 __device__ __forceinline__ void unpack_x(const u32x4 (&xv)[NS], float (&xs)[NS][8]) {
 #pragma unroll
   for (int k = 0; k < NS; ++k)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      xs[k][2 * j] = bf16_lo(xv[k][j]);
-      xs[k][2 * j + 1] = bf16_hi(xv[k][j]);
+      xs[k][2 * j] = lo16<E16>(xv[k][j]);
+      xs[k][2 * j + 1] = hi16<E16>(xv[k][j]);
     }
 }
 
@@ -509,15 +549,16 @@ __device__ __forceinline__ float group_scale(uint32_t gmax_bits, float inv_q, in
 
 // ---------------------------------------------------------------- element types
 
-// Element types of the tensors around the operator.  The bf16 kernel
-// (fagq_rows) reads and writes bf16 only; the typed kernel (fagq_rows_typed)
-// takes one element type for the activation tensors (x, gamma, norm_out) and
-// one for the residual stream (residual, residual_out), and converts every
-// load to fp32 and every store from fp32 (round to nearest even), as the
-// reference's kernels do (task01.py:88-89, :93-94 loads; :91, :118 stores).
-enum ElemType { ET_BF16 = 0, ET_F16 = 1, ET_F32 = 2 };
+// Element types of the tensors around the operator.  fagq_rows reads and
+// writes one 16-bit type (bf16, or fp16 for the typed form's fp16 family);
+// the typed kernel (fagq_rows_typed) serves the families with an fp32 tensor:
+// one element type for the activation tensors (x, gamma, norm_out) and one for
+// the residual stream (residual, residual_out).  Both convert every load to
+// fp32 and every store from fp32 (round to nearest even), as the reference's
+// kernels do (task01.py:88-89, :93-94 loads; :91, :118 stores).
 
-// Type families of the typed kernel: (activation type, residual-stream type).
+// Type families of the typed form: (activation type, residual-stream type).
+// TF_F16 runs fagq_rows<..., ET_F16>, the others fagq_rows_typed.
 enum TypeFamily { TF_F16 = 0, TF_BF16_R32 = 1, TF_F16_R32 = 2, TF_F32 = 3 };
 constexpr int kNumTypeFamilies = 4;
 
@@ -586,13 +627,6 @@ __device__ __forceinline__ void lane_order(Vec8<ET>& p, int lane, Stage& st) {
   }
 }
 
-__device__ __forceinline__ float f16_lo(uint32_t v) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xffffu));
-}
-__device__ __forceinline__ float f16_hi(uint32_t v) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
-}
-
 template <int ET>
 __device__ __forceinline__ void unpack_elems8(const Vec8<ET>& p, float (&f)[8]) {
 #pragma unroll
@@ -608,15 +642,6 @@ __device__ __forceinline__ void unpack_elems8(const Vec8<ET>& p, float (&f)[8]) 
       f[4 + j] = __uint_as_float(p.v[1][j]);
     }
   }
-}
-
-// Two fp32 -> packed fp16x2, round to nearest even.
-__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
-  typedef float f32x2 __attribute__((ext_vector_type(2)));
-  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-  f32x2 v = {lo, hi};
-  f16x2 h = __builtin_convertvector(v, f16x2);
-  return __builtin_bit_cast(uint32_t, h);
 }
 
 // Stores a lane's 8 fp32 values of step k as ET (streaming stores); fp32
@@ -732,7 +757,9 @@ __device__ __forceinline__ void row_scale(double ss, const KArgs& a, int wave, i
 //     stores each group's rpb consecutive column-major words with one store.
 //     A workgroup whose rows would pass M, or a call whose scale pointer or M
 //     does not allow the wide alignment (wide_ok == 0), stores row by row.
-template <int NS, int LPG, int QF, int SF, bool NORM, int MODE>
+// E16: element type of x, residual, gamma, residual_out and norm_out
+// (ET_BF16, or ET_F16 for the typed form's fp16 tensors).
+template <int NS, int LPG, int QF, int SF, bool NORM, int MODE, int E16 = ET_BF16>
 __global__ void __launch_bounds__(1024)
 fagq_rows(const KArgs a) {
   static_assert(NS >= 1 && NS <= kMaxStepsPerWave, "steps per wave");
@@ -782,8 +809,8 @@ fagq_rows(const KArgs a) {
   double ss;
   {
     float xs[NS][8];
-    unpack_x<NS>(xv, xs);
-    ss = row_sum<NS>(rr, lane, xs, rv, w);
+    unpack_x<NS, E16>(xv, xs);
+    ss = row_sum<NS, E16>(rr, lane, xs, rv, w);
   }
   auto publish_gmax = [&](int rg) {
     if ((lane & (LPG - 1)) == 0) {
@@ -795,7 +822,7 @@ fagq_rows(const KArgs a) {
     }
   };
   if (gamma_loader) {
-    row_weight<NS, LPG>(w, gv, gmax);
+    row_weight<NS, LPG, E16>(w, gv, gmax);
     if constexpr (SHARED) {
 #pragma unroll
       for (int k = 0; k < NS; ++k) s_gamma[(part * NS + k) * 64 + lane] = gv[k];
@@ -815,7 +842,7 @@ fagq_rows(const KArgs a) {
     if (SHARED && !gamma_loader) {
 #pragma unroll
       for (int k = 0; k < NS; ++k) gv[k] = s_gamma[(part * NS + k) * 64 + lane];
-      row_weight<NS, LPG>(w, gv, gmax);
+      row_weight<NS, LPG, E16>(w, gv, gmax);
       if constexpr (WIDE) publish_gmax(rib);
     }
     if (part == 0) {
@@ -839,7 +866,7 @@ fagq_rows(const KArgs a) {
     const int R = a.rpb();
     const bool wide = a.wide_ok() && row0 + R <= a.M;
     if (wide) {
-      row_out<NS, LPG, QF, SF, NORM, false>(rr, lane, (uint32_t)wc.gl, w, gmax, inv, inv_q);
+      row_out<NS, LPG, QF, SF, NORM, false, E16>(rr, lane, (uint32_t)wc.gl, w, gmax, inv, inv_q);
       if (rib == 0 && (lane & (LPG - 1)) == 0) {
         // Scale words g * M + row0 .. + R - 1, offsets below M * groups * sb.
         const rsrc_t rs = make_rsrc(a.scale, (uint32_t)((int64_t)a.M * a.groups * sb));
@@ -874,10 +901,10 @@ fagq_rows(const KArgs a) {
         }
       }
     } else {
-      row_out<NS, LPG, QF, SF, NORM>(rr, lane, (uint32_t)wc.gl, w, gmax, inv, inv_q);
+      row_out<NS, LPG, QF, SF, NORM, true, E16>(rr, lane, (uint32_t)wc.gl, w, gmax, inv, inv_q);
     }
   } else {
-    row_out<NS, LPG, QF, SF, NORM>(rr, lane, (uint32_t)wc.gl, w, gmax, inv, inv_q);
+    row_out<NS, LPG, QF, SF, NORM, true, E16>(rr, lane, (uint32_t)wc.gl, w, gmax, inv, inv_q);
   }
 }
 
@@ -930,13 +957,15 @@ fagq_rows_parts(const PArgs pa) {
   row_out<NS, LPG, QF, SF, false>(rr, lane, (uint32_t)wc.gl, w, gmax, inv, inv_q);
 }
 
-// Typed form (fagq_launch_typed): the operator with activation tensors (x,
-// gamma, norm_out) of element type Family<TF>::A and a residual stream
-// (residual, residual_out) of type Family<TF>::R, each converted to fp32 on
-// load and rounded to nearest even on store; the arithmetic from r = x +
-// residual on is the bf16 kernel's, operation for operation.  Row groups are
-// independent (each wave loads its own gamma slice, each row stores its own
-// scales); the element sizes set the descriptors and offsets.
+// Typed form (fagq_launch_typed) for the families with an fp32 tensor: the
+// operator with activation tensors (x, gamma, norm_out) of element type
+// Family<TF>::A and a residual stream (residual, residual_out) of type
+// Family<TF>::R, each converted to fp32 on load and rounded to nearest even on
+// store; the arithmetic from r = x + residual on is the bf16 kernel's,
+// operation for operation.  Row groups are independent (each wave loads its
+// own gamma slice, each row stores its own scales); the element sizes set the
+// descriptors and offsets.  (TF_F16 would also compile here; it runs
+// fagq_rows with fp16 elements instead, with the bf16 operator's route.)
 template <int NS, int LPG, int QF, int SF, bool NORM, int TF>
 __global__ void __launch_bounds__(1024)
 fagq_rows_typed(const KArgs a) {

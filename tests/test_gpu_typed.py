@@ -70,9 +70,10 @@ def run(pkg, dev, x, r, w, G=128, fmt="fp8", ue8m0=False, col=False, with_norm=F
     return st
 
 
-# Shapes reaching every steps-per-wave count of the typed route: decode rows
-# (M < 1024) take 1-step waves up to D = 8192, then ceil(D / 8192) steps;
-# prefill rows take 1 step at 5..8 steps per row and 2 otherwise.
+# Shapes reaching every steps-per-wave count of the typed route (the families
+# with an fp32 tensor): decode rows (M < 1024) take 1-step waves up to
+# D = 8192, then ceil(D / 8192) steps; prefill rows take 1 step at 5..8 steps
+# per row and 2 otherwise.  fp16 tensors take the bf16 operator's route.
 @pytest.mark.parametrize("at,rt", PAIRS)
 @pytest.mark.parametrize("M,D", [(7, 4096), (5, 16384), (3, 24576), (2, 32768), (1024, 4096),
                                  (1024, 7168), (33, 1536)])
@@ -88,6 +89,22 @@ def test_typed_shapes(pkg, gpu, at, rt, M, D):
 def test_typed_format_matrix(pkg, gpu, at, rt, G, fmt, ue8m0, col):
     x, r, w = make(37, 3072, at, rt, seed=G, scale=2.0)
     run(pkg, gpu, x, r, w, G, fmt, ue8m0, col, with_norm=(G == 128), label="format")
+
+
+# fp16 tensors run the bf16 operator's kernels with fp16 elements and its
+# route, row-group modes included: 2 rows per workgroup sharing gamma, with the
+# column-major scales of both rows stored together (mode 2), and independent
+# rows (mode 0); M = 2049 leaves a last workgroup with one row.
+@pytest.mark.parametrize("M,D,ue8m0,col,mode", [(2048, 7168, False, True, 2),
+                                                (2049, 7168, True, True, 2),
+                                                (2048, 7168, False, False, 0),
+                                                (4096, 4096, True, True, 0)])
+def test_f16_route_modes(pkg, gpu, M, D, ue8m0, col, mode):
+    from fagq_mi355x import _lib
+    route = _lib.query_route(M, D, 128, 1 if ue8m0 else 0, 1 if col else 0)
+    assert route["row_group_mode"] == mode, route
+    x, r, w = make(M, D, torch.float16, torch.float16, seed=M + D)
+    run(pkg, gpu, x, r, w, ue8m0=ue8m0, col=col, with_norm=True, label=f"f16 mode {mode}")
 
 
 @pytest.mark.parametrize("at,rt", PAIRS)
