@@ -12,7 +12,8 @@
 // (up to 16 waves); a lane holds 16 scores in VGPRs, loaded through a buffer
 // descriptor sized to the row's valid prefix, so blocks past it are never
 // fetched, and waves wholly past the prefix exit at once (a workgroup barrier
-// waits only for the waves still running).  Rows whose base is 16-byte
+// waits only for the waves still running); for top_k > 256 they stay idle
+// until the rank phase and share its candidates.  Rows whose base is 16-byte
 // aligned (scores pointer aligned and NB * element size a multiple of 16) are
 // read as 16-byte vectors, other rows one score per load.  A row of more than
 // 16 chunks (NB > 16384) is walked in chunks of 16 x 1024 blocks, each wave
@@ -398,7 +399,14 @@ dsa_topk_rows(const DArgs g) {
   }
   const int nchunk = nvalid > kChunk ? (nvalid + kChunk - 1) / kChunk : 1;
   const int nwv = nchunk < (int)(blockDim.x >> 6) ? nchunk : (int)(blockDim.x >> 6);  // waves with work
-  if (w >= nwv) return;
+  // top_k > kSmallTopK: the waves past the prefix stay for the rank phase,
+  // where the candidates (up to CAP) outnumber the live waves' lanes; they
+  // skip the score, histogram and scatter work (their chunks lie wholly past
+  // the prefix) and take part in every barrier.  For smaller top_k they
+  // leave at once.
+  constexpr bool KEEP = CAP != kCapSmall && !MULTI;
+  const bool live = w < nwv;
+  if (!KEEP && !live) return;
 
   if (w == 0) {
     u32x4* z = reinterpret_cast<u32x4*>(lds.hist);
@@ -438,7 +446,7 @@ dsa_topk_rows(const DArgs g) {
       vmin = fminf(vmin, lo);
       vmax = fmaxf(vmax, hi);
     });
-  } else {
+  } else if (live) {
     // Every load is issued before the full / partial split.
     u32x4 raw[kEPL / VEC];
     load_chunk<BF16, VECLD>(rs, wbase0, lane, raw);
@@ -504,7 +512,7 @@ dsa_topk_rows(const DArgs g) {
       hist(BoolC<false>());
       (void)full;
     });
-  } else {
+  } else if (live) {
     make_bins();
     hist_rt(full0);
   }
@@ -556,7 +564,7 @@ dsa_topk_rows(const DArgs g) {
         scatter(wbase);
       });
     } else {
-      scatter(wbase0);
+      if (live) scatter(wbase0);
     }
   } else {
     // Radix refinement on the composite key over [lo, hi]: found blocks lie
@@ -653,7 +661,7 @@ dsa_topk_rows(const DArgs g) {
   }
   __syncthreads();
 
-  const int stride = 64 * nwv;
+  const int stride = KEEP ? (int)blockDim.x : 64 * nwv;
   const int t = w * 64 + lane;
   if (!refine) {
     for (uint32_t i = (uint32_t)t; i < nc; i += (uint32_t)stride) {
