@@ -1,5 +1,5 @@
 """The CPU tests of the host code under AddressSanitizer and
-UndefinedBehaviorSanitizer (SURVEY.md §5).
+UndefinedBehaviorSanitizer.
 
 The library is rebuilt with both sanitizers on every host function (argument
 validation, route table, host-side diagnostics; device code as usual) and
