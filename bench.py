@@ -410,7 +410,7 @@ def main() -> int:
     traffic = measured_traffic(name)
 
     route = pkg.route_for(w.M, w.D, w.group_size, scale_ue8m0=w.scale_ue8m0,
-                          scale_col_major=w.scale_col_major)
+                          scale_col_major=w.scale_col_major, x_dtype=w.act, residual_dtype=w.res)
     out = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -530,6 +530,10 @@ def route_sweep(args, torch, pkg, w) -> int:
     import ctypes
     from fagq_mi355x import _lib
     from fagq_mi355x.workloads import make_inputs
+    if w.act != torch.bfloat16 or w.res != torch.bfloat16:
+        print("bench.py: --route-sweep times fagq_launch_mapped, which takes bf16 tensors only",
+              file=sys.stderr)
+        return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream(dev)

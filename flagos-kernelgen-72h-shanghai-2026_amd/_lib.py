@@ -61,6 +61,7 @@ SIGNATURES = {
     "fagq_launch_parts": ([_P, _I] + [_P] * 5 + [_I64, _I64, _I64, _F, _I, _I, _I, _I, _P], _I),
     "fagq_launch_mapped": ([_P] * 7 + [_I64, _I64, _I64, _F] + [_I] * 9 + [_P], _I),
     "fagq_query_route": ([_I64, _I64, _I64, _I, _I, ctypes.POINTER(Route)], _I),
+    "fagq_query_route_typed": ([_I64, _I64, _I64, _I, _I, _I, _I, ctypes.POINTER(Route)], _I),
     "fagq_status_string": ([_I], ctypes.c_char_p),
     "fagq_version": ([], _I),
     "fagq_diag_encode": ([_P, _P, _I64, _I, _I, _I, _P], _I),
@@ -182,8 +183,16 @@ def check(status: int, what: str = "fagq_launch") -> None:
 
 
 def query_route(M: int, D: int, group_size: int, scale_format: int = SCALE_F32,
-                scale_layout: int = LAYOUT_ROW_MAJOR) -> dict:
+                scale_layout: int = LAYOUT_ROW_MAJOR, act_dtype: int | None = None,
+                res_dtype: int | None = None) -> dict:
+    """The route of fagq_launch, or of fagq_launch_typed when element types are given."""
     r = Route()
-    check(load().fagq_query_route(M, D, group_size, scale_format, scale_layout, ctypes.byref(r)),
-          "fagq_query_route")
+    if act_dtype is None and res_dtype is None:
+        check(load().fagq_query_route(M, D, group_size, scale_format, scale_layout,
+                                      ctypes.byref(r)), "fagq_query_route")
+    else:
+        act = DT_BF16 if act_dtype is None else act_dtype
+        res = act if res_dtype is None else res_dtype
+        check(load().fagq_query_route_typed(M, D, group_size, scale_format, scale_layout, act, res,
+                                            ctypes.byref(r)), "fagq_query_route_typed")
     return {f: getattr(r, f) for f, _ in Route._fields_ if f != "reserved"}

@@ -471,6 +471,13 @@ FAGQ_API int fagq_launch_parts(const void* const* x_parts, int nparts, const voi
 
 FAGQ_API int fagq_query_route(int64_t M, int64_t D, int64_t group_size, int scale_format,
                                int scale_layout, fagq_route* route) {
+  return fagq_query_route_typed(M, D, group_size, scale_format, scale_layout, FAGQ_DT_BF16,
+                                FAGQ_DT_BF16, route);
+}
+
+FAGQ_API int fagq_query_route_typed(int64_t M, int64_t D, int64_t group_size, int scale_format,
+                                    int scale_layout, int act_dtype, int res_dtype,
+                                    fagq_route* route) {
   if (!route) return FAGQ_E_NULL;
   if (group_size != 64 && group_size != 128 && group_size != 256) return FAGQ_E_GROUP;
   if (M < 0 || D <= 0 || D % group_size != 0) return FAGQ_E_SHAPE;
@@ -478,8 +485,14 @@ FAGQ_API int fagq_query_route(int64_t M, int64_t D, int64_t group_size, int scal
   if (scale_format != FAGQ_SCALE_F32 && scale_format != FAGQ_SCALE_UE8M0) return FAGQ_E_FORMAT;
   if (scale_layout != FAGQ_LAYOUT_ROW_MAJOR && scale_layout != FAGQ_LAYOUT_COL_MAJOR)
     return FAGQ_E_FORMAT;
+  const bool bf16 = act_dtype == FAGQ_DT_BF16 && res_dtype == FAGQ_DT_BF16;
+  const int tf = bf16 ? -1 : type_family(act_dtype, res_dtype);
+  if (!bf16 && tf < 0) return FAGQ_E_FORMAT;
+  // fagq_launch_typed: bf16 and fp16 tensors take the operator's route, the
+  // families with an fp32 tensor the typed kernel's default mapping.
   Mapping m;
-  choose_mapping(M, (int)D, scale_format, scale_layout, &m);
+  if (bf16 || tf == TF_F16) choose_mapping(M, (int)D, scale_format, scale_layout, &m);
+  else default_mapping(M, (int)D, &m);
   route->waves_per_row = m.wpr;
   route->steps_per_wave = m.ns;
   route->rows_per_block = m.rpb;

@@ -355,8 +355,16 @@ def fused_reduce_add_rmsnorm_group_quant(
 
 
 def route_for(M: int, D: int, group_size: int = 128, *, scale_ue8m0: bool = False,
-              scale_col_major: bool = False) -> dict:
-    """The launch mapping the library chooses for a shape and scale format."""
-    return _lib.query_route(M, D, group_size,
-                            _lib.SCALE_UE8M0 if scale_ue8m0 else _lib.SCALE_F32,
-                            _lib.LAYOUT_COL_MAJOR if scale_col_major else _lib.LAYOUT_ROW_MAJOR)
+              scale_col_major: bool = False, x_dtype: torch.dtype = torch.bfloat16,
+              residual_dtype: torch.dtype | None = None) -> dict:
+    """The launch mapping the library chooses for a shape, scale format and
+    element types (x / gamma / norm_out, residual / residual_out; the
+    residual stream defaults to x's type)."""
+    rt = x_dtype if residual_dtype is None else residual_dtype
+    if x_dtype not in _DT_CODE or rt not in _DT_CODE:
+        raise TypeError(f"unsupported (x, residual) dtypes ({x_dtype}, {rt})")
+    sf = _lib.SCALE_UE8M0 if scale_ue8m0 else _lib.SCALE_F32
+    layout = _lib.LAYOUT_COL_MAJOR if scale_col_major else _lib.LAYOUT_ROW_MAJOR
+    if x_dtype is torch.bfloat16 and rt is torch.bfloat16:
+        return _lib.query_route(M, D, group_size, sf, layout)
+    return _lib.query_route(M, D, group_size, sf, layout, _DT_CODE[x_dtype], _DT_CODE[rt])

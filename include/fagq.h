@@ -190,6 +190,14 @@ typedef struct fagq_route {
 FAGQ_API int fagq_query_route(int64_t M, int64_t D, int64_t group_size, int scale_format,
                               int scale_layout, fagq_route* route);
 
+/* The route fagq_launch_typed takes for an element-type pair: fagq_launch's
+ * for (BF16, BF16) and (F16, F16); for the pairs with an fp32 tensor, the
+ * typed kernel's (independent rows, row_group_mode 0).  Other pairs
+ * FAGQ_E_FORMAT.  Never touches the device. */
+FAGQ_API int fagq_query_route_typed(int64_t M, int64_t D, int64_t group_size, int scale_format,
+                                    int scale_layout, int act_dtype, int res_dtype,
+                                    fagq_route* route);
+
 /* Static description of a status code; never NULL. */
 FAGQ_API const char* fagq_status_string(int status);
 

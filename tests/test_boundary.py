@@ -116,6 +116,52 @@ def test_route_rejects_bad_shapes(lib, args, status):
     from fagq_mi355x import _lib
     r = _lib.Route()
     assert lib.fagq_query_route(*args, ctypes.byref(r)) == status
+    # The typed query validates the shape the same way, before the dtypes.
+    assert lib.fagq_query_route_typed(*args, 2, 2, ctypes.byref(r)) == status
+
+
+TYPED_PAIRS = [(torch.float16, torch.float16), (torch.bfloat16, torch.float32),
+               (torch.float16, torch.float32), (torch.float32, torch.float32)]
+
+
+@pytest.mark.parametrize("M,D", [(1, 4096), (32, 8192), (4096, 4096), (8192, 5120),
+                                 (16384, 7168), (16384, 16384)])
+@pytest.mark.parametrize("at,rt", TYPED_PAIRS)
+@pytest.mark.parametrize("ue8m0,col", [(False, False), (False, True), (True, True)])
+def test_typed_routes(pkg, M, D, at, rt, ue8m0, col):
+    """fp16 tensors take the bf16 operator's route; the pairs with an fp32
+    tensor take the typed kernel's default mapping: independent rows, one row
+    per workgroup when a row has 4 or more waves, and 1-step waves for
+    prefill rows of 5-8 steps, 2-step waves otherwise (1 for decode)."""
+    r = pkg.route_for(M, D, 128, scale_ue8m0=ue8m0, scale_col_major=col, x_dtype=at,
+                      residual_dtype=rt)
+    bf16 = pkg.route_for(M, D, 128, scale_ue8m0=ue8m0, scale_col_major=col)
+    if at is torch.float16 and rt is torch.float16:
+        assert r == bf16
+        return
+    steps = math.ceil(D / 512)
+    prefill = M >= 1024
+    ns = (1 if 5 <= steps <= 8 else 2) if prefill else 1
+    ns = min(max(ns, math.ceil(steps / 16)), steps)
+    wpr = math.ceil(steps / ns)
+    rpb = 1 if wpr >= 4 else 4 // wpr
+    assert (r["waves_per_row"], r["steps_per_wave"], r["rows_per_block"], r["row_group_mode"]) == \
+        (wpr, ns, rpb, 0)
+    assert r["block_threads"] == 64 * wpr * rpb
+    assert r["grid_blocks"] == math.ceil(M / rpb)
+    assert r["lds_bytes"] == (36864 if prefill and ns == 2 and rpb == 1 and 9 <= steps <= 11 else 0)
+
+
+def test_typed_route_rejects_unknown_pairs(lib):
+    from fagq_mi355x import _lib
+    r = _lib.Route()
+    # (fp32 x, bf16 residual) and out-of-range codes are not element-type pairs.
+    for at, rt in ((2, 0), (2, 1), (0, 1), (1, 0), (3, 3), (-1, 0)):
+        assert lib.fagq_query_route_typed(4096, 4096, 128, 0, 0, at, rt, ctypes.byref(r)) == 5
+    assert lib.fagq_query_route_typed(4096, 4096, 128, 0, 0, 0, 0, None) == 1
+    with pytest.raises(TypeError):
+        import fagq_mi355x
+        fagq_mi355x.route_for(64, 4096, x_dtype=torch.int8)
 
 
 # Fake, aligned, non-overlapping device addresses: validation never dereferences them.
