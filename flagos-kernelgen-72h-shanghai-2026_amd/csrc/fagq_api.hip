@@ -293,15 +293,29 @@ int parts_steps() {
   return v;
 }
 
-// The multi-input form's mapping: FAGQ_PARTS_STEPS (default 2; 1 measured
-// 5 % slower at D = 7168) steps per wave, 2 whenever the row would need more
-// than 16 waves; one row per row group; small rows share a workgroup as in
-// choose_mapping.
-void choose_mapping_parts(int64_t M, int D, Mapping* m) {
+// The multi-input form's mapping, one row per row group (small rows share a
+// workgroup as in choose_mapping):
+// * at least 6 partials and 12..16 steps (6144 < D <= 8192): 4-step waves,
+//   each holding 4 KB of every partial in flight, 2 waves per SIMD.  Medians
+//   of interleaved runs at D = 7168, against 2-step waves: 2048 rows with 8
+//   partials 51.7 against 52.9 us, with 6 partials 41.9 against 42.6; 4096
+//   rows with 8 partials 100.5 against 102.6; 1024 rows 27.2 against 27.7.
+//   With 4 partials even (61.6 against 61.8 us at 4096 rows), with 2 or 1
+//   slower (88.5 against 84.7 at 8192 rows, 139.4 against 137.0 at 16384);
+//   3-step waves (5 per row, 3 waves per SIMD) slower everywhere (60.7 us
+//   at 2048 rows with 8 partials).
+// * otherwise FAGQ_PARTS_STEPS (default 2; 1 measured 5 % slower at D =
+//   7168) steps per wave, 2 whenever the row would need more than 16 waves.
+void choose_mapping_parts(int64_t M, int D, int nparts, Mapping* m) {
   const int steps = ceil_div(D, kStepCols);
-  int ns = parts_steps() >= kMaxStepsParts ? kMaxStepsParts : 1;
-  if (ceil_div(steps, ns) > kMaxWavesPerBlock) ns = kMaxStepsParts;
-  if (ns > steps) ns = steps;
+  int ns;
+  if (nparts >= 6 && steps >= 12 && steps <= 16) {
+    ns = 4;
+  } else {
+    ns = parts_steps() >= 2 ? 2 : 1;
+    if (ceil_div(steps, ns) > kMaxWavesPerBlock) ns = 2;
+    if (ns > steps) ns = steps;
+  }
   const int wpr = ceil_div(steps, ns);
   const int rpb = wpr >= 4 ? 1 : 4 / wpr;
   finish_mapping(M, D, wpr, rpb, RG_INDEPENDENT, 0, m);
@@ -455,7 +469,7 @@ FAGQ_API int fagq_launch_parts(const void* const* x_parts, int nparts, const voi
   const int dc = device_check();
   if (dc != FAGQ_OK) return dc;
   Mapping m;
-  choose_mapping_parts(M, (int)D, &m);
+  choose_mapping_parts(M, (int)D, nparts, &m);
   PArgs a;
   fill_args(&a.k, m, x_parts[0], residual, gamma, residual_out, nullptr, q, scale, M, D,
             group_size, eps, scale_format, scale_layout,

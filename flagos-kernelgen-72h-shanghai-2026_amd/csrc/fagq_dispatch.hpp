@@ -69,7 +69,7 @@ LaunchFn lookup_typed_q2_s0(int lpg_idx, int steps, bool norm, int family);
 LaunchFn lookup_typed_q2_s1(int lpg_idx, int steps, bool norm, int family);
 
 // Multi-input form (fagq_rows_parts): lookup_parts_q<code>_s<scale>(lpg index,
-// steps per wave in [1, kMaxStepsParts]).
+// steps per wave 1, 2 or 4).
 PartsLaunchFn lookup_parts_q0_s0(int lpg_idx, int steps);
 PartsLaunchFn lookup_parts_q0_s1(int lpg_idx, int steps);
 PartsLaunchFn lookup_parts_q1_s0(int lpg_idx, int steps);

@@ -55,14 +55,15 @@ LaunchFn FAGQ_LOOKUP(FAGQ_QF, FAGQ_SF)(int lpg_idx, int steps, bool norm, int mo
   return table[lpg_idx][steps - 1][norm ? 1 : 0][mode];
 }
 
-static_assert(kMaxStepsParts == 2, "the parts table lists 2 step counts");
+static_assert(kMaxStepsParts == 4, "the parts table lists the step counts 1, 2 and 4");
 
+// steps in {1, 2, 4} (the multi-input route never takes 3).
 PartsLaunchFn FAGQ_LOOKUP_PARTS(FAGQ_QF, FAGQ_SF)(int lpg_idx, int steps) {
-  static const PartsLaunchFn table[kNumLpg][kMaxStepsParts] = {
-      {&launch_rows_parts<1, 8>, &launch_rows_parts<2, 8>},
-      {&launch_rows_parts<1, 16>, &launch_rows_parts<2, 16>},
-      {&launch_rows_parts<1, 32>, &launch_rows_parts<2, 32>}};
-  return table[lpg_idx][steps - 1];
+  static const PartsLaunchFn table[kNumLpg][3] = {
+      {&launch_rows_parts<1, 8>, &launch_rows_parts<2, 8>, &launch_rows_parts<4, 8>},
+      {&launch_rows_parts<1, 16>, &launch_rows_parts<2, 16>, &launch_rows_parts<4, 16>},
+      {&launch_rows_parts<1, 32>, &launch_rows_parts<2, 32>, &launch_rows_parts<4, 32>}};
+  return table[lpg_idx][steps == 4 ? 2 : steps - 1];
 }
 
 }  // namespace fagq

@@ -53,7 +53,7 @@ constexpr int kStepCols = 512;      // columns per wave step (64 lanes x 8)
 constexpr int kMaxWavesPerBlock = 16;
 constexpr int kMaxStepsPerWave = 4;
 constexpr int kMaxParts = 8;        // partial sums of x in the multi-input form
-constexpr int kMaxStepsParts = 2;   // steps per wave in the multi-input form
+constexpr int kMaxStepsParts = 4;   // steps per wave in the multi-input form (1, 2 or 4)
 
 // Row-group modes of a workgroup of rpb row groups x wpr waves.
 enum RowGroupMode {
@@ -912,9 +912,11 @@ fagq_rows(const KArgs a) {
 // sum of nparts partial tensors, one per rank, added in fp32 in rank order
 // before the residual; everything after is the operator above.  One row per
 // row group, no norm_out, at most kMaxStepsParts steps per wave (the partial
-// loads of a wave's steps are all in flight at once).
+// loads of a wave's steps are all in flight at once).  4-step waves hold up to
+// 8 x 4 partial loads (about 200 VGPRs), so their workgroups are bounded to 8
+// waves (256 VGPRs per lane).
 template <int NS, int LPG, int QF, int SF>
-__global__ void __launch_bounds__(1024)
+__global__ void __launch_bounds__(NS > 2 ? 512 : 1024)
 fagq_rows_parts(const PArgs pa) {
   const KArgs& a = pa.k;
   static_assert(NS >= 1 && NS <= kMaxStepsParts, "steps per wave");

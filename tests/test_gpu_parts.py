@@ -55,6 +55,11 @@ CASES = [  # nparts, M, D, G, out dtype, col, ue8m0, rounding
     (5, 33, 640, 64, torch.int8, False, False, "trunc"),  # ragged row, small D (rows share a workgroup)
     (2, 17, 8192, 256, torch.int8, False, True, "rne"),
     (7, 1, 5120, 128, FP8, True, True, "rne"),
+    # 6-8 partials and 12-16 steps: 4-step waves
+    (6, 64, 6144, 128, FP8, False, True, "rne"),           # 3 waves of 4 steps
+    (6, 100, 6400, 128, torch.int8, False, False, "rne"),  # last wave 1.5 steps
+    (7, 33, 6656, 64, torch.int8, True, False, "trunc"),
+    (8, 50, 8192, 256, FP8, True, True, "rne"),
 ]
 
 
