@@ -101,7 +101,7 @@ bool finish_mapping(int64_t M, int D, int wpr, int rpb, int mode, int lds, Mappi
 // then keep the set of rows in flight small, which HBM rewards).  Rows below
 // refer to prefill (M >= prefill_rows()) unless stated; timings are medians of
 // interleaved runs at M = 16384 (MI355X):
-// * column-major scales, 12..16 steps (6144 <= D <= 8192): two rows per
+// * column-major scales, 12..16 steps (5632 < D <= 8192): two rows per
 //   workgroup of 4-step waves, gamma loaded once and shared through LDS, each
 //   group's scale words of both rows stored together (RG_WIDE_SCALES).
 //   D = 7168 fp32: 130.2 us against 134.6 us for one row of 2-step waves;
@@ -295,7 +295,7 @@ int parts_steps() {
 
 // The multi-input form's mapping, one row per row group (small rows share a
 // workgroup as in choose_mapping):
-// * at least 6 partials and 12..16 steps (6144 < D <= 8192): 4-step waves,
+// * at least 6 partials and 12..16 steps (5632 < D <= 8192): 4-step waves,
 //   each holding 4 KB of every partial in flight, 2 waves per SIMD.  Medians
 //   of interleaved runs at D = 7168, against 2-step waves: 2048 rows with 8
 //   partials 51.7 against 52.9 us, with 6 partials 41.9 against 42.6; 4096

@@ -85,7 +85,7 @@ def test_route_invariants(pkg, M, D, ue8m0, col):
     prefill = M >= 1024
     if prefill and 12 <= steps <= 16:
         if col:
-            # 6144 <= D <= 8192, column-major: two rows per workgroup of 4-step
+            # 5632 < D <= 8192, column-major: two rows per workgroup of 4-step
             # waves, shared gamma, wide scale stores, 16 rows per XCD chunk
             # (fp32) or 32 (ue8m0).
             assert (ns, rpb, mode, r["xcd_remap"]) == (4, 2, 2, 8 if not ue8m0 else 16)
