@@ -117,9 +117,11 @@ __device__ __forceinline__ void store8(const rsrc_t& rs, bool bf16, uint32_t e, 
 
 // grid (ceil(S / rows_per_wg), B, hsplit); rows_per_wg = 256 / (D / 8);
 // z picks the head group [z hps, min(H, (z + 1) hps)).  U heads' loads are in
-// flight per lane: U = 2 keeps the kernel at 50 VGPRs, 8 workgroups per CU,
-// for grids of 2048 and more; U = 8 (110 VGPRs, 4 per CU) for grids that fit
-// 4 per CU, where each workgroup's few heads are then loaded at once.
+// flight per lane: for grids of 2048 and more U = 2 with bf16 dq (50 VGPRs, 8
+// workgroups per CU) and U = 1 with fp32 dq, whose stores are twice the
+// loads' bytes (2 B / 4 B, 2 x 64 x 4096 x 512: 297 against 308 us for the
+// pass); U = 8 (110 VGPRs, 4 per CU) for grids that fit 4 per CU, where each
+// workgroup's few heads are then loaded at once.
 template <int U, bool HALVES>
 __global__ void __launch_bounds__(kThreads) mla_stream_do(const MArgs g) {
   const int lpr = g.D / 8;                        // lanes per row
@@ -694,7 +696,7 @@ int launch(const void* q, const void* c_kv, const void* out, const void* dout, c
     const bool k1_wide = (int64_t)k1_grid.x * k1_grid.y * k1_grid.z <= kMinK1Groups;
     const bool halves = dq_dtype == FAGQ_MLA_F32;
     const void* k1 = halves ? (k1_wide ? reinterpret_cast<const void*>(&mla_stream_do<8, true>)
-                                       : reinterpret_cast<const void*>(&mla_stream_do<2, true>))
+                                       : reinterpret_cast<const void*>(&mla_stream_do<1, true>))
                             : (k1_wide ? reinterpret_cast<const void*>(&mla_stream_do<8, false>)
                                        : reinterpret_cast<const void*>(&mla_stream_do<2, false>));
     int ls = launch_kernel(k1, k1_grid, dim3(kThreads), args, 0, st);
