@@ -763,7 +763,9 @@ def parts_bench(args, torch, pkg, w) -> int:
         "data": "synthetic",
         "config": {"workload": w.name, "M": w.M, "D": w.D, "nparts": w.nparts,
                    "group_size": w.group_size, "q": "float8_e4m3fn", "scale": "f32 col-major",
-                   "algorithmic_bytes": set_bytes, "buffer_sets": nsets},
+                   "algorithmic_bytes": set_bytes, "buffer_sets": nsets,
+                   "route": _lib.query_route_parts(w.M, w.D, w.group_size, w.nparts,
+                                                   _lib.SCALE_F32, _lib.LAYOUT_COL_MAJOR)},
         "us_per_call": round(kern_ms * 1e3, 2),
         "us_per_call_host_wall": round(wall_ms * 1e3, 2),
         **steady_fields(steady_ms, set_bytes),

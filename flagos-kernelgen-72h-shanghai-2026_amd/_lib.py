@@ -62,6 +62,7 @@ SIGNATURES = {
     "fagq_launch_mapped": ([_P] * 7 + [_I64, _I64, _I64, _F] + [_I] * 9 + [_P], _I),
     "fagq_query_route": ([_I64, _I64, _I64, _I, _I, ctypes.POINTER(Route)], _I),
     "fagq_query_route_typed": ([_I64, _I64, _I64, _I, _I, _I, _I, ctypes.POINTER(Route)], _I),
+    "fagq_query_route_parts": ([_I64, _I64, _I64, _I, _I, _I, ctypes.POINTER(Route)], _I),
     "fagq_status_string": ([_I], ctypes.c_char_p),
     "fagq_version": ([], _I),
     "fagq_diag_encode": ([_P, _P, _I64, _I, _I, _I, _P], _I),
@@ -195,4 +196,13 @@ def query_route(M: int, D: int, group_size: int, scale_format: int = SCALE_F32,
         res = act if res_dtype is None else res_dtype
         check(load().fagq_query_route_typed(M, D, group_size, scale_format, scale_layout, act, res,
                                             ctypes.byref(r)), "fagq_query_route_typed")
+    return {f: getattr(r, f) for f, _ in Route._fields_ if f != "reserved"}
+
+
+def query_route_parts(M: int, D: int, group_size: int, nparts: int,
+                      scale_format: int = SCALE_F32, scale_layout: int = LAYOUT_ROW_MAJOR) -> dict:
+    """The route of fagq_launch_parts for nparts partials."""
+    r = Route()
+    check(load().fagq_query_route_parts(M, D, group_size, nparts, scale_format, scale_layout,
+                                        ctypes.byref(r)), "fagq_query_route_parts")
     return {f: getattr(r, f) for f, _ in Route._fields_ if f != "reserved"}

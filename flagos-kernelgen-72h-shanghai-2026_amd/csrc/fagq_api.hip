@@ -359,6 +359,32 @@ int launch_with(const Mapping& m, const void* x, const void* residual, const voi
             static_cast<hipStream_t>(stream));
 }
 
+// Shape checks shared by the route queries (those of validate() that need no
+// pointers).
+int check_route_shape(int64_t M, int64_t D, int64_t group_size, int scale_format,
+                      int scale_layout, const fagq_route* route) {
+  if (!route) return FAGQ_E_NULL;
+  if (group_size != 64 && group_size != 128 && group_size != 256) return FAGQ_E_GROUP;
+  if (M < 0 || D <= 0 || D % group_size != 0) return FAGQ_E_SHAPE;
+  if (D > FAGQ_MAX_D || M > (int64_t)INT32_MAX) return FAGQ_E_TOO_LARGE;
+  if (scale_format != FAGQ_SCALE_F32 && scale_format != FAGQ_SCALE_UE8M0) return FAGQ_E_FORMAT;
+  if (scale_layout != FAGQ_LAYOUT_ROW_MAJOR && scale_layout != FAGQ_LAYOUT_COL_MAJOR)
+    return FAGQ_E_FORMAT;
+  return FAGQ_OK;
+}
+
+void fill_route(const Mapping& m, int scale_format, int scale_layout, fagq_route* route) {
+  route->waves_per_row = m.wpr;
+  route->steps_per_wave = m.ns;
+  route->rows_per_block = m.rpb;
+  route->row_group_mode = m.mode;
+  route->block_threads = m.block;
+  route->lds_bytes = m.lds;
+  route->grid_blocks = m.grid;
+  route->xcd_remap = remap_for(scale_layout, scale_format, m.rpb, m.mode);
+  route->reserved = 0;
+}
+
 }  // namespace
 }  // namespace fagq
 
@@ -489,16 +515,23 @@ FAGQ_API int fagq_query_route(int64_t M, int64_t D, int64_t group_size, int scal
                                 FAGQ_DT_BF16, route);
 }
 
+FAGQ_API int fagq_query_route_parts(int64_t M, int64_t D, int64_t group_size, int nparts,
+                                    int scale_format, int scale_layout, fagq_route* route) {
+  const int v = check_route_shape(M, D, group_size, scale_format, scale_layout, route);
+  if (v != FAGQ_OK) return v;
+  if (nparts < 1 || nparts > FAGQ_MAX_PARTS) return FAGQ_E_SHAPE;
+  if (D > FAGQ_MAX_D_PARTS) return FAGQ_E_TOO_LARGE;
+  Mapping m;
+  choose_mapping_parts(M, (int)D, nparts, &m);
+  fill_route(m, scale_format, scale_layout, route);
+  return FAGQ_OK;
+}
+
 FAGQ_API int fagq_query_route_typed(int64_t M, int64_t D, int64_t group_size, int scale_format,
                                     int scale_layout, int act_dtype, int res_dtype,
                                     fagq_route* route) {
-  if (!route) return FAGQ_E_NULL;
-  if (group_size != 64 && group_size != 128 && group_size != 256) return FAGQ_E_GROUP;
-  if (M < 0 || D <= 0 || D % group_size != 0) return FAGQ_E_SHAPE;
-  if (D > FAGQ_MAX_D || M > (int64_t)INT32_MAX) return FAGQ_E_TOO_LARGE;
-  if (scale_format != FAGQ_SCALE_F32 && scale_format != FAGQ_SCALE_UE8M0) return FAGQ_E_FORMAT;
-  if (scale_layout != FAGQ_LAYOUT_ROW_MAJOR && scale_layout != FAGQ_LAYOUT_COL_MAJOR)
-    return FAGQ_E_FORMAT;
+  const int v = check_route_shape(M, D, group_size, scale_format, scale_layout, route);
+  if (v != FAGQ_OK) return v;
   const bool bf16 = act_dtype == FAGQ_DT_BF16 && res_dtype == FAGQ_DT_BF16;
   const int tf = bf16 ? -1 : type_family(act_dtype, res_dtype);
   if (!bf16 && tf < 0) return FAGQ_E_FORMAT;
@@ -507,15 +540,7 @@ FAGQ_API int fagq_query_route_typed(int64_t M, int64_t D, int64_t group_size, in
   Mapping m;
   if (bf16 || tf == TF_F16) choose_mapping(M, (int)D, scale_format, scale_layout, &m);
   else default_mapping(M, (int)D, &m);
-  route->waves_per_row = m.wpr;
-  route->steps_per_wave = m.ns;
-  route->rows_per_block = m.rpb;
-  route->row_group_mode = m.mode;
-  route->block_threads = m.block;
-  route->lds_bytes = m.lds;
-  route->grid_blocks = m.grid;
-  route->xcd_remap = remap_for(scale_layout, scale_format, m.rpb, m.mode);
-  route->reserved = 0;
+  fill_route(m, scale_format, scale_layout, route);
   return FAGQ_OK;
 }
 

@@ -190,6 +190,14 @@ typedef struct fagq_route {
 FAGQ_API int fagq_query_route(int64_t M, int64_t D, int64_t group_size, int scale_format,
                               int scale_layout, fagq_route* route);
 
+/* The route fagq_launch_parts takes for nparts partials (1..FAGQ_MAX_PARTS) of a
+ * shape: independent rows (row_group_mode 0), 4 steps per wave for 6 or more
+ * partials at 12..16 steps of 512 columns, else 2 (or FAGQ_PARTS_STEPS = 1).
+ * The same shape checks as fagq_launch_parts (D <= FAGQ_MAX_D_PARTS); never
+ * touches the device. */
+FAGQ_API int fagq_query_route_parts(int64_t M, int64_t D, int64_t group_size, int nparts,
+                                    int scale_format, int scale_layout, fagq_route* route);
+
 /* The route fagq_launch_typed takes for an element-type pair: fagq_launch's
  * for (BF16, BF16) and (F16, F16); for the pairs with an fp32 tensor, the
  * typed kernel's (independent rows, row_group_mode 0).  Other pairs

@@ -152,6 +152,37 @@ def test_typed_routes(pkg, M, D, at, rt, ue8m0, col):
     assert r["lds_bytes"] == (36864 if prefill and ns == 2 and rpb == 1 and 9 <= steps <= 11 else 0)
 
 
+@pytest.mark.parametrize("M,D", [(1, 640), (33, 4096), (2048, 5632), (2048, 5760), (2048, 6144),
+                                 (2048, 7168), (2048, 8192), (2048, 8320), (4096, 16384)])
+@pytest.mark.parametrize("nparts", [1, 2, 4, 5, 6, 8])
+def test_parts_routes(lib, M, D, nparts):
+    """The multi-input form: 4-step waves for 6 or more partials at 12..16
+    steps of 512 columns (5632 < D <= 8192), 2-step waves otherwise (1 step
+    for rows of one step), independent rows, small rows sharing a workgroup."""
+    from fagq_mi355x import _lib
+    r = _lib.query_route_parts(M, D, 128, nparts, _lib.SCALE_F32, _lib.LAYOUT_COL_MAJOR)
+    steps = math.ceil(D / 512)
+    ns = 4 if nparts >= 6 and 12 <= steps <= 16 else min(2, steps)
+    wpr = math.ceil(steps / ns)
+    rpb = 1 if wpr >= 4 else 4 // wpr
+    assert (r["waves_per_row"], r["steps_per_wave"], r["rows_per_block"], r["row_group_mode"]) == \
+        (wpr, ns, rpb, 0)
+    assert r["block_threads"] == 64 * wpr * rpb <= (512 if ns == 4 else 1024)
+    assert r["grid_blocks"] == math.ceil(M / rpb)
+    assert r["lds_bytes"] == 0
+
+
+@pytest.mark.parametrize("args,status", [
+    ((4, 4096, 128, 0, 0, 0), 2), ((4, 4096, 128, 9, 0, 0), 2), ((4, 16896, 128, 8, 0, 0), 7),
+    ((4, 4096, 100, 8, 0, 0), 3), ((4, 4096, 128, 8, 2, 0), 5),
+])
+def test_parts_route_rejects_bad_arguments(lib, args, status):
+    from fagq_mi355x import _lib
+    r = _lib.Route()
+    assert lib.fagq_query_route_parts(*args, ctypes.byref(r)) == status
+    assert lib.fagq_query_route_parts(4096, 4096, 128, 8, 0, 0, None) == 1
+
+
 def test_typed_route_rejects_unknown_pairs(lib):
     from fagq_mi355x import _lib
     r = _lib.Route()
