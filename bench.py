@@ -23,6 +23,10 @@ us_per_call_host_wall).
               the GPU's rows); cpu_baseline_config1 = BASELINE config 1
               (128 x 4096) in full, with the GPU's output checked against it
 
+--config f16_* / bf16_r32_*: the typed form (fp16 tensors; fp32 residual stream).
+--config ref4_*: the reference operator's own output mode: norm_out written
+(4 outputs), int8 codes by truncation, fp32 row-major scales.
+
 --config tp*_shard_*: the multi-input form (fagq_launch_parts) at one rank's
 shard of a tensor-parallel layer: nparts partial sums reduced, normalized and
 quantized (fp8, fp32 column-major scales); cpu_baseline = the C oracle.
@@ -336,8 +340,8 @@ def main() -> int:
         return gemm_bench(args, torch, pkg, GEMM_CONFIGS[name])
     if name in PARTS_CONFIGS:
         return parts_bench(args, torch, pkg, PARTS_CONFIGS[name])
-    from fagq_mi355x.workloads import TYPED_CONFIGS
-    w = CONFIGS[name] if name in CONFIGS else TYPED_CONFIGS[name]
+    from fagq_mi355x.workloads import REFERENCE_MODE_CONFIGS, TYPED_CONFIGS
+    w = {**CONFIGS, **TYPED_CONFIGS, **REFERENCE_MODE_CONFIGS}[name]
     if args.rows_sweep:
         return rows_sweep(args, torch, pkg, w)
     if args.route_sweep:
@@ -358,12 +362,13 @@ def main() -> int:
         q = torch.empty((w.M, w.D), dtype=w.out_dtype, device=dev)
         sc = pkg.empty_scales(w.M, w.groups, ue8m0=w.scale_ue8m0, col_major=w.scale_col_major,
                               device=dev)
-        sets.append((xs, rs, ro, q, sc))
+        no = torch.empty_like(xs) if w.norm else None
+        sets.append((xs, rs, ro, q, sc, no))
 
     def step(i: int):
-        xs, rs, ro, q, sc = sets[i % nsets]
+        xs, rs, ro, q, sc, no = sets[i % nsets]
         pkg.fused_add_rmsnorm_group_quant(
-            xs, rs, gd, ro, None, q, sc, w.eps, w.group_size,
+            xs, rs, gd, ro, no, q, sc, w.eps, w.group_size,
             rounding=w.rounding if w.out_dtype == torch.int8 else None)
 
     for i in range(args.warmup):
@@ -483,12 +488,13 @@ def rows_sweep(args, torch, pkg, w0) -> int:
             sets.append((xs, rs, torch.empty_like(rs),
                          torch.empty((M, w.D), dtype=w.out_dtype, device=dev),
                          pkg.empty_scales(M, w.groups, ue8m0=w.scale_ue8m0,
-                                          col_major=w.scale_col_major, device=dev)))
+                                          col_major=w.scale_col_major, device=dev),
+                         torch.empty_like(xs) if w.norm else None))
 
         def step(i, sets=sets, w=w):
-            xs, rs, ro, q, sc = sets[i % len(sets)]
+            xs, rs, ro, q, sc, no = sets[i % len(sets)]
             pkg.fused_add_rmsnorm_group_quant(
-                xs, rs, gd, ro, None, q, sc, w.eps, w.group_size,
+                xs, rs, gd, ro, no, q, sc, w.eps, w.group_size,
                 rounding=w.rounding if w.out_dtype == torch.int8 else None)
         runs.append((M, nb, step, sets, gd))
     heat(torch, dev, runs[-1][2], 300.0)
@@ -547,7 +553,8 @@ def route_sweep(args, torch, pkg, w) -> int:
         xs, rs = (xd, rd) if i == 0 else (xd.clone(), rd.clone())
         sets.append((xs, rs, torch.empty_like(rs), torch.empty((w.M, w.D), dtype=w.out_dtype, device=dev),
                      pkg.empty_scales(w.M, w.groups, ue8m0=w.scale_ue8m0, col_major=w.scale_col_major,
-                                      device=dev)))
+                                      device=dev),
+                     torch.empty_like(xs) if w.norm else None))
     qf = _lib.Q_INT8 if w.out_dtype == torch.int8 else _lib.Q_FP8_E4M3FN
     sf = _lib.SCALE_UE8M0 if w.scale_ue8m0 else _lib.SCALE_F32
     lay = _lib.LAYOUT_COL_MAJOR if w.scale_col_major else _lib.LAYOUT_ROW_MAJOR
@@ -560,8 +567,9 @@ def route_sweep(args, torch, pkg, w) -> int:
 
     def stepper(wpr, rpb, mode):
         def step(i):
-            xs, rs, ro, q, sc = sets[i % nsets]
-            e = lib.fagq_launch_mapped(P(xs), P(rs), P(gd), P(ro), None, P(q), P(sc), w.M, w.D,
+            xs, rs, ro, q, sc, no = sets[i % nsets]
+            e = lib.fagq_launch_mapped(P(xs), P(rs), P(gd), P(ro), None if no is None else P(no),
+                                       P(q), P(sc), w.M, w.D,
                                        w.group_size, w.eps, qf, sf, lay, rnd, wpr, rpb, mode,
                                        remap, lds, st)
             if e:
@@ -569,8 +577,8 @@ def route_sweep(args, torch, pkg, w) -> int:
         return step
 
     def route_step(i):
-        xs, rs, ro, q, sc = sets[i % nsets]
-        pkg.fused_add_rmsnorm_group_quant(xs, rs, gd, ro, None, q, sc, w.eps, w.group_size,
+        xs, rs, ro, q, sc, no = sets[i % nsets]
+        pkg.fused_add_rmsnorm_group_quant(xs, rs, gd, ro, no, q, sc, w.eps, w.group_size,
                                           rounding=w.rounding if w.out_dtype == torch.int8 else None)
 
     steps_total = -(-w.D // 512)
@@ -631,7 +639,7 @@ def _time_cpu(run, min_runs: int, seconds: float, max_runs: int = 1000):
 def _gpu_rows_parity(w, gpu_set, ref, rows, torch):
     import numpy as np
     from oracle.compare import compare
-    _, _, ro, q, sc = gpu_set
+    _, _, ro, q, sc, no = gpu_set
     torch.cuda.synchronize()
     scale_rows = sc[:rows]
     scale_phys = scale_rows.t() if w.scale_col_major else scale_rows
@@ -640,6 +648,9 @@ def _gpu_rows_parity(w, gpu_set, ref, rows, torch):
            "scale": np.ascontiguousarray(scale_phys.cpu().numpy())}
     refd = {"residual_out": ref[0].view(torch.uint16).numpy(),
             "q": ref[1].view(torch.uint8).numpy(), "scale": ref[2].numpy()}
+    if no is not None:
+        gpu["norm_out"] = no[:rows].cpu().view(torch.uint16).numpy()
+        refd["norm_out"] = ref[3].view(torch.uint16).numpy()
     try:
         st = compare(gpu, refd, fp8=w.out_dtype == torch.float8_e4m3fn, ue8m0=w.scale_ue8m0)
         return {"ok": True, "exact": st["exact"], "q_mismatch": st["q_mismatch"]}
@@ -660,7 +671,7 @@ def cpu_baseline(w, x, res, gamma, gpu_set, args, torch) -> dict:
 
     def run():
         return fagq_torch(xs, rs, gamma, w.eps, w.group_size, w.out_dtype, w.scale_ue8m0,
-                          w.scale_col_major, w.rounding)
+                          w.scale_col_major, w.rounding, with_norm=w.norm)
 
     ref = run()
     t, n = _time_cpu(run, 3, args.cpu_seconds)
@@ -702,7 +713,7 @@ def cpu_config1(pkg, dev, args, torch) -> dict:
             "sample": f"all {w.M} rows, eager PyTorch CPU restatement (oracle/torch_eager.py), "
                       f"{threads} threads, median of {n} runs",
             "host": host_info(threads),
-            "parity_vs_gpu": _gpu_rows_parity(w, (xd, rd, ro, q, sc), ref, w.M, torch)}
+            "parity_vs_gpu": _gpu_rows_parity(w, (xd, rd, ro, q, sc, None), ref, w.M, torch)}
 
 
 def parts_bench(args, torch, pkg, w) -> int:

@@ -26,6 +26,7 @@ class Workload:
     seed: int = 0
     act: torch.dtype = torch.bfloat16     # x and weight (the typed form: fp16 or fp32 too)
     res: torch.dtype = torch.bfloat16     # residual and residual_out
+    norm: bool = False                    # norm_out written too (the 4-output form)
 
     @property
     def groups(self) -> int:
@@ -35,9 +36,11 @@ class Workload:
     def scale_bytes(self) -> int:
         return 1 if self.scale_ue8m0 else 4
 
-    def algorithmic_bytes(self, with_norm: bool = False) -> int:
+    def algorithmic_bytes(self, with_norm: bool | None = None) -> int:
         """HBM bytes one call must move: read x, residual (2 B each per bf16
-        element) and gamma once; write residual_out, codes (1 B) and scales."""
+        element) and gamma once; write residual_out, codes (1 B) and scales,
+        and norm_out in the 4-output form (with_norm, default: the workload's)."""
+        with_norm = self.norm if with_norm is None else with_norm
         N = self.M * self.D
         ba, br = self.act.itemsize, self.res.itemsize
         b = (ba + br) * N + ba * self.D + br * N + N + self.scale_bytes * self.M * self.groups
@@ -67,6 +70,16 @@ TYPED_CONFIGS = {
                                dist="outliers", act=torch.float16, res=torch.float16),
     "bf16_r32_16384x7168": Workload("bf16_r32_16384x7168", 16384, 7168, scale_col_major=True,
                                     dist="outliers", res=torch.float32),
+}
+
+# The reference operator's own output mode (task01.py:1731-1741, :112-116):
+# norm_out written (4 outputs), int8 codes by truncation toward zero, fp32
+# row-major scales.  Not BASELINE configs.
+REFERENCE_MODE_CONFIGS = {
+    "ref4_16384x7168": Workload("ref4_16384x7168", 16384, 7168, out_dtype=torch.int8,
+                                rounding="trunc", dist="outliers", norm=True),
+    "ref4_4096x4096": Workload("ref4_4096x4096", 4096, 4096, out_dtype=torch.int8,
+                               rounding="trunc", norm=True),
 }
 
 

@@ -22,6 +22,17 @@ def test_algorithmic_bytes_match_the_byte_model(pkg):
     assert w.algorithmic_bytes(with_norm=True) == 825_767_936 + 2 * w.M * w.D
 
 
+def test_reference_mode_workloads(pkg):
+    """The 4-output workloads count norm_out (2 B per element) by default."""
+    from fagq_mi355x.workloads import REFERENCE_MODE_CONFIGS
+    w = REFERENCE_MODE_CONFIGS["ref4_16384x7168"]
+    N = w.M * w.D
+    assert w.norm and w.out_dtype == torch.int8 and w.rounding == "trunc"
+    assert not w.scale_col_major and not w.scale_ue8m0
+    assert w.algorithmic_bytes() == 9 * N + 2 * w.D + 4 * N // 128
+    assert w.algorithmic_bytes(with_norm=False) == 7 * N + 2 * w.D + 4 * N // 128
+
+
 def test_inputs_are_deterministic_and_shaped(pkg):
     from fagq_mi355x.workloads import CONFIGS, make_inputs
     w = CONFIGS["cpu_ref_128x4096"]
