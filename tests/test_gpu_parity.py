@@ -56,6 +56,19 @@ def test_baseline_configs_full_size(pkg, gpu, name):
     assert st["exact"], st
 
 
+@pytest.mark.parametrize("name", ["ref4_16384x7168", "ref4_4096x4096"])
+def test_reference_mode_full_size(pkg, gpu, name):
+    """The reference's own output mode at full size: norm_out written, int8
+    codes by truncation, fp32 row-major scales (the bench's ref4 workloads)."""
+    from fagq_mi355x.workloads import REFERENCE_MODE_CONFIGS, make_inputs
+    w = REFERENCE_MODE_CONFIGS[name]
+    x, r, g = make_inputs(w)
+    st, _ = check(pkg, gpu, x, r, g, w.group_size, f"int8_{w.rounding}", w.scale_ue8m0,
+                  w.scale_col_major, with_norm=w.norm, label=name)
+    note(f"  {name}: {st}")
+    assert st["exact"], st
+
+
 @pytest.mark.parametrize("G", [64, 128, 256])
 @pytest.mark.parametrize("fmt", ["fp8", "int8_rne", "int8_trunc"])
 @pytest.mark.parametrize("ue8m0", [False, True])
