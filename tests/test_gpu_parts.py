@@ -93,10 +93,12 @@ def test_parts_in_place_residual(pkg, gpu):
     assert compare(got, want, fp8=True, ue8m0=False)["exact"]
 
 
-def test_parts_tp8_shard_full_size(pkg, gpu):
-    """The headline shape sharded over 8 ranks: 2048 rows x 7168, 8 partial sums."""
+@pytest.mark.parametrize("name", ["tp8_shard_2048x7168", "tp4_shard_4096x7168"])
+def test_parts_tp_shards_full_size(pkg, gpu, name):
+    """The headline shape sharded over 8 or 4 ranks: 2048 rows x 7168 with 8
+    partial sums (4-step waves), 4096 rows with 4 (2-step waves)."""
     from fagq_mi355x.workloads import PARTS_CONFIGS, make_parts_inputs
-    w = PARTS_CONFIGS["tp8_shard_2048x7168"]
+    w = PARTS_CONFIGS[name]
     note(f"parts full size {w.name}")
     parts, r, g = make_parts_inputs(w)
     got = run(pkg, gpu, parts, r, g)

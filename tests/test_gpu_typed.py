@@ -107,6 +107,15 @@ def test_f16_route_modes(pkg, gpu, M, D, ue8m0, col, mode):
     run(pkg, gpu, x, r, w, ue8m0=ue8m0, col=col, with_norm=True, label=f"f16 mode {mode}")
 
 
+@pytest.mark.parametrize("name", ["f16_16384x7168", "bf16_r32_16384x7168"])
+def test_typed_workloads_full_size(pkg, gpu, name):
+    """The bench's typed workloads at full size (the headline shape and format)."""
+    from fagq_mi355x.workloads import TYPED_CONFIGS, make_inputs
+    w = TYPED_CONFIGS[name]
+    x, r, g = make_inputs(w)
+    run(pkg, gpu, x, r, g, w.group_size, "fp8", w.scale_ue8m0, w.scale_col_major, label=name)
+
+
 @pytest.mark.parametrize("at,rt", PAIRS)
 def test_typed_in_place_residual(pkg, gpu, at, rt):
     x, r, w = make(64, 7168, at, rt, seed=3)
