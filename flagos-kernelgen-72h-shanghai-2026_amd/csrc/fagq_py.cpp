@@ -191,7 +191,7 @@ PyMethodDef kMethods[] = {
     {nullptr, nullptr, 0, nullptr}};
 
 PyModuleDef kModule = {PyModuleDef_HEAD_INIT, "_fagq_py", "Per-call binding of fagq_launch.", -1,
-                       kMethods};
+                       kMethods, nullptr, nullptr, nullptr, nullptr};
 
 }  // namespace
 
