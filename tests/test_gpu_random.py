@@ -62,6 +62,28 @@ def test_random_operator(pkg, gpu, seed):
     assert st["exact"], st
 
 
+@pytest.mark.parametrize("seed", range(10))
+def test_random_operator_large(pkg, gpu, seed):
+    """Large grids: M up to 40000, D up to 32768, up to 60 M elements."""
+    rng = random.Random(7000 + seed)
+    G = rng.choice([64, 128, 256])
+    D = G * rng.randint(1, 32768 // G)
+    M = log_uniform(rng, 1024, max(1024, min(40000, 60_000_000 // D)))
+    fmt = rng.choice(FMT_NAMES)
+    ue8m0 = rng.random() < 0.4
+    col = rng.random() < 0.6
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, D, generator=g).bfloat16()
+    r = torch.randn(M, D, generator=g).bfloat16()
+    w = (1.0 + 0.1 * torch.randn(D, generator=g)).bfloat16()
+    label = f"random large operator {seed}: M={M} D={D} G={G} {fmt} ue8m0={ue8m0} col={col}"
+    note(label)
+    got = run_gpu(pkg, gpu, x, r, w, G, fmt, ue8m0, col)
+    want = run_ref(x, r, w, G, fmt, ue8m0, col)
+    st = compare(got, want, fp8=fmt == "fp8", ue8m0=ue8m0, label=label)
+    assert st["exact"], st
+
+
 @pytest.mark.parametrize("seed", range(80))
 def test_random_typed(pkg, gpu, seed):
     rng = random.Random(2000 + seed)
