@@ -161,9 +161,10 @@ def test_typed_graph_replays_match_eager(pkg, gpu, at, rt):
     _replays_match_eager(gpu, call, refresh, [ro, norm, q, sc], "typed")
 
 
-def test_parts_graph_replays_match_eager(pkg, gpu):
+@pytest.mark.parametrize("P_", [4, 8])       # 2-step and 4-step waves
+def test_parts_graph_replays_match_eager(pkg, gpu, P_):
     from fagq_mi355x import _lib
-    P_, M, D = 4, 512, 7168
+    M, D = 512, 7168
     note(f"case graph capture parts P={P_} M={M} D={D}")
     g = torch.Generator(device="cpu").manual_seed(6)
     parts = [torch.randn(M, D, generator=g).bfloat16().to(gpu) for _ in range(P_)]
