@@ -64,24 +64,29 @@ def test_quantizer_graph_replays_match_eager(pkg, gpu, M, D, qdt, col, ue8m0):
             assert torch.equal(_bits(a), _bits(b)), f"replay {rep}"
 
 
-def test_mla_noalloc_graph_replays_match_eager(pkg, gpu):
+@pytest.mark.parametrize("S,gdt", [
+    (512, torch.bfloat16),       # 128 row workgroups x 8 head groups: the wide K1
+    (8192, torch.float32)])      # 2048 row workgroups: the one-head-in-flight fp32 K1
+def test_mla_noalloc_graph_replays_match_eager(pkg, gpu, S, gdt):
     """fagq_mla_bwd_launch_noalloc (three kernels, the library's own workspace)
     captured once and replayed with new dO between replays, against the
     caller-workspace entry point run eagerly."""
     from fagq_mi355x import _lib
     from fagq_mi355x.workloads import MlaWorkload, make_mla_inputs
-    B, H, S, D = 1, 16, 512, 512
-    w = MlaWorkload("graph", B, H, S, D, torch.bfloat16, seed=3)
-    note(f"case graph capture mla noalloc B={B} H={H} S={S} D={D}")
+    B, H, D = 1, 16, 512
+    code = 1 if gdt == torch.bfloat16 else 0            # FAGQ_MLA_BF16 / FAGQ_MLA_F32
+    w = MlaWorkload("graph", B, H, S, D, gdt, seed=3)
+    note(f"case graph capture mla noalloc B={B} H={H} S={S} D={D} grads {gdt}")
     q, c, out, do, lse = make_mla_inputs(w, device=gpu)
     lib = _lib.load()
+    assert lib.fagq_mla_bwd_workspace_bytes(B, S, D) <= 32 << 20   # FAGQ_MLA_SCRATCH_BYTES
     P = lambda t: ctypes.c_void_p(t.data_ptr())
-    dq = torch.empty(B, H, S, D, dtype=torch.bfloat16, device=gpu)
-    dc = torch.empty(B, S, D, dtype=torch.bfloat16, device=gpu)
+    dq = torch.empty(B, H, S, D, dtype=gdt, device=gpu)
+    dc = torch.empty(B, S, D, dtype=gdt, device=gpu)
 
     def noalloc(stream):
         _lib.check(lib.fagq_mla_bwd_launch_noalloc(P(q), P(c), P(out), P(do), P(lse), P(dq), P(dc),
-                                                   B, H, S, D, w.sm_scale, 1, 1,
+                                                   B, H, S, D, w.sm_scale, code, code,
                                                    ctypes.c_void_p(stream.cuda_stream)),
                    "fagq_mla_bwd_launch_noalloc")
 
@@ -104,7 +109,7 @@ def test_mla_noalloc_graph_replays_match_eager(pkg, gpu):
         dq_e, dc_e = torch.empty_like(dq), torch.empty_like(dc)
         st = torch.cuda.current_stream(gpu)
         _lib.check(lib.fagq_mla_bwd_launch(P(q), P(c), P(out), P(do), P(lse), P(dq_e), P(dc_e),
-                                           P(ws), ws.numel(), B, H, S, D, w.sm_scale, 1, 1,
+                                           P(ws), ws.numel(), B, H, S, D, w.sm_scale, code, code,
                                            ctypes.c_void_p(st.cuda_stream)),
                    "fagq_mla_bwd_launch")
         torch.cuda.synchronize(gpu)
