@@ -29,7 +29,10 @@
 // f(r) = (r >> 1) & 7 or r & 7 at 8 (a 2-way conflict on every read).
 //
 // Pipelines.
-//   * Ring (both scales UE8M0, and every BN = 192 kernel): five 32 KB slots,
+//   * Ping-pong (both scales UE8M0 at BN = 256): the ring's slots below, and
+//     two groups of four waves half a k-block apart, so that one group's
+//     products run while the other reads its fragments (fagq_gemm_pp_kernel).
+//   * Ring (every BN = 192 kernel): five 32 KB slots,
 //     all 160 KB of LDS, hold the tile sequence A(0), B(0), A(1), B(1), ...;
 //     while k-block kb is consumed, B(kb + 1) and A(kb + 2) are in flight, so
 //     each activation tile has two k-blocks to land.
@@ -431,6 +434,202 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g)
   }
 }
 
+// ring_barrier() fenced for the scheduler as well: nothing moves across it,
+// so the products of a product interval cannot be hoisted into the read
+// interval before it (MFMAs have no memory operands, and the compiler
+// otherwise interleaves them with the fragment reads).
+__device__ __forceinline__ void pp_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  ring_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Ping-pong pipeline (both scales UE8M0, 256-wide tiles; with fp32 scales
+// the same pipeline measured 2.5 % slower than the two stages, since each
+// product's promotion then waits for its MFMA within the one running wave).  The 8 waves form
+// two groups of 4: group 0 (waves 0-3) owns the tile's columns 0-127, group
+// 1 (waves 4-7) columns 128-255, and each SIMD runs one wave of each.  Every
+// k-block spans two barrier intervals, and group 1 runs half a k-block
+// behind group 0, so in each interval one group reads its operand fragments
+// from LDS (and issues copies) while the other runs its 32 products from
+// registers:
+//   interval 2k + 1: group 0 reads k-block k's fragments  | group 1 multiplies k - 1
+//   interval 2k + 2: group 0 multiplies k                  | group 1 reads k
+// A wave holds a whole k-block's fragments (4 activation and 8 weight 16 x
+// 128-byte operands) between its read and product intervals.  The ring of
+// five 32 KB slots is the one above (A(k) in slot 2k % 5, B(k) in 2k + 1 % 5):
+// group 0 copies B(k + 1) while reading k, group 1 copies A(k + 2) while
+// reading k, and each waits for its own copies before the barrier that ends
+// its next product interval (B) or read interval (A), so every copy has one
+// k-block to land.  A copy only fills a slot whose last reader finished
+// before the barrier that precedes the copy.  Both groups run the same
+// number of iterations and barriers; past the last k-block group 1 still
+// multiplies once, and group 0 waits at the barriers.
+template <class L>
+__global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_pp_kernel(const GArgs g) {
+  static_assert(L::BN == 256 && L::WAVES_M == 4 && L::WAVES_N == 2 && !L::SPLIT,
+                "two groups of four 64 x 128 waves");
+  constexpr int kTM = L::TM, kTN = L::TN;
+  constexpr int kCopy = kATileBytes / 1024 / 4;   // 1 KB copies per wave: a group copies a tile
+  static_assert(L::B_TILE_BYTES == kATileBytes, "both operand tiles fill one slot");
+  constexpr int kScaleLoads = kTM + 1;             // memory instructions of load_scales
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kSlots * kSlotBytes];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave % L::WAVES_M, wn = wave / L::WAVES_M;
+  const bool g0 = wn == 0;
+  int mt, nt;
+  tile_coords((int)blockIdx.x, g.m_tiles, g.n_tiles, mt, nt);
+  const int m0 = mt * kBM, n0 = nt * L::BN;
+  const int mrows = g.M - m0 < kBM ? g.M - m0 : kBM;
+  const int nrows = g.N - n0 < L::BN ? g.N - n0 : L::BN;
+  const rsrc_t ra = make_rsrc(g.a + (int64_t)m0 * g.K, (uint32_t)mrows * (uint32_t)g.K);
+  const rsrc_t rb = make_rsrc(g.b + (int64_t)n0 * g.K, (uint32_t)nrows * (uint32_t)g.K);
+  const rsrc_t ras = make_rsrc(g.as, g.as_bytes);
+  const rsrc_t rbs = make_rsrc(g.bs, g.bs_bytes);
+
+  // Copies as in fagq_gemm_kernel, but a wave issues kCopy instructions of
+  // one whole tile: instruction u of wave wm fills LDS rows 8 (wm kCopy + u) .. +8.
+  const int crow = lane >> 3;
+  const uint32_t cvoff = (uint32_t)crow * (uint32_t)g.K + (uint32_t)swz(lane & 7, crow) * 16u;
+  auto issue_tile = [&](const rsrc_t& rs, int kb, int slot) {
+    uint8_t* dst = lds + slot * kSlotBytes;
+#pragma unroll
+    for (int u = 0; u < kCopy; ++u) {
+      const int inst = wm * kCopy + u;
+      const uint32_t off = cvoff + (uint32_t)__builtin_amdgcn_readfirstlane(
+          (int)((uint32_t)inst * 8u * (uint32_t)g.K + (uint32_t)kb * (uint32_t)kBK));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(dst + inst * 1024), 16, off, 0, 0, 0);
+    }
+  };
+
+  // E8M0 scale bytes of the lane's rows and of the wave's weight block.
+  const int arow = m0 + wm * 16 * kTM + (lane & 15);
+  const int wblk = (n0 + wn * 16 * kTN) >> 7;
+  const uint32_t a_voff = (uint32_t)arow * (uint32_t)g.as_mstride;
+  struct Scales {
+    uint32_t a[kTM], b;
+  };
+  auto load_scales = [&](int kb) {
+    Scales sc;
+    const uint32_t boff = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)((uint32_t)wblk * (uint32_t)g.kblocks + (uint32_t)kb));
+    sc.b = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rbs, boff, 0, 0);
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+      const uint32_t e = (uint32_t)kb * (uint32_t)g.as_kstride +
+                         16u * (uint32_t)i * (uint32_t)g.as_mstride;
+      sc.a[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(
+          ras, a_voff + (uint32_t)__builtin_amdgcn_readfirstlane((int)e), 0, 0);
+    }
+    return sc;
+  };
+
+  f32x4 acc[kTN][kTM];
+#pragma unroll
+  for (int j = 0; j < kTN; ++j)
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) acc[j][i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  i32x8 af[kTM], bf[kTN];
+  auto read_frags = [&](int kb) {
+    const int sa = (2 * kb) % kSlots, sb = (2 * kb + 1) % kSlots;
+    const uint8_t* ta = lds + sa * kSlotBytes;
+    const uint8_t* tb = lds + sb * kSlotBytes;
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) af[i] = lds_frag(ta, wm * 16 * kTM + 16 * i + (lane & 15), lane);
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) bf[j] = lds_frag(tb, wn * 16 * kTN + 16 * j + (lane & 15), lane);
+  };
+  // One k-block's products: the matrix core applies both E8M0 scales.
+  auto products = [&](const Scales& s) {
+#pragma unroll
+    for (int j = 0; j < kTN; ++j)
+#pragma unroll
+      for (int i = 0; i < kTM; ++i)
+        acc[j][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+            bf[j], af[i], acc[j][i], 0, 0, 0, (int)s.b, 0, (int)s.a[i]);
+#pragma unroll
+    for (int j = 0; j < kTN; ++j)
+#pragma unroll
+      for (int i = 0; i < kTM; ++i) pin(acc[j][i]);
+  };
+
+  const int nk = g.kblocks, last = nk - 1;
+  // Past the last k-block the copies and scale loads fetch the last k-block
+  // again, into the slots the next k-blocks would take (free at that point,
+  // and never read): every iteration issues the same instructions, so the
+  // in-order counter's waits are constants (a scale wait does not also wait
+  // for the copies issued after the scales).
+  // Each group runs its own loop (the branch is uniform per wave); both pass
+  // 2 nk + 2 barriers, so every barrier is met by all 8 waves.  Barrier
+  // 2k + 2 starts group 0's products of k-block k and group 1's reads of it;
+  // barrier 2k + 3 starts group 1's products of k and group 0's reads of k + 1.
+  if (g0) {
+    // Prologue: A(0); with group 1's B(0) it lands before the first barrier.
+    issue_tile(ra, 0, 0);
+    Scales cur = load_scales(0);
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    pp_barrier();
+#pragma clang loop unroll(disable)
+    for (int k = 0; k < nk; ++k) {
+      // Reads k-block k and copies B(k + 1) into the slot A(k - 1) left.
+      read_frags(k);
+      const Scales nxt = load_scales(k + 1 < last ? k + 1 : last);
+      issue_order_fence();
+      issue_tile(rb, k + 1 < last ? k + 1 : last, (2 * k + 3) % kSlots);
+      pp_barrier();
+      // Multiplies k while group 1 reads it.
+      products(cur);
+      cur = nxt;
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);   // B(k + 1) and k + 1's scales have landed
+      pp_barrier();
+    }
+    pp_barrier();                           // while group 1 multiplies the last k-block
+  } else {
+    // Prologue: B(0), then A(1) left in flight.
+    issue_tile(rb, 0, 1);
+    issue_order_fence();
+    issue_tile(ra, 1 < last ? 1 : last, 2);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kCopy));
+    pp_barrier();
+    pp_barrier();                           // group 0 reads k-block 0
+    Scales cur;
+#pragma clang loop unroll(disable)
+    for (int k = 0; k < nk; ++k) {
+      // Reads k-block k (group 0 multiplies it) and copies A(k + 2) into
+      // the slot B(k - 1) left; A(k + 1) must land before the barrier.
+      read_frags(k);
+      cur = load_scales(k);
+      issue_order_fence();
+      issue_tile(ra, k + 2 < last ? k + 2 : last, (2 * k + 4) % kSlots);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kScaleLoads + kCopy));
+      pp_barrier();
+      // Multiplies k while group 0 reads k + 1.
+      products(cur);
+      pp_barrier();
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);
+
+  const rsrc_t rc = make_rsrc(g.c + (int64_t)m0 * g.N, (uint32_t)mrows * (uint32_t)g.N * 2u);
+  const int wcol = n0 + wn * 16 * kTN;
+#pragma unroll
+  for (int j = 0; j < kTN; ++j) {
+    const int ncol = wcol + 16 * j;
+    if (ncol >= g.N) continue;   // uniform over the wave
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+      const uint32_t row = (uint32_t)(wm * 16 * kTM + 16 * i + (lane & 15));
+      u32x2 v;
+      v[0] = pack_bf16x2(acc[j][i][0], acc[j][i][1]);
+      v[1] = pack_bf16x2(acc[j][i][2], acc[j][i][3]);
+      const uint32_t off = (row * (uint32_t)g.N + (uint32_t)(ncol + 4 * (lane >> 4))) * 2u;
+      __builtin_amdgcn_raw_buffer_store_b64(v, rc, off, 0, 0);
+    }
+  }
+}
+
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -472,7 +671,10 @@ int validate(const void* a_q, const void* a_scale, const void* b_q, const void* 
 template <class L>
 const void* kernel_for_layout(int asf, int bsf) {
   const bool au = asf == FAGQ_SCALE_UE8M0, bu = bsf == FAGQ_SCALE_UE8M0;
-  if (au && bu) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_UE8M0, SF_UE8M0, L>);
+  if (au && bu) {
+    if constexpr (L::BN == 256) return reinterpret_cast<const void*>(&fagq_gemm_pp_kernel<L>);
+    else return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_UE8M0, SF_UE8M0, L>);
+  }
   if (au) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_UE8M0, SF_F32, L>);
   if (bu) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_F32, SF_UE8M0, L>);
   return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_F32, SF_F32, L>);
