@@ -599,8 +599,9 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_pp_kernel(const GArgs
     for (int k = 0; k < nk; ++k) {
       // Reads k-block k (group 0 multiplies it) and copies A(k + 2) into
       // the slot B(k - 1) left; A(k + 1) must land before the barrier.
+      cur = load_scales(k);                   // first: the products wait for them at the barrier
+      issue_order_fence();
       read_frags(k);
-      cur = load_scales(k);
       issue_order_fence();
       issue_tile(ra, k + 2 < last ? k + 2 : last, (2 * k + 4) % kSlots);
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(kScaleLoads + kCopy));
