@@ -29,17 +29,13 @@
 // f(r) = (r >> 1) & 7 or r & 7 at 8 (a 2-way conflict on every read).
 //
 // Pipelines.
-//   * Ping-pong (both scales UE8M0 at BN = 256): the ring's slots below, and
-//     two groups of four waves half a k-block apart, so that one group's
+//   * Ping-pong (every BN = 256 kernel): the ring's slots below, and two
+//     groups of four waves half a k-block apart, so that one group's
 //     products run while the other reads its fragments (fagq_gemm_pp_kernel).
-//   * Ring (every BN = 192 kernel): five 32 KB slots,
+//   * Ring (BN = 192 kernels): five 32 KB slots,
 //     all 160 KB of LDS, hold the tile sequence A(0), B(0), A(1), B(1), ...;
 //     while k-block kb is consumed, B(kb + 1) and A(kb + 2) are in flight, so
 //     each activation tile has two k-blocks to land.
-//   * Two stages (fp32-promoted scales at BN = 256): 2 x 64 KB, the next
-//     k-block's copies issued before the current one is consumed.  The ring
-//     measured slower there: with its copies and waits in one block the
-//     compiler stops reading the next weight fragment ahead of the products.
 //
 // Scales.  fp32 (or mixed) scales: each k-block's 16 x 16 x 128 product goes
 // to a temporary and is added to the accumulator as t * (sa * sb) with fmaf.
@@ -93,7 +89,6 @@ struct Layout {
   static constexpr int TM = kBM / 16 / WAVES_M;
   static constexpr int TN = BN / 16 / WAVES_N;
   static constexpr int B_TILE_BYTES = BN * kBK;
-  static constexpr int STAGE_BYTES = kATileBytes + B_TILE_BYTES;
   static constexpr int COPY_A = kATileBytes / 1024 / WAVES;    // 1 KB copy instructions per wave
   static constexpr int COPY_B = B_TILE_BYTES / 1024 / WAVES;
   // A wave's columns lie in one weight block unless they can straddle two.
@@ -111,12 +106,6 @@ constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 constexpr int kSlotBytes = kATileBytes;  // ring slot: one operand tile
 constexpr int kSlots = 5;                // 160 KB, all of a gfx950 CU's LDS
 static_assert(kMaxBN * kBK <= kSlotBytes, "a weight tile fits a ring slot");
-
-// The ring pipeline for a pair of scale formats and a layout (see the header).
-template <int ASF, int BSF, class L>
-constexpr bool uses_ring() {
-  return (ASF == SF_UE8M0 && BSF == SF_UE8M0) || L::BN != 256;
-}
 
 struct GArgs {
   const uint8_t* a;       // fp8 [M, K]
@@ -180,11 +169,10 @@ __device__ __forceinline__ void pin(const f32x4& v) { asm volatile("" ::"v"(v));
 
 template <int ASF, int BSF, class L>
 __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g) {
+  static_assert(L::BN != 256, "256-wide tiles run fagq_gemm_pp_kernel");
   constexpr bool kHwScale = ASF == SF_UE8M0 && BSF == SF_UE8M0;
-  constexpr bool kRing = uses_ring<ASF, BSF, L>();
   constexpr int kTM = L::TM, kTN = L::TN;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kRing ? kSlots * kSlotBytes
-                                                              : 2 * L::STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kSlots * kSlotBytes];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -237,27 +225,6 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g)
       const int inst = wave * L::COPY_B + u;
       const uint32_t off = cvoff + copy_off(inst, kb);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(dst + inst * 1024), 16, off, 0, 0, 0);
-    }
-  };
-  // Two stages: both tiles of k-block kb into a stage, their copies interleaved.
-  auto issue = [&](int kb, int stage) {
-    uint8_t* sa_tile = lds + stage * L::STAGE_BYTES;
-    uint8_t* sb_tile = sa_tile + kATileBytes;
-    constexpr int kCopies = L::COPY_A > L::COPY_B ? L::COPY_A : L::COPY_B;
-#pragma unroll
-    for (int u = 0; u < kCopies; ++u) {   // the two tiles' copies interleaved
-      if (u < L::COPY_A) {
-        const int inst = wave * L::COPY_A + u;
-        const uint32_t off = cvoff + copy_off(inst, kb);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(sa_tile + inst * 1024), 16, off,
-                                                 0, 0, 0);
-      }
-      if (u < L::COPY_B) {
-        const int inst = wave * L::COPY_B + u;
-        const uint32_t off = cvoff + copy_off(inst, kb);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(sb_tile + inst * 1024), 16, off,
-                                                 0, 0, 0);
-      }
     }
   };
 
@@ -319,46 +286,26 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g)
   // across, and the wait's count is a constant.
   const int last = g.kblocks - 1;
   Scales cur;
-  if constexpr (kRing) {
-    issue_a(0, 0);
-    issue_b(0, 1);
-    cur = load_scales(0);
-    issue_order_fence();
-    issue_a(last < 1 ? last : 1, 2);
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(L::COPY_A));
-    ring_barrier();
-  } else {
-    issue(0, 0);
-    cur = load_scales(0);
-    __builtin_amdgcn_s_waitcnt(kVmcnt0);
-    __syncthreads();
-  }
+  issue_a(0, 0);
+  issue_b(0, 1);
+  cur = load_scales(0);
+  issue_order_fence();
+  issue_a(last < 1 ? last : 1, 2);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(L::COPY_A));
+  ring_barrier();
 
-  int slot_a = 0;   // ring: (2 kb) % kSlots
+  int slot_a = 0;   // (2 kb) % kSlots
   for (int kb = 0; kb < g.kblocks; ++kb) {
-    const uint8_t* ta;
-    const uint8_t* tb;
-    Scales nxt = cur;
-    if constexpr (kRing) {
-      const int slot_b = slot_a + 1 < kSlots ? slot_a + 1 : 0;
-      const int slot_nb = slot_a + 3 < kSlots ? slot_a + 3 : slot_a + 3 - kSlots;   // B(kb + 1)
-      const int slot_na = slot_a + 4 < kSlots ? slot_a + 4 : slot_a + 4 - kSlots;   // A(kb + 2)
-      const int kb1 = kb + 1 < last ? kb + 1 : last, kb2 = kb + 2 < last ? kb + 2 : last;
-      issue_b(kb1, slot_nb);
-      nxt = load_scales(kb1);
-      issue_order_fence();
-      issue_a(kb2, slot_na);
-      ta = lds + slot_a * kSlotBytes;
-      tb = lds + slot_b * kSlotBytes;
-    } else {
-      const int stage = kb & 1;
-      if (kb + 1 < g.kblocks) {
-        issue(kb + 1, stage ^ 1);
-        nxt = load_scales(kb + 1);
-      }
-      ta = lds + stage * L::STAGE_BYTES;
-      tb = ta + kATileBytes;
-    }
+    const int slot_b = slot_a + 1 < kSlots ? slot_a + 1 : 0;
+    const int slot_nb = slot_a + 3 < kSlots ? slot_a + 3 : slot_a + 3 - kSlots;   // B(kb + 1)
+    const int slot_na = slot_a + 4 < kSlots ? slot_a + 4 : slot_a + 4 - kSlots;   // A(kb + 2)
+    const int kb1 = kb + 1 < last ? kb + 1 : last, kb2 = kb + 2 < last ? kb + 2 : last;
+    issue_b(kb1, slot_nb);
+    const Scales nxt = load_scales(kb1);
+    issue_order_fence();
+    issue_a(kb2, slot_na);
+    const uint8_t* ta = lds + slot_a * kSlotBytes;
+    const uint8_t* tb = lds + slot_b * kSlotBytes;
     constexpr int kNB = L::SPLIT ? 2 : 1;
     float smul[kNB][kTM];
     if constexpr (!kHwScale) {
@@ -391,7 +338,7 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g)
         }
       }
     }
-    if constexpr (kRing && kHwScale) {
+    if constexpr (kHwScale) {
       // The products are issued before the ring's wait.  (With fp32-promoted
       // scales the compiler keeps most of them there by itself, and pinning
       // serialises each product with its promotion: slower.)
@@ -401,21 +348,14 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g)
         for (int i = 0; i < kTM; ++i) pin(acc[j][i]);
     }
     cur = nxt;
-    if constexpr (kRing) {
-      // The next k-block's tiles and scales have landed (each wave waits for
-      // its own copies) and every wave is done reading this k-block's slots
-      // before the next iteration refills them.
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(L::COPY_A));
-      ring_barrier();
-      slot_a = slot_a + 2 < kSlots ? slot_a + 2 : slot_a + 2 - kSlots;
-    } else {
-      // The next stage's copies have landed (each wave waits for its own) and
-      // every wave is done reading this stage before it is refilled.
-      __builtin_amdgcn_s_waitcnt(kVmcnt0);
-      __syncthreads();
-    }
+    // The next k-block's tiles and scales have landed (each wave waits for
+    // its own copies) and every wave is done reading this k-block's slots
+    // before the next iteration refills them.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(L::COPY_A));
+    ring_barrier();
+    slot_a = slot_a + 2 < kSlots ? slot_a + 2 : slot_a + 2 - kSlots;
   }
-  if constexpr (kRing) __builtin_amdgcn_s_waitcnt(kVmcnt0);   // no copy into LDS outlives the workgroup
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);   // no copy into LDS outlives the workgroup
 
   const rsrc_t rc = make_rsrc(g.c + (int64_t)m0 * g.N, (uint32_t)mrows * (uint32_t)g.N * 2u);
 #pragma unroll
@@ -444,9 +384,7 @@ __device__ __forceinline__ void pp_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Ping-pong pipeline (both scales UE8M0, 256-wide tiles; with fp32 scales
-// the same pipeline measured 2.5 % slower than the two stages, since each
-// product's promotion then waits for its MFMA within the one running wave).  The 8 waves form
+// Ping-pong pipeline (every scale format at 256-wide tiles).  The 8 waves form
 // two groups of 4: group 0 (waves 0-3) owns the tile's columns 0-127, group
 // 1 (waves 4-7) columns 128-255, and each SIMD runs one wave of each.  Every
 // k-block spans two barrier intervals, and group 1 runs half a k-block
@@ -465,10 +403,11 @@ __device__ __forceinline__ void pp_barrier() {
 // before the barrier that precedes the copy.  Both groups run the same
 // number of iterations and barriers; past the last k-block group 1 still
 // multiplies once, and group 0 waits at the barriers.
-template <class L>
+template <int ASF, int BSF, class L>
 __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_pp_kernel(const GArgs g) {
   static_assert(L::BN == 256 && L::WAVES_M == 4 && L::WAVES_N == 2 && !L::SPLIT,
                 "two groups of four 64 x 128 waves");
+  constexpr bool kHwScale = ASF == SF_UE8M0 && BSF == SF_UE8M0;
   constexpr int kTM = L::TM, kTN = L::TN;
   constexpr int kCopy = kATileBytes / 1024 / 4;   // 1 KB copies per wave: a group copies a tile
   static_assert(L::B_TILE_BYTES == kATileBytes, "both operand tiles fill one slot");
@@ -504,24 +443,28 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_pp_kernel(const GArgs
     }
   };
 
-  // E8M0 scale bytes of the lane's rows and of the wave's weight block.
+  // Scale bits of the lane's rows and of the wave's weight block, as in
+  // fagq_gemm_kernel.
   const int arow = m0 + wm * 16 * kTM + (lane & 15);
   const int wblk = (n0 + wn * 16 * kTN) >> 7;
-  const uint32_t a_voff = (uint32_t)arow * (uint32_t)g.as_mstride;
+  constexpr uint32_t asb = ASF == SF_F32 ? 4u : 1u, bsb = BSF == SF_F32 ? 4u : 1u;
+  const uint32_t a_voff = (uint32_t)arow * (uint32_t)g.as_mstride * asb;
   struct Scales {
     uint32_t a[kTM], b;
   };
   auto load_scales = [&](int kb) {
     Scales sc;
     const uint32_t boff = (uint32_t)__builtin_amdgcn_readfirstlane(
-        (int)((uint32_t)wblk * (uint32_t)g.kblocks + (uint32_t)kb));
-    sc.b = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rbs, boff, 0, 0);
+        (int)(((uint32_t)wblk * (uint32_t)g.kblocks + (uint32_t)kb) * bsb));
+    sc.b = BSF == SF_F32 ? __builtin_amdgcn_raw_buffer_load_b32(rbs, boff, 0, 0)
+                         : (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rbs, boff, 0, 0);
 #pragma unroll
     for (int i = 0; i < kTM; ++i) {
       const uint32_t e = (uint32_t)kb * (uint32_t)g.as_kstride +
                          16u * (uint32_t)i * (uint32_t)g.as_mstride;
-      sc.a[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(
-          ras, a_voff + (uint32_t)__builtin_amdgcn_readfirstlane((int)e), 0, 0);
+      const uint32_t off = a_voff + (uint32_t)__builtin_amdgcn_readfirstlane((int)(e * asb));
+      sc.a[i] = ASF == SF_F32 ? __builtin_amdgcn_raw_buffer_load_b32(ras, off, 0, 0)
+                              : (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(ras, off, 0, 0);
     }
     return sc;
   };
@@ -541,14 +484,40 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_pp_kernel(const GArgs
 #pragma unroll
     for (int j = 0; j < kTN; ++j) bf[j] = lds_frag(tb, wn * 16 * kTN + 16 * j + (lane & 15), lane);
   };
-  // One k-block's products: the matrix core applies both E8M0 scales.
+  // One k-block's products.  Both UE8M0: the matrix core applies the scales.
+  // fp32 (or mixed): each product goes to a temporary and is added as
+  // fmaf(t, sa * sb, acc), as in fagq_gemm_kernel, and the schedule
+  // alternates one MFMA with four FMAs, so that a product's promotion runs
+  // while the next MFMA executes.
   auto products = [&](const Scales& s) {
+    if constexpr (kHwScale) {
 #pragma unroll
-    for (int j = 0; j < kTN; ++j)
+      for (int j = 0; j < kTN; ++j)
+#pragma unroll
+        for (int i = 0; i < kTM; ++i)
+          acc[j][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              bf[j], af[i], acc[j][i], 0, 0, 0, (int)s.b, 0, (int)s.a[i]);
+    } else {
+      const float sb = BSF == SF_UE8M0 ? e8m0_to_f32(s.b) : __uint_as_float(s.b);
+      float sm[kTM];
 #pragma unroll
       for (int i = 0; i < kTM; ++i)
-        acc[j][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-            bf[j], af[i], acc[j][i], 0, 0, 0, (int)s.b, 0, (int)s.a[i]);
+        sm[i] = (ASF == SF_UE8M0 ? e8m0_to_f32(s.a[i]) : __uint_as_float(s.a[i])) * sb;
+#pragma unroll
+      for (int j = 0; j < kTN; ++j)
+#pragma unroll
+        for (int i = 0; i < kTM; ++i) {
+          const f32x4 t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              bf[j], af[i], f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 127, 0, 127);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[j][i][r] = __builtin_fmaf(t[r], sm[i], acc[j][i][r]);
+        }
+#pragma unroll
+      for (int n = 0; n < kTN * kTM; ++n) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // four VALU
+      }
+    }
 #pragma unroll
     for (int j = 0; j < kTN; ++j)
 #pragma unroll
@@ -672,13 +641,17 @@ int validate(const void* a_q, const void* a_scale, const void* b_q, const void* 
 template <class L>
 const void* kernel_for_layout(int asf, int bsf) {
   const bool au = asf == FAGQ_SCALE_UE8M0, bu = bsf == FAGQ_SCALE_UE8M0;
-  if (au && bu) {
-    if constexpr (L::BN == 256) return reinterpret_cast<const void*>(&fagq_gemm_pp_kernel<L>);
-    else return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_UE8M0, SF_UE8M0, L>);
+  if constexpr (L::BN == 256) {
+    if (au && bu) return reinterpret_cast<const void*>(&fagq_gemm_pp_kernel<SF_UE8M0, SF_UE8M0, L>);
+    if (au) return reinterpret_cast<const void*>(&fagq_gemm_pp_kernel<SF_UE8M0, SF_F32, L>);
+    if (bu) return reinterpret_cast<const void*>(&fagq_gemm_pp_kernel<SF_F32, SF_UE8M0, L>);
+    return reinterpret_cast<const void*>(&fagq_gemm_pp_kernel<SF_F32, SF_F32, L>);
+  } else {
+    if (au && bu) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_UE8M0, SF_UE8M0, L>);
+    if (au) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_UE8M0, SF_F32, L>);
+    if (bu) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_F32, SF_UE8M0, L>);
+    return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_F32, SF_F32, L>);
   }
-  if (au) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_UE8M0, SF_F32, L>);
-  if (bu) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_F32, SF_UE8M0, L>);
-  return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_F32, SF_F32, L>);
 }
 static_assert(Layout256::THREADS == Layout192::THREADS, "one workgroup size");
 
