@@ -28,14 +28,10 @@
 // measures the fragment read with this f at 4 cycles per instruction and with
 // f(r) = (r >> 1) & 7 or r & 7 at 8 (a 2-way conflict on every read).
 //
-// Pipelines.
-//   * Ping-pong (every BN = 256 kernel): the ring's slots below, and two
-//     groups of four waves half a k-block apart, so that one group's
-//     products run while the other reads its fragments (fagq_gemm_pp_kernel).
-//   * Ring (BN = 192 kernels): five 32 KB slots,
-//     all 160 KB of LDS, hold the tile sequence A(0), B(0), A(1), B(1), ...;
-//     while k-block kb is consumed, B(kb + 1) and A(kb + 2) are in flight, so
-//     each activation tile has two k-blocks to land.
+// Pipeline (fagq_gemm_pp_kernel).  Five 32 KB slots, all 160 KB of LDS,
+// hold the tile sequence A(0), B(0), A(1), B(1), ...; the 8 waves are two
+// groups of four half a k-block apart, so that one group's products run
+// while the other reads its fragments from LDS and issues the copies.
 //
 // Scales.  fp32 (or mixed) scales: each k-block's 16 x 16 x 128 product goes
 // to a temporary and is added to the accumulator as t * (sa * sb) with fmaf.
@@ -89,13 +85,9 @@ struct Layout {
   static constexpr int TM = kBM / 16 / WAVES_M;
   static constexpr int TN = BN / 16 / WAVES_N;
   static constexpr int B_TILE_BYTES = BN * kBK;
-  static constexpr int COPY_A = kATileBytes / 1024 / WAVES;    // 1 KB copy instructions per wave
-  static constexpr int COPY_B = B_TILE_BYTES / 1024 / WAVES;
   // A wave's columns lie in one weight block unless they can straddle two.
   static constexpr bool SPLIT = BN % 128 != 0 || (16 * TN) % 128 != 0;
   static_assert(16 * TN <= 128, "a wave's columns touch at most two 128-column weight blocks");
-  static_assert(kATileBytes == COPY_A * 1024 * WAVES && B_TILE_BYTES == COPY_B * 1024 * WAVES,
-                "copy instructions cover each operand tile");
   static_assert(BN <= kMaxBN, "tile width");
 };
 using Layout256 = Layout<256, 4, 2>;
@@ -164,215 +156,8 @@ __device__ __forceinline__ void ring_barrier() {
 }
 // The value is computed before this point, in program order with the other
 // volatile asm statements (the compiler would otherwise sink MFMAs, which
-// have no memory operands, past the ring's wait and barrier).
+// have no memory operands, past a wait and barrier).
 __device__ __forceinline__ void pin(const f32x4& v) { asm volatile("" ::"v"(v)); }
-
-template <int ASF, int BSF, class L>
-__global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_kernel(const GArgs g) {
-  static_assert(L::BN != 256, "256-wide tiles run fagq_gemm_pp_kernel");
-  constexpr bool kHwScale = ASF == SF_UE8M0 && BSF == SF_UE8M0;
-  constexpr int kTM = L::TM, kTN = L::TN;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kSlots * kSlotBytes];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave % L::WAVES_M, wn = wave / L::WAVES_M;
-  int mt, nt;
-  tile_coords((int)blockIdx.x, g.m_tiles, g.n_tiles, mt, nt);
-  const int m0 = mt * kBM, n0 = nt * L::BN;
-  const int mrows = g.M - m0 < kBM ? g.M - m0 : kBM;
-  const int nrows = g.N - n0 < L::BN ? g.N - n0 : L::BN;
-  const rsrc_t ra = make_rsrc(g.a + (int64_t)m0 * g.K, (uint32_t)mrows * (uint32_t)g.K);
-  const rsrc_t rb = make_rsrc(g.b + (int64_t)n0 * g.K, (uint32_t)nrows * (uint32_t)g.K);
-  const rsrc_t ras = make_rsrc(g.as, g.as_bytes);
-  const rsrc_t rbs = make_rsrc(g.bs, g.bs_bytes);
-
-  // Copy geometry: instruction u of this wave is copy instruction i = wave *
-  // COPY + u of an operand tile (COPY_A for the activation tile, COPY_B for
-  // the weight tile) and fills LDS rows 8 i .. +8; the lane's row within them
-  // is lane / 8, its position lane % 8, and it fetches the logical chunk
-  // stored there.  The swizzle of row 8 i + lane / 8 depends on lane / 8
-  // only, so one lane offset serves every instruction.
-  // The whole offset goes in the VGPR offset and the scalar offset is zero:
-  // the hardware range-checks only the VGPR offset (plus the immediate), so
-  // this is what turns rows past M or N into zero reads.  The lane part is
-  // kept in one VGPR and the uniform part added per instruction.
-  const int crow = lane >> 3;
-  const uint32_t cvoff = (uint32_t)crow * (uint32_t)g.K + (uint32_t)swz(lane & 7, crow) * 16u;
-
-  // Uniform part of copy instruction inst's offset for k-block kb.  Offsets
-  // are computed in uint32: the launch checks that every one fits.
-  auto copy_off = [&](int inst, int kb) {
-    return (uint32_t)__builtin_amdgcn_readfirstlane(
-        (int)((uint32_t)inst * 8u * (uint32_t)g.K + (uint32_t)kb * (uint32_t)kBK));
-  };
-  // Ring: one operand tile's copies into a slot.  (The offset goes through a
-  // local: passed to the builtin as an expression, the host pass dropped the
-  // kernel's handle.)
-  auto issue_a = [&](int kb, int slot) {
-    uint8_t* dst = lds + slot * kSlotBytes;
-#pragma unroll
-    for (int u = 0; u < L::COPY_A; ++u) {
-      const int inst = wave * L::COPY_A + u;
-      const uint32_t off = cvoff + copy_off(inst, kb);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(dst + inst * 1024), 16, off, 0, 0, 0);
-    }
-  };
-  auto issue_b = [&](int kb, int slot) {
-    uint8_t* dst = lds + slot * kSlotBytes;
-#pragma unroll
-    for (int u = 0; u < L::COPY_B; ++u) {
-      const int inst = wave * L::COPY_B + u;
-      const uint32_t off = cvoff + copy_off(inst, kb);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(dst + inst * 1024), 16, off, 0, 0, 0);
-    }
-  };
-
-  // Scales of this lane's rows (m0 + 16 (TM wm + i) + lane % 16) and of the
-  // 128-column weight blocks of the wave's columns (block wblk for tiles
-  // j < jsplit, wblk + 1 for the rest) for k-block kb, as loaded bits: they
-  // are converted only after the barrier that ends the k-block, so no wait
-  // for them (and, the counter being in order, for the LDS copies issued
-  // before them) lands inside the MFMA loop.
-  const int arow = m0 + wm * 16 * kTM + (lane & 15);
-  const int wcol = n0 + wn * 16 * kTN;             // the wave's first column
-  const int wblk = wcol >> 7;
-  const int jsplit = L::SPLIT ? (((wblk + 1) << 7) - wcol) >> 4 : kTN;
-  struct Scales {
-    uint32_t a[kTM], b[L::SPLIT ? 2 : 1];
-  };
-  // Offsets as for the copies: all in the range-checked VGPR offset, so scale
-  // reads for rows past M or weight blocks past N fall outside the arrays'
-  // descriptors and read zeros (those rows and columns are never stored).
-  constexpr uint32_t asb = ASF == SF_F32 ? 4u : 1u, bsb = BSF == SF_F32 ? 4u : 1u;
-  const uint32_t a_voff = (uint32_t)arow * (uint32_t)g.as_mstride * asb;   // lane part
-  auto load_scales = [&](int kb) {
-    Scales sc;
-#pragma unroll
-    for (int h = 0; h < (L::SPLIT ? 2 : 1); ++h) {
-      const uint32_t boff = (uint32_t)__builtin_amdgcn_readfirstlane(
-          (int)(((uint32_t)(wblk + h) * (uint32_t)g.kblocks + (uint32_t)kb) * bsb));
-      sc.b[h] = BSF == SF_F32 ? __builtin_amdgcn_raw_buffer_load_b32(rbs, boff, 0, 0)
-                              : (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rbs, boff, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < kTM; ++i) {
-      const uint32_t e = (uint32_t)kb * (uint32_t)g.as_kstride +
-                         16u * (uint32_t)i * (uint32_t)g.as_mstride;
-      const uint32_t off = a_voff + (uint32_t)__builtin_amdgcn_readfirstlane((int)(e * asb));
-      sc.a[i] = ASF == SF_F32 ? __builtin_amdgcn_raw_buffer_load_b32(ras, off, 0, 0)
-                              : (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(ras, off, 0, 0);
-    }
-    return sc;
-  };
-  auto to_f32 = [](uint32_t bits, bool e8m0) {
-    return e8m0 ? e8m0_to_f32(bits) : __uint_as_float(bits);
-  };
-
-  f32x4 acc[kTN][kTM];
-#pragma unroll
-  for (int j = 0; j < kTN; ++j)
-#pragma unroll
-    for (int i = 0; i < kTM; ++i) acc[j][i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-  // Ring: k-block kb reads slots (2 kb) % 5 and (2 kb + 1) % 5.  Its
-  // iteration issues B(kb + 1), then kb + 1's scales, then A(kb + 2), into
-  // the two slots the barrier ending k-block kb - 1 released; A(kb + 1) was
-  // issued one k-block earlier.  The k-block ends with a wait for all but the
-  // last COPY_A memory instructions; the counter is in order, so that leaves
-  // only A(kb + 2) in flight.  Past the last k-block the same instructions
-  // fetch the last k-block again into slots nobody reads, so every iteration
-  // issues and waits alike: no branch for the compiler to move the products
-  // across, and the wait's count is a constant.
-  const int last = g.kblocks - 1;
-  Scales cur;
-  issue_a(0, 0);
-  issue_b(0, 1);
-  cur = load_scales(0);
-  issue_order_fence();
-  issue_a(last < 1 ? last : 1, 2);
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(L::COPY_A));
-  ring_barrier();
-
-  int slot_a = 0;   // (2 kb) % kSlots
-  for (int kb = 0; kb < g.kblocks; ++kb) {
-    const int slot_b = slot_a + 1 < kSlots ? slot_a + 1 : 0;
-    const int slot_nb = slot_a + 3 < kSlots ? slot_a + 3 : slot_a + 3 - kSlots;   // B(kb + 1)
-    const int slot_na = slot_a + 4 < kSlots ? slot_a + 4 : slot_a + 4 - kSlots;   // A(kb + 2)
-    const int kb1 = kb + 1 < last ? kb + 1 : last, kb2 = kb + 2 < last ? kb + 2 : last;
-    issue_b(kb1, slot_nb);
-    const Scales nxt = load_scales(kb1);
-    issue_order_fence();
-    issue_a(kb2, slot_na);
-    const uint8_t* ta = lds + slot_a * kSlotBytes;
-    const uint8_t* tb = lds + slot_b * kSlotBytes;
-    constexpr int kNB = L::SPLIT ? 2 : 1;
-    float smul[kNB][kTM];
-    if constexpr (!kHwScale) {
-#pragma unroll
-      for (int h = 0; h < kNB; ++h) {
-        const float sb = to_f32(cur.b[h], BSF == SF_UE8M0);
-#pragma unroll
-        for (int i = 0; i < kTM; ++i) smul[h][i] = to_f32(cur.a[i], ASF == SF_UE8M0) * sb;
-      }
-    }
-    i32x8 af[kTM];
-#pragma unroll
-    for (int i = 0; i < kTM; ++i) af[i] = lds_frag(ta, wm * 16 * kTM + 16 * i + (lane & 15), lane);
-#pragma unroll
-    for (int j = 0; j < kTN; ++j) {
-      const bool hi = L::SPLIT && j >= jsplit;   // weight block wblk + 1; uniform over the wave
-      const i32x8 bf = lds_frag(tb, wn * 16 * kTN + 16 * j + (lane & 15), lane);
-#pragma unroll
-      for (int i = 0; i < kTM; ++i) {
-        if constexpr (kHwScale) {
-          const int sbj = (int)(hi ? cur.b[kNB - 1] : cur.b[0]);
-          acc[j][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-              bf, af[i], acc[j][i], 0, 0, 0, sbj, 0, (int)cur.a[i]);
-        } else {
-          const float sm = hi ? smul[kNB - 1][i] : smul[0][i];
-          const f32x4 t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-              bf, af[i], f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 127, 0, 127);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[j][i][r] = __builtin_fmaf(t[r], sm, acc[j][i][r]);
-        }
-      }
-    }
-    if constexpr (kHwScale) {
-      // The products are issued before the ring's wait.  (With fp32-promoted
-      // scales the compiler keeps most of them there by itself, and pinning
-      // serialises each product with its promotion: slower.)
-#pragma unroll
-      for (int j = 0; j < kTN; ++j)
-#pragma unroll
-        for (int i = 0; i < kTM; ++i) pin(acc[j][i]);
-    }
-    cur = nxt;
-    // The next k-block's tiles and scales have landed (each wave waits for
-    // its own copies) and every wave is done reading this k-block's slots
-    // before the next iteration refills them.
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(L::COPY_A));
-    ring_barrier();
-    slot_a = slot_a + 2 < kSlots ? slot_a + 2 : slot_a + 2 - kSlots;
-  }
-  __builtin_amdgcn_s_waitcnt(kVmcnt0);   // no copy into LDS outlives the workgroup
-
-  const rsrc_t rc = make_rsrc(g.c + (int64_t)m0 * g.N, (uint32_t)mrows * (uint32_t)g.N * 2u);
-#pragma unroll
-  for (int j = 0; j < kTN; ++j) {
-    const int ncol = wcol + 16 * j;
-    if (ncol >= g.N) continue;   // uniform over the wave
-#pragma unroll
-    for (int i = 0; i < kTM; ++i) {
-      const uint32_t row = (uint32_t)(wm * 16 * kTM + 16 * i + (lane & 15));
-      u32x2 v;
-      v[0] = pack_bf16x2(acc[j][i][0], acc[j][i][1]);
-      v[1] = pack_bf16x2(acc[j][i][2], acc[j][i][3]);
-      const uint32_t off = (row * (uint32_t)g.N + (uint32_t)(ncol + 4 * (lane >> 4))) * 2u;
-      __builtin_amdgcn_raw_buffer_store_b64(v, rc, off, 0, 0);
-    }
-  }
-}
 
 // ring_barrier() fenced for the scheduler as well: nothing moves across it,
 // so the products of a product interval cannot be hoisted into the read
@@ -384,18 +169,19 @@ __device__ __forceinline__ void pp_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Ping-pong pipeline (every scale format at 256-wide tiles).  The 8 waves form
-// two groups of 4: group 0 (waves 0-3) owns the tile's columns 0-127, group
-// 1 (waves 4-7) columns 128-255, and each SIMD runs one wave of each.  Every
+// The GEMM kernel: the ping-pong pipeline.  The 8 waves form two groups of
+// 4: group 0 (waves 0-3) owns the tile's columns 0 .. BN / 2 - 1, group 1
+// (waves 4-7) the other half, and each SIMD runs one wave of each.  Every
 // k-block spans two barrier intervals, and group 1 runs half a k-block
 // behind group 0, so in each interval one group reads its operand fragments
 // from LDS (and issues copies) while the other runs its 32 products from
 // registers:
 //   interval 2k + 1: group 0 reads k-block k's fragments  | group 1 multiplies k - 1
 //   interval 2k + 2: group 0 multiplies k                  | group 1 reads k
-// A wave holds a whole k-block's fragments (4 activation and 8 weight 16 x
-// 128-byte operands) between its read and product intervals.  The ring of
-// five 32 KB slots is the one above (A(k) in slot 2k % 5, B(k) in 2k + 1 % 5):
+// A wave holds a whole k-block's fragments (4 activation and BN / 32 weight
+// 16 x 128-byte operands) between its read and product intervals.  Five 32 KB
+// LDS slots form a ring over the tile sequence A(0), B(0), A(1), B(1), ...
+// (A(k) in slot 2k % 5, B(k) in 2k + 1 % 5):
 // group 0 copies B(k + 1) while reading k, group 1 copies A(k + 2) while
 // reading k, and each waits for its own copies before the barrier that ends
 // its next product interval (B) or read interval (A), so every copy has one
@@ -405,13 +191,15 @@ __device__ __forceinline__ void pp_barrier() {
 // multiplies once, and group 0 waits at the barriers.
 template <int ASF, int BSF, class L>
 __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_pp_kernel(const GArgs g) {
-  static_assert(L::BN == 256 && L::WAVES_M == 4 && L::WAVES_N == 2 && !L::SPLIT,
-                "two groups of four 64 x 128 waves");
+  static_assert(L::WAVES_M == 4 && L::WAVES_N == 2, "two groups of four 64 x BN / 2 waves");
   constexpr bool kHwScale = ASF == SF_UE8M0 && BSF == SF_UE8M0;
   constexpr int kTM = L::TM, kTN = L::TN;
-  constexpr int kCopy = kATileBytes / 1024 / 4;   // 1 KB copies per wave: a group copies a tile
-  static_assert(L::B_TILE_BYTES == kATileBytes, "both operand tiles fill one slot");
-  constexpr int kScaleLoads = kTM + 1;             // memory instructions of load_scales
+  constexpr int kNB = L::SPLIT ? 2 : 1;            // weight blocks a wave's columns touch
+  // 1 KB copies per wave: group 1 copies the activation tile, group 0 the weight tile.
+  constexpr int kCopyA = kATileBytes / 1024 / 4, kCopyB = L::B_TILE_BYTES / 1024 / 4;
+  static_assert(kCopyA * 4096 == kATileBytes && kCopyB * 4096 == L::B_TILE_BYTES,
+                "four waves copy each tile");
+  constexpr int kScaleLoads = kTM + kNB;           // memory instructions of load_scales
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kSlots * kSlotBytes];
 
   const int lane = threadIdx.x & 63;
@@ -428,36 +216,56 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_pp_kernel(const GArgs
   const rsrc_t ras = make_rsrc(g.as, g.as_bytes);
   const rsrc_t rbs = make_rsrc(g.bs, g.bs_bytes);
 
-  // Copies as in fagq_gemm_kernel, but a wave issues kCopy instructions of
-  // one whole tile: instruction u of wave wm fills LDS rows 8 (wm kCopy + u) .. +8.
+  // Copy geometry: the four waves of a group copy one whole tile; copy
+  // instruction u of wave wm is instruction i = wm C + u of the tile (C =
+  // kCopyA or kCopyB) and fills LDS rows 8 i .. +8.  The lane's row within
+  // them is lane / 8, its position lane % 8, and it fetches the logical chunk
+  // stored there; the swizzle of row 8 i + lane / 8 depends on lane / 8
+  // only, so one lane offset serves every instruction.  The whole offset goes
+  // in the VGPR offset and the scalar offset is zero: the hardware
+  // range-checks only the VGPR offset (plus the immediate), so this is what
+  // turns rows past M or N into zero reads.  Offsets are computed in uint32:
+  // the launch checks that every one fits.
   const int crow = lane >> 3;
   const uint32_t cvoff = (uint32_t)crow * (uint32_t)g.K + (uint32_t)swz(lane & 7, crow) * 16u;
-  auto issue_tile = [&](const rsrc_t& rs, int kb, int slot) {
-    uint8_t* dst = lds + slot * kSlotBytes;
+  auto copy_one = [&](const rsrc_t& rs, int kb, uint8_t* dst, int inst) {
+    const uint32_t off = cvoff + (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)((uint32_t)inst * 8u * (uint32_t)g.K + (uint32_t)kb * (uint32_t)kBK));
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(dst + inst * 1024), 16, off, 0, 0, 0);
+  };
+  auto issue_a = [&](int kb, int slot) {
 #pragma unroll
-    for (int u = 0; u < kCopy; ++u) {
-      const int inst = wm * kCopy + u;
-      const uint32_t off = cvoff + (uint32_t)__builtin_amdgcn_readfirstlane(
-          (int)((uint32_t)inst * 8u * (uint32_t)g.K + (uint32_t)kb * (uint32_t)kBK));
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(dst + inst * 1024), 16, off, 0, 0, 0);
-    }
+    for (int u = 0; u < kCopyA; ++u) copy_one(ra, kb, lds + slot * kSlotBytes, wm * kCopyA + u);
+  };
+  auto issue_b = [&](int kb, int slot) {
+#pragma unroll
+    for (int u = 0; u < kCopyB; ++u) copy_one(rb, kb, lds + slot * kSlotBytes, wm * kCopyB + u);
   };
 
-  // Scale bits of the lane's rows and of the wave's weight block, as in
-  // fagq_gemm_kernel.
+  // Scale bits of the lane's rows (m0 + 16 (TM wm + i) + lane % 16) and of
+  // the 128-column weight blocks of the wave's columns (block wblk for tiles
+  // j < jsplit, wblk + 1 for the rest), as loaded bits.  Offsets as for the
+  // copies: all in the range-checked VGPR offset, so scale reads for rows
+  // past M or weight blocks past N read zeros (those rows and columns are
+  // never stored).
   const int arow = m0 + wm * 16 * kTM + (lane & 15);
-  const int wblk = (n0 + wn * 16 * kTN) >> 7;
+  const int wcol = n0 + wn * 16 * kTN;
+  const int wblk = wcol >> 7;
+  const int jsplit = L::SPLIT ? (((wblk + 1) << 7) - wcol) >> 4 : kTN;
   constexpr uint32_t asb = ASF == SF_F32 ? 4u : 1u, bsb = BSF == SF_F32 ? 4u : 1u;
   const uint32_t a_voff = (uint32_t)arow * (uint32_t)g.as_mstride * asb;
   struct Scales {
-    uint32_t a[kTM], b;
+    uint32_t a[kTM], b[kNB];
   };
   auto load_scales = [&](int kb) {
     Scales sc;
-    const uint32_t boff = (uint32_t)__builtin_amdgcn_readfirstlane(
-        (int)(((uint32_t)wblk * (uint32_t)g.kblocks + (uint32_t)kb) * bsb));
-    sc.b = BSF == SF_F32 ? __builtin_amdgcn_raw_buffer_load_b32(rbs, boff, 0, 0)
-                         : (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rbs, boff, 0, 0);
+#pragma unroll
+    for (int h = 0; h < kNB; ++h) {
+      const uint32_t boff = (uint32_t)__builtin_amdgcn_readfirstlane(
+          (int)(((uint32_t)(wblk + h) * (uint32_t)g.kblocks + (uint32_t)kb) * bsb));
+      sc.b[h] = BSF == SF_F32 ? __builtin_amdgcn_raw_buffer_load_b32(rbs, boff, 0, 0)
+                              : (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rbs, boff, 0, 0);
+    }
 #pragma unroll
     for (int i = 0; i < kTM; ++i) {
       const uint32_t e = (uint32_t)kb * (uint32_t)g.as_kstride +
@@ -486,32 +294,40 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_pp_kernel(const GArgs
   };
   // One k-block's products.  Both UE8M0: the matrix core applies the scales.
   // fp32 (or mixed): each product goes to a temporary and is added as
-  // fmaf(t, sa * sb, acc), as in fagq_gemm_kernel, and the schedule
+  // fmaf(t, sa * sb, acc), and the schedule
   // alternates one MFMA with four FMAs, so that a product's promotion runs
   // while the next MFMA executes.
   auto products = [&](const Scales& s) {
     if constexpr (kHwScale) {
 #pragma unroll
-      for (int j = 0; j < kTN; ++j)
+      for (int j = 0; j < kTN; ++j) {
+        const int sbj = (int)(L::SPLIT && j >= jsplit ? s.b[kNB - 1] : s.b[0]);
 #pragma unroll
         for (int i = 0; i < kTM; ++i)
           acc[j][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-              bf[j], af[i], acc[j][i], 0, 0, 0, (int)s.b, 0, (int)s.a[i]);
+              bf[j], af[i], acc[j][i], 0, 0, 0, sbj, 0, (int)s.a[i]);
+      }
     } else {
-      const float sb = BSF == SF_UE8M0 ? e8m0_to_f32(s.b) : __uint_as_float(s.b);
-      float sm[kTM];
+      float sm[kNB][kTM];
 #pragma unroll
-      for (int i = 0; i < kTM; ++i)
-        sm[i] = (ASF == SF_UE8M0 ? e8m0_to_f32(s.a[i]) : __uint_as_float(s.a[i])) * sb;
+      for (int h = 0; h < kNB; ++h) {
+        const float sb = BSF == SF_UE8M0 ? e8m0_to_f32(s.b[h]) : __uint_as_float(s.b[h]);
 #pragma unroll
-      for (int j = 0; j < kTN; ++j)
+        for (int i = 0; i < kTM; ++i)
+          sm[h][i] = (ASF == SF_UE8M0 ? e8m0_to_f32(s.a[i]) : __uint_as_float(s.a[i])) * sb;
+      }
+#pragma unroll
+      for (int j = 0; j < kTN; ++j) {
+        const bool hi = L::SPLIT && j >= jsplit;   // weight block wblk + 1; uniform over the wave
 #pragma unroll
         for (int i = 0; i < kTM; ++i) {
+          const float smv = hi ? sm[kNB - 1][i] : sm[0][i];
           const f32x4 t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
               bf[j], af[i], f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 127, 0, 127);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[j][i][r] = __builtin_fmaf(t[r], sm[i], acc[j][i][r]);
+          for (int r = 0; r < 4; ++r) acc[j][i][r] = __builtin_fmaf(t[r], smv, acc[j][i][r]);
         }
+      }
 #pragma unroll
       for (int n = 0; n < kTN * kTM; ++n) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
@@ -536,7 +352,7 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_pp_kernel(const GArgs
   // barrier 2k + 3 starts group 1's products of k and group 0's reads of k + 1.
   if (g0) {
     // Prologue: A(0); with group 1's B(0) it lands before the first barrier.
-    issue_tile(ra, 0, 0);
+    issue_a(0, 0);
     Scales cur = load_scales(0);
     __builtin_amdgcn_s_waitcnt(kVmcnt0);
     pp_barrier();
@@ -546,7 +362,7 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_pp_kernel(const GArgs
       read_frags(k);
       const Scales nxt = load_scales(k + 1 < last ? k + 1 : last);
       issue_order_fence();
-      issue_tile(rb, k + 1 < last ? k + 1 : last, (2 * k + 3) % kSlots);
+      issue_b(k + 1 < last ? k + 1 : last, (2 * k + 3) % kSlots);
       pp_barrier();
       // Multiplies k while group 1 reads it.
       products(cur);
@@ -557,10 +373,10 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_pp_kernel(const GArgs
     pp_barrier();                           // while group 1 multiplies the last k-block
   } else {
     // Prologue: B(0), then A(1) left in flight.
-    issue_tile(rb, 0, 1);
+    issue_b(0, 1);
     issue_order_fence();
-    issue_tile(ra, 1 < last ? 1 : last, 2);
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kCopy));
+    issue_a(1 < last ? 1 : last, 2);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kCopyA));
     pp_barrier();
     pp_barrier();                           // group 0 reads k-block 0
     Scales cur;
@@ -572,8 +388,8 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_pp_kernel(const GArgs
       issue_order_fence();
       read_frags(k);
       issue_order_fence();
-      issue_tile(ra, k + 2 < last ? k + 2 : last, (2 * k + 4) % kSlots);
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kScaleLoads + kCopy));
+      issue_a(k + 2 < last ? k + 2 : last, (2 * k + 4) % kSlots);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kScaleLoads + kCopyA));
       pp_barrier();
       // Multiplies k while group 0 reads k + 1.
       products(cur);
@@ -583,7 +399,6 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_pp_kernel(const GArgs
   __builtin_amdgcn_s_waitcnt(kVmcnt0);
 
   const rsrc_t rc = make_rsrc(g.c + (int64_t)m0 * g.N, (uint32_t)mrows * (uint32_t)g.N * 2u);
-  const int wcol = n0 + wn * 16 * kTN;
 #pragma unroll
   for (int j = 0; j < kTN; ++j) {
     const int ncol = wcol + 16 * j;
@@ -641,17 +456,10 @@ int validate(const void* a_q, const void* a_scale, const void* b_q, const void* 
 template <class L>
 const void* kernel_for_layout(int asf, int bsf) {
   const bool au = asf == FAGQ_SCALE_UE8M0, bu = bsf == FAGQ_SCALE_UE8M0;
-  if constexpr (L::BN == 256) {
-    if (au && bu) return reinterpret_cast<const void*>(&fagq_gemm_pp_kernel<SF_UE8M0, SF_UE8M0, L>);
-    if (au) return reinterpret_cast<const void*>(&fagq_gemm_pp_kernel<SF_UE8M0, SF_F32, L>);
-    if (bu) return reinterpret_cast<const void*>(&fagq_gemm_pp_kernel<SF_F32, SF_UE8M0, L>);
-    return reinterpret_cast<const void*>(&fagq_gemm_pp_kernel<SF_F32, SF_F32, L>);
-  } else {
-    if (au && bu) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_UE8M0, SF_UE8M0, L>);
-    if (au) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_UE8M0, SF_F32, L>);
-    if (bu) return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_F32, SF_UE8M0, L>);
-    return reinterpret_cast<const void*>(&fagq_gemm_kernel<SF_F32, SF_F32, L>);
-  }
+  if (au && bu) return reinterpret_cast<const void*>(&fagq_gemm_pp_kernel<SF_UE8M0, SF_UE8M0, L>);
+  if (au) return reinterpret_cast<const void*>(&fagq_gemm_pp_kernel<SF_UE8M0, SF_F32, L>);
+  if (bu) return reinterpret_cast<const void*>(&fagq_gemm_pp_kernel<SF_F32, SF_UE8M0, L>);
+  return reinterpret_cast<const void*>(&fagq_gemm_pp_kernel<SF_F32, SF_F32, L>);
 }
 static_assert(Layout256::THREADS == Layout192::THREADS, "one workgroup size");
 
