@@ -67,7 +67,8 @@ FORMATS = [("f32", "f32", True), ("f32", "f32", False), ("ue8m0", "ue8m0", True)
 
 
 @pytest.mark.parametrize("afmt,bfmt,col", FORMATS)
-@pytest.mark.parametrize("M,N,K", [(256, 256, 128), (300, 272, 1024), (17, 2112, 7168)])
+@pytest.mark.parametrize("M,N,K", [(256, 256, 128), (64, 256, 384), (130, 2112, 640),
+                                   (300, 272, 1024), (17, 2112, 7168)])
 def test_gemm_formats(pkg, gpu, M, N, K, afmt, bfmt, col):
     note(f"gemm M={M} N={N} K={K} a={afmt} b={bfmt} col={col}")
     a_q, a_s, b_q, b_s = make(M, N, K, afmt, bfmt, col, seed=M + N + K)
