@@ -353,21 +353,20 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_pp_kernel(const GArgs
   if (g0) {
     // Prologue: A(0); with group 1's B(0) it lands before the first barrier.
     issue_a(0, 0);
-    Scales cur = load_scales(0);
     __builtin_amdgcn_s_waitcnt(kVmcnt0);
     pp_barrier();
 #pragma clang loop unroll(disable)
     for (int k = 0; k < nk; ++k) {
       // Reads k-block k and copies B(k + 1) into the slot A(k - 1) left.
+      const Scales cur = load_scales(k);
+      issue_order_fence();
       read_frags(k);
-      const Scales nxt = load_scales(k + 1 < last ? k + 1 : last);
       issue_order_fence();
       issue_b(k + 1 < last ? k + 1 : last, (2 * k + 3) % kSlots);
       pp_barrier();
       // Multiplies k while group 1 reads it.
       products(cur);
-      cur = nxt;
-      __builtin_amdgcn_s_waitcnt(kVmcnt0);   // B(k + 1) and k + 1's scales have landed
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);   // B(k + 1) has landed
       pp_barrier();
     }
     pp_barrier();                           // while group 1 multiplies the last k-block
