@@ -200,6 +200,10 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_pp_kernel(const GArgs
   static_assert(kCopyA * 4096 == kATileBytes && kCopyB * 4096 == L::B_TILE_BYTES,
                 "four waves copy each tile");
   constexpr int kScaleLoads = kTM + kNB;           // memory instructions of load_scales
+  // At BN = 192 the reading group runs at raised wave priority during its
+  // reads and copies (q_a + kv_a 256.7 -> 241.7 us, same box); at BN = 256 that
+  // measured 0.8-1 % slower.
+  constexpr bool kReadPrio = L::BN != 256;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kSlots * kSlotBytes];
 
   const int lane = threadIdx.x & 63;
@@ -358,11 +362,13 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_pp_kernel(const GArgs
 #pragma clang loop unroll(disable)
     for (int k = 0; k < nk; ++k) {
       // Reads k-block k and copies B(k + 1) into the slot A(k - 1) left.
+      if constexpr (kReadPrio) __builtin_amdgcn_s_setprio(1);
       const Scales cur = load_scales(k);
       issue_order_fence();
       read_frags(k);
       issue_order_fence();
       issue_b(k + 1 < last ? k + 1 : last, (2 * k + 3) % kSlots);
+      if constexpr (kReadPrio) __builtin_amdgcn_s_setprio(0);
       pp_barrier();
       // Multiplies k while group 1 reads it.
       products(cur);
@@ -383,11 +389,13 @@ __global__ void __launch_bounds__(L::THREADS, 1) fagq_gemm_pp_kernel(const GArgs
     for (int k = 0; k < nk; ++k) {
       // Reads k-block k (group 0 multiplies it) and copies A(k + 2) into
       // the slot B(k - 1) left; A(k + 1) must land before the barrier.
+      if constexpr (kReadPrio) __builtin_amdgcn_s_setprio(1);
       cur = load_scales(k);                   // first: the products wait for them at the barrier
       issue_order_fence();
       read_frags(k);
       issue_order_fence();
       issue_a(k + 2 < last ? k + 2 : last, (2 * k + 4) % kSlots);
+      if constexpr (kReadPrio) __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(kScaleLoads + kCopyA));
       pp_barrier();
       // Multiplies k while group 0 reads k + 1.
